@@ -1,0 +1,843 @@
+// Host side of the HIP backend: the hy_device_ops vtable the reference host calls
+// (src/device.h:70-80), built MI355X-first: weights resident in HBM in kernel-friendly layouts,
+// one HIP stream per context, single-token forwards replayed from a captured hipGraph, one
+// host synchronisation per fused_forward, and a device-resident greedy loop.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unistd.h>
+#include <vector>
+
+#include "../../include/hymt2_hip.h"
+#include "hy_kernels.h"
+
+using namespace hy;
+
+// ----------------------------------------------------------------------------------- ABI
+
+static_assert(sizeof(hymt2_weight) == 64, "weight_t size");
+static_assert(offsetof(hymt2_weight, row_bytes) == 24 && offsetof(hymt2_weight, pk) == 32 &&
+                  offsetof(hymt2_weight, ps) == 40 && offsetof(hymt2_weight, pshift) == 48 &&
+                  offsetof(hymt2_weight, gpu) == 56,
+              "weight_t layout");
+static_assert(sizeof(hymt2_q8k_block) == 576 && sizeof(HyQ8K) == 576, "q8k_block size");
+static_assert(sizeof(hymt2_fused_layer) == 88, "hy_fused_layer size");
+static_assert(sizeof(hymt2_fused_args) == 112 && offsetof(hymt2_fused_args, eps) == 48 &&
+                  offsetof(hymt2_fused_args, layers) == 56 && offsetof(hymt2_fused_args, logits) == 104,
+              "hy_fused_args layout");
+static_assert(sizeof(hymt2_device_ops) == 64, "hy_device_ops size");
+
+// The reference host's wrapper (src/device.c:25-35). Weak: absent when this library is loaded
+// on its own, in which case hy_cuda_create reports that the host is missing.
+extern "C" hy_device* hy_device_wrap(int kind, const char* name, void* impl, const hymt2_device_ops* ops,
+                                     bool software) __attribute__((weak));
+static constexpr int kDevKindCuda = 2;  // HY_DEV_CUDA, src/device.h:15-21
+
+// ggml type codes, src/internal.h:46
+enum { GT_F32 = 0, GT_F16 = 1, GT_Q4_K = 12, GT_Q6_K = 14, GT_Q2_0C = 40, GT_STQ1_0 = 43 };
+
+struct Ctx;
+
+struct DW {  // hy_dweight
+    Ctx* c = nullptr;
+    int gtype = 0;
+    MvWeight mw{};
+    void* mem = nullptr;
+    size_t bytes = 0;
+};
+
+struct Fused {
+    int n_layer = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, hdim = 0, qdim = 0, kvdim = 0, ctx = 0,
+        rope_half = 0;
+    float eps = 0.f;
+    char* in_dev = nullptr;   // [MAX_BATCH * hidden floats][pos int]
+    char* in_host = nullptr;  // pinned staging of the same layout
+    float* d_h = nullptr;
+    int* d_pos = nullptr;
+    size_t in_bytes = 0;
+    float *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr, *g = nullptr, *u = nullptr, *logits = nullptr;
+    HyQ8K *act_h = nullptr, *act_q = nullptr, *act_f = nullptr;
+    float *rope_c = nullptr, *rope_s = nullptr, *out_norm = nullptr, *norms = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+    size_t logits_cap = 0;
+    unsigned long long* key = nullptr;
+    int* ids = nullptr;
+    int ids_cap = 0;
+    hipGraphExec_t g_fwd = nullptr, g_step = nullptr;
+    std::vector<const void*> sig_fwd, sig_step;
+    float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
+        const size_t per = 2 * (size_t)hidden + 2 * (size_t)hdim;
+        float* base = norms + per * li;
+        return which == 0 ? base : which == 1 ? base + hidden : which == 2 ? base + 2 * hidden : base + 2 * hidden + hdim;
+    }
+};
+
+struct Ctx {
+    int dev = 0;
+    hipStream_t s = nullptr;
+    bool broken = false;
+    std::string err;
+    void* act = nullptr;
+    size_t act_cap = 0;
+    float* out = nullptr;
+    size_t out_cap = 0;
+    Fused* f = nullptr;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+};
+
+static void set_err(Ctx* c, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+    if (getenv("HYMT2_VERBOSE")) fprintf(stderr, "[hymt2-hip] %s\n", buf);
+}
+
+#define HIPCHK(c, x)                                                                  \
+    do {                                                                              \
+        hipError_t e_ = (x);                                                          \
+        if (e_ != hipSuccess) {                                                       \
+            set_err((c), "%s failed: %s (%s:%d)", #x, hipGetErrorString(e_), __FILE__, __LINE__); \
+            (c)->broken = true;                                                       \
+            return false;                                                             \
+        }                                                                             \
+    } while (0)
+
+template <typename T>
+static bool dalloc(Ctx* c, T** p, size_t bytes) {
+    void* q = nullptr;
+    hipError_t e = hipMalloc(&q, bytes ? bytes : 64);
+    if (e != hipSuccess) {
+        set_err(c, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+        return false;
+    }
+    *p = static_cast<T*>(q);
+    return true;
+}
+
+// ----------------------------------------------------------------------------------- upload
+
+// Q6_K blocks (210 B, src/internal.h:23: ql[128] qh[64] scales[16] d) -> four aligned planes of
+// the same bytes, so every lane issues 16-byte loads.
+static void q6k_to_planes(const uint8_t* src, size_t nblk, uint8_t* ql, uint8_t* qh, int8_t* sc, uint16_t* d) {
+    for (size_t i = 0; i < nblk; i++) {
+        const uint8_t* b = src + i * 210;
+        memcpy(ql + i * 128, b, 128);
+        memcpy(qh + i * 64, b + 128, 64);
+        memcpy(sc + i * 16, b + 192, 16);
+        memcpy(d + i, b + 208, 2);
+    }
+}
+
+static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !w || w->k <= 0 || w->n <= 0) return nullptr;
+    DW* d = new DW();
+    d->c = c;
+    d->gtype = w->type;
+    MvWeight& m = d->mw;
+    m.n = w->n;
+    m.k = w->k;
+    const size_t n = (size_t)w->n;
+    std::vector<uint8_t> host;
+    if ((w->type == GT_STQ1_0 || w->type == GT_Q2_0C) && w->pk && w->ps && w->k % 256 == 0) {
+        m.kind = KIND_PANEL;
+        m.nb = w->k / 256;
+        m.pshift = w->pshift;
+        m.poff = w->poff;
+        const size_t cb = n * m.nb * 64, sb = n * m.nb * 4;
+        d->bytes = cb + sb;
+        host.resize(d->bytes);
+        memcpy(host.data(), w->pk, cb);
+        memcpy(host.data() + cb, w->ps, sb);
+    } else if (w->type == GT_Q4_K && w->k % 256 == 0) {
+        m.kind = KIND_Q4K;
+        m.nb = w->k / 256;
+        d->bytes = n * m.nb * 144;
+        host.assign(w->data, w->data + d->bytes);
+    } else if (w->type == GT_Q6_K && w->k % 256 == 0) {
+        m.kind = KIND_Q6K;
+        m.nb = w->k / 256;
+        const size_t nblk = n * m.nb;
+        d->bytes = nblk * 210;
+        host.resize(d->bytes);
+        q6k_to_planes(w->data, nblk, host.data(), host.data() + nblk * 128,
+                      reinterpret_cast<int8_t*>(host.data() + nblk * 192),
+                      reinterpret_cast<uint16_t*>(host.data() + nblk * 208));
+    } else if (w->type == GT_F16 && w->k % 32 == 0) {
+        m.kind = KIND_F16;
+        m.nb = w->k / 256;
+        d->bytes = n * w->k * 2;
+        host.assign(w->data, w->data + d->bytes);
+    } else if (w->type == GT_F32 && w->k % 16 == 0) {
+        m.kind = KIND_F32;
+        m.nb = w->k / 256;
+        d->bytes = n * w->k * 4;
+        host.assign(w->data, w->data + d->bytes);
+    } else {
+        set_err(c, "upload: unsupported weight type %d (k=%d, panel=%d)", w->type, w->k, w->pk != nullptr);
+        delete d;
+        return nullptr;
+    }
+    if (!dalloc(c, &d->mem, d->bytes) ||
+        hipMemcpy(d->mem, host.data(), d->bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        if (d->mem) (void)hipFree(d->mem);
+        set_err(c, "upload: device copy of %zu bytes failed", d->bytes);
+        delete d;
+        return nullptr;
+    }
+    uint8_t* base = static_cast<uint8_t*>(d->mem);
+    m.w = base;
+    if (m.kind == KIND_PANEL) {
+        m.ps = reinterpret_cast<const float*>(base + n * m.nb * 64);
+    } else if (m.kind == KIND_Q6K) {
+        const size_t nblk = n * m.nb;
+        m.w2 = base + nblk * 128;
+        m.sc = reinterpret_cast<const int8_t*>(base + nblk * 192);
+        m.dh = reinterpret_cast<const uint16_t*>(base + nblk * 208);
+    }
+    return reinterpret_cast<hy_dweight*>(d);
+}
+
+static void hip_release(hy_dweight* w) {
+    DW* d = reinterpret_cast<DW*>(w);
+    if (!d) return;
+    if (d->mem) (void)hipFree(d->mem);
+    delete d;
+}
+
+static bool hip_is_sw(const void*) { return false; }
+static float* hip_weight_out(hy_dweight*) { return nullptr; }
+
+// ----------------------------------------------------------------------------------- matvec
+
+static bool quant_kind(int kind) { return kind == KIND_PANEL || kind == KIND_Q4K || kind == KIND_Q6K; }
+
+struct JobSpec {
+    const DW* w;
+    float* out;
+    int ldo;
+    int epi;
+};
+
+// Tile the jobs over workgroups: the smallest segments-per-thread whose grid stays within
+// about four resident workgroups per CU.
+static bool build_launch(const JobSpec* js, int njobs, bool pair, int nt, MvLaunch& L, int& grid) {
+    memset(&L, 0, sizeof L);
+    L.njobs = njobs;
+    L.pair = pair ? 1 : 0;
+    L.nt = nt;
+    const int K = js[0].w->mw.k;
+    for (int segs : {1, 2, 4}) {
+        int wgs = 0;
+        bool ok = true;
+        for (int j = 0; j < njobs; j++) {
+            const MvWeight& m = js[j].w->mw;
+            const int spr = m.nb * mv_segments_per_block(m.kind) * (pair ? 2 : 1);
+            const int rpw = (256 * segs) / spr;
+            if (rpw < 1) {
+                ok = false;
+                break;
+            }
+            L.job[j].rows_per_wg = rpw;
+            L.job[j].wg_begin = wgs;
+            if (!pair || j == 0) wgs += (m.n + rpw - 1) / rpw;
+        }
+        if (!ok) continue;
+        L.segs = segs;
+        grid = wgs;
+        if (wgs <= 1024 || segs == 4) break;
+    }
+    if (!L.segs) return false;
+    for (int j = 0; j < njobs; j++) {
+        L.job[j].W = js[j].w->mw;
+        L.job[j].out = js[j].out;
+        L.job[j].ldo = js[j].ldo;
+        L.job[j].epi = js[j].epi;
+        if (js[j].w->mw.k != K || !quant_kind(js[j].w->mw.kind)) return false;
+    }
+    if (pair) {
+        if (njobs != 2 || js[0].w->mw.kind != js[1].w->mw.kind || js[0].w->mw.n != js[1].w->mw.n) return false;
+        L.job[1].rows_per_wg = L.job[0].rows_per_wg;
+        L.job[1].wg_begin = 0;
+    }
+    L.K = K;
+    return true;
+}
+
+static bool run_matvec(Ctx* c, const JobSpec* js, int njobs, bool pair, int nt, int pro, const HyQ8K* act,
+                       const float* x, const float* norm_w, float eps) {
+    MvLaunch L;
+    int grid = 0;
+    if (!build_launch(js, njobs, pair, nt, L, grid)) {
+        set_err(c, "matvec: unsupported job combination");
+        return false;
+    }
+    L.act = act;
+    L.x = x;
+    L.norm_w = norm_w;
+    L.eps = eps;
+    HIPCHK(c, launch_matvec(L, pro, grid, c->s));
+    return true;
+}
+
+static bool ensure_scratch(Ctx* c, size_t act_bytes, size_t out_bytes) {
+    if (act_bytes > c->act_cap) {
+        if (c->act) (void)hipFree(c->act);
+        c->act = nullptr;
+        c->act_cap = 0;
+        if (!dalloc(c, &c->act, act_bytes)) return false;
+        c->act_cap = act_bytes;
+    }
+    if (out_bytes > c->out_cap) {
+        if (c->out) (void)hipFree(c->out);
+        c->out = nullptr;
+        c->out_cap = 0;
+        if (!dalloc(c, &c->out, out_bytes)) return false;
+        c->out_cap = out_bytes;
+    }
+    return true;
+}
+
+// Per-op path (src/device.h:37-39; reference cu_matmul src/cuda.c:258-280): the weights of one
+// group share the host's Q8_K activations; one synchronisation for the group. F16/F32 weights
+// are rejected: the reference multiplies them with fp32 activations (src/kernels.c:1279-1300),
+// which this entry point does not receive.
+static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, int cnt, const hymt2_q8k_block* xq,
+                       int nt) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || cnt < 1 || nt < 1 || nt > HY_MAX_BATCH || !xq) return false;
+    const DW* w0 = reinterpret_cast<const DW*>(ws[0]);
+    const int nb = w0->mw.nb;
+    size_t out_total = 0;
+    for (int i = 0; i < cnt; i++) {
+        const DW* w = reinterpret_cast<const DW*>(ws[i]);
+        if (!w || w->mw.nb != nb || w->mw.k != w0->mw.k || !quant_kind(w->mw.kind)) {
+            set_err(c, "matmul: weight %d unsupported for the per-op path", i);
+            return false;
+        }
+        out_total += (size_t)w->mw.n * nt;
+    }
+    const size_t abytes = (size_t)nt * nb * sizeof(HyQ8K);
+    if (!ensure_scratch(c, abytes, out_total * sizeof(float))) return false;
+    HIPCHK(c, hipMemcpyAsync(c->act, xq, abytes, hipMemcpyHostToDevice, c->s));
+    size_t off = 0;
+    for (int i = 0; i < cnt; i++) {
+        const DW* w = reinterpret_cast<const DW*>(ws[i]);
+        JobSpec j{w, c->out + off, w->mw.n, EPI_STORE};
+        if (!run_matvec(c, &j, 1, false, nt, PRO_NONE, static_cast<const HyQ8K*>(c->act), nullptr, nullptr, 0.f)) {
+            c->broken = true;
+            return false;
+        }
+        off += (size_t)w->mw.n * nt;
+    }
+    off = 0;
+    for (int i = 0; i < cnt; i++) {
+        const DW* w = reinterpret_cast<const DW*>(ws[i]);
+        const size_t nbytes = (size_t)w->mw.n * nt * sizeof(float);
+        HIPCHK(c, hipMemcpyAsync(outs[i], c->out + off, nbytes, hipMemcpyDeviceToHost, c->s));
+        off += (size_t)w->mw.n * nt;
+    }
+    HIPCHK(c, hipStreamSynchronize(c->s));
+    return true;
+}
+
+// ----------------------------------------------------------------------------------- fused
+
+static void free_graphs(Fused* f) {
+    if (f->g_fwd) (void)hipGraphExecDestroy(f->g_fwd);
+    if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
+    f->g_fwd = f->g_step = nullptr;
+    f->sig_fwd.clear();
+    f->sig_step.clear();
+}
+
+static void free_fused(Fused* f) {
+    if (!f) return;
+    free_graphs(f);
+    void* dev[] = {f->in_dev, f->q, f->k, f->v, f->ao, f->g, f->u, f->logits, f->act_h, f->act_q, f->act_f,
+                   f->rope_c, f->rope_s, f->out_norm, f->norms, f->kc, f->vc, f->key, f->ids};
+    for (void* p : dev)
+        if (p) (void)hipFree(p);
+    if (f->in_host) (void)hipHostFree(f->in_host);
+    delete f;
+}
+
+static bool same_shape(const Fused* f, const hymt2_fused_args* a) {
+    return f && f->n_layer == a->n_layer && f->hidden == a->hidden && f->ffn == a->ffn && f->heads == a->heads &&
+           f->kv_heads == a->kv_heads && f->hdim == a->hdim && f->qdim == a->qdim && f->kvdim == a->kvdim &&
+           f->ctx == a->ctx && f->rope_half == a->rope_half;
+}
+
+// Allocates KV cache and work buffers for the model shape and copies norms and RoPE tables
+// (reference cu_fused_prepare, src/cuda.c:282-337; idempotent for the same shape).
+static bool copy_params(Ctx* c, const hymt2_fused_args* a) {
+    Fused* f = c->f;
+    const size_t H = f->hidden;
+    const size_t rb = (size_t)a->ctx * a->rope_half * 4;
+    HIPCHK(c, hipMemcpy(f->rope_c, a->rope_cos, rb, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(f->rope_s, a->rope_sin, rb, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(f->out_norm, a->out_norm, H * 4, hipMemcpyHostToDevice));
+    for (int li = 0; li < a->n_layer; li++) {
+        const hymt2_fused_layer& L = a->layers[li];
+        HIPCHK(c, hipMemcpy(f->norm_ptr(li, 0), L.attn_norm, H * 4, hipMemcpyHostToDevice));
+        HIPCHK(c, hipMemcpy(f->norm_ptr(li, 1), L.ffn_norm, H * 4, hipMemcpyHostToDevice));
+        HIPCHK(c, hipMemcpy(f->norm_ptr(li, 2), L.q_norm, (size_t)a->hdim * 4, hipMemcpyHostToDevice));
+        HIPCHK(c, hipMemcpy(f->norm_ptr(li, 3), L.k_norm, (size_t)a->hdim * 4, hipMemcpyHostToDevice));
+    }
+    f->eps = a->eps;
+    return true;
+}
+
+static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !a || !a->layers) return false;
+    // Same shape: keep the buffers and the KV cache (prefix reuse), refresh the parameters.
+    if (same_shape(c->f, a)) return copy_params(c, a);
+    if (a->hidden % 256 || a->ffn % 256 || a->qdim % 256 || a->heads % a->kv_heads || a->qdim != a->heads * a->hdim ||
+        a->kvdim != a->kv_heads * a->hdim || (a->hdim != 64 && a->hdim != 128 && a->hdim != 256) ||
+        2 * a->rope_half > a->hdim || a->ctx < 1 || (size_t)(a->ctx + 256) * 4 > 160 * 1024) {
+        set_err(c, "fused_prepare: unsupported shape (hidden %d ffn %d qdim %d hdim %d ctx %d)", a->hidden, a->ffn,
+                a->qdim, a->hdim, a->ctx);
+        return false;
+    }
+    free_fused(c->f);
+    c->f = nullptr;
+    Fused* f = new Fused();
+    f->n_layer = a->n_layer;
+    f->hidden = a->hidden;
+    f->ffn = a->ffn;
+    f->heads = a->heads;
+    f->kv_heads = a->kv_heads;
+    f->hdim = a->hdim;
+    f->qdim = a->qdim;
+    f->kvdim = a->kvdim;
+    f->ctx = a->ctx;
+    f->rope_half = a->rope_half;
+    f->eps = a->eps;
+    const size_t B = HY_MAX_BATCH, H = a->hidden, F = a->ffn, Q = a->qdim, KV = a->kvdim;
+    f->in_bytes = B * H * 4 + 64;
+    bool ok = dalloc(c, &f->in_dev, f->in_bytes) && hipHostMalloc(&f->in_host, f->in_bytes, 0) == hipSuccess;
+    ok = ok && dalloc(c, &f->q, B * Q * 4) && dalloc(c, &f->k, B * KV * 4) && dalloc(c, &f->v, B * KV * 4) &&
+         dalloc(c, &f->ao, B * Q * 4) && dalloc(c, &f->g, B * F * 4) && dalloc(c, &f->u, B * F * 4) &&
+         dalloc(c, &f->act_h, B * (H / 256) * sizeof(HyQ8K)) && dalloc(c, &f->act_q, B * (Q / 256) * sizeof(HyQ8K)) &&
+         dalloc(c, &f->act_f, B * (F / 256) * sizeof(HyQ8K)) &&
+         dalloc(c, &f->rope_c, (size_t)a->ctx * a->rope_half * 4 + 4) &&
+         dalloc(c, &f->rope_s, (size_t)a->ctx * a->rope_half * 4 + 4) && dalloc(c, &f->out_norm, H * 4) &&
+         dalloc(c, &f->norms, (size_t)a->n_layer * (2 * H + 2 * a->hdim) * 4) &&
+         dalloc(c, &f->kc, (size_t)a->n_layer * a->ctx * KV * 2) &&
+         dalloc(c, &f->vc, (size_t)a->n_layer * a->ctx * KV * 2) && dalloc(c, &f->key, 64);
+    if (!ok) {
+        free_fused(f);
+        return false;
+    }
+    f->d_h = reinterpret_cast<float*>(f->in_dev);
+    f->d_pos = reinterpret_cast<int*>(f->in_dev + B * H * 4);
+    c->f = f;
+    if (!copy_params(c, a)) return false;
+    HIPCHK(c, hipMemset(f->kc, 0, (size_t)a->n_layer * a->ctx * KV * 2));
+    HIPCHK(c, hipMemset(f->vc, 0, (size_t)a->n_layer * a->ctx * KV * 2));
+    HIPCHK(c, hipMemset(f->key, 0, 64));
+    HIPCHK(c, hipMemset(f->in_dev, 0, f->in_bytes));
+    return true;
+}
+
+static bool ensure_logits(Ctx* c, Fused* f, int n) {
+    if ((size_t)n <= f->logits_cap) return true;
+    if (f->logits) (void)hipFree(f->logits);
+    f->logits = nullptr;
+    f->logits_cap = 0;
+    if (!dalloc(c, &f->logits, (size_t)n * 4)) return false;
+    f->logits_cap = n;
+    free_graphs(f);  // graphs hold the old pointer
+    return true;
+}
+
+static const DW* dw(hy_dweight* p) { return reinterpret_cast<const DW*>(p); }
+
+// Enqueues all layers of one forward of nt tokens (the order of src/model.c:822-886). nt == 1
+// uses the fused single-token kernels (RMSNorm / quantization folded into the matvec
+// prologues, SwiGLU and residual adds into their epilogues); nt > 1 quantizes each token's
+// activations once into global memory and runs the same matvec kernels over all tokens.
+static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, const int* pos_dev) {
+    Fused* f = c->f;
+    const int H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
+    for (int li = 0; li < f->n_layer; li++) {
+        const hymt2_fused_layer& L = a->layers[li];
+        const DW *wq = dw(L.wq), *wk = dw(L.wk), *wv = dw(L.wv), *wo = dw(L.wo), *wg = dw(L.wg), *wu = dw(L.wu),
+                 *wd = dw(L.wd);
+        if (!wq || !wk || !wv || !wo || !wg || !wu || !wd) {
+            set_err(c, "fused_forward: layer %d has a missing device weight", li);
+            return false;
+        }
+        const float* attn_norm = f->norm_ptr(li, 0);
+        const float* ffn_norm = f->norm_ptr(li, 1);
+        // ---- attention block
+        JobSpec qkv[3] = {{wq, f->q, Q, EPI_STORE}, {wk, f->k, KV, EPI_STORE}, {wv, f->v, KV, EPI_STORE}};
+        if (nt == 1) {
+            if (!run_matvec(c, qkv, 3, false, 1, PRO_NORM, nullptr, f->d_h, attn_norm, f->eps)) return false;
+        } else {
+            HIPCHK(c, launch_rmsnorm_q8k(f->d_h, attn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
+            if (!run_matvec(c, qkv, 3, false, nt, PRO_NONE, f->act_h, nullptr, nullptr, 0.f)) return false;
+        }
+        AttnArgs at{};
+        at.q = f->q;
+        at.k = f->k;
+        at.v = f->v;
+        at.kc = f->kc + (size_t)li * f->ctx * KV;
+        at.vc = f->vc + (size_t)li * f->ctx * KV;
+        at.ao = f->ao;
+        at.q_norm = f->norm_ptr(li, 2);
+        at.k_norm = f->norm_ptr(li, 3);
+        at.rope_cos = f->rope_c;
+        at.rope_sin = f->rope_s;
+        at.pos_dev = pos_dev;
+        at.pos0 = pos0;
+        at.nt = nt;
+        at.heads = f->heads;
+        at.kv_heads = f->kv_heads;
+        at.hdim = f->hdim;
+        at.rope_half = f->rope_half;
+        at.ctx = f->ctx;
+        at.eps = f->eps;
+        HIPCHK(c, launch_rope_norm_store(at, c->s));
+        HIPCHK(c, launch_attention(at, c->s));
+        JobSpec o{wo, f->d_h, H, EPI_ADD};
+        if (nt == 1) {
+            if (!run_matvec(c, &o, 1, false, 1, PRO_QUANT, nullptr, f->ao, nullptr, 0.f)) return false;
+        } else {
+            HIPCHK(c, launch_quantize_q8k(f->ao, Q, f->act_q, Q, nt, c->s));
+            if (!run_matvec(c, &o, 1, false, nt, PRO_NONE, f->act_q, nullptr, nullptr, 0.f)) return false;
+        }
+        // ---- feed-forward block
+        const bool pair = wg->mw.kind == wu->mw.kind && wg->mw.n == wu->mw.n;
+        JobSpec gu[2] = {{wg, f->g, F, EPI_STORE}, {wu, f->u, F, EPI_STORE}};
+        if (nt == 1) {
+            if (!run_matvec(c, gu, 2, pair, 1, PRO_NORM, nullptr, f->d_h, ffn_norm, f->eps)) return false;
+        } else {
+            HIPCHK(c, launch_rmsnorm_q8k(f->d_h, ffn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
+            if (!run_matvec(c, gu, 2, pair, nt, PRO_NONE, f->act_h, nullptr, nullptr, 0.f)) return false;
+        }
+        if (!pair) HIPCHK(c, launch_silu_mul(f->g, f->u, nt * F, c->s));
+        JobSpec dn{wd, f->d_h, H, EPI_ADD};
+        if (nt == 1) {
+            if (!run_matvec(c, &dn, 1, false, 1, PRO_QUANT, nullptr, f->g, nullptr, 0.f)) return false;
+        } else {
+            HIPCHK(c, launch_quantize_q8k(f->g, F, f->act_f, F, nt, c->s));
+            if (!run_matvec(c, &dn, 1, false, nt, PRO_NONE, f->act_f, nullptr, nullptr, 0.f)) return false;
+        }
+    }
+    return true;
+}
+
+// Output RMSNorm + LM head on the last token (src/model.c:887-900), optionally folding the
+// greedy argmax into f->key.
+static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax, int vocab_out) {
+    Fused* f = c->f;
+    const DW* ow = dw(a->outw);
+    if (!ow || ow->mw.k != f->hidden) {
+        set_err(c, "fused_forward: missing or mismatched output weight");
+        return false;
+    }
+    if (!ensure_logits(c, f, ow->mw.n)) return false;
+    const float* hl = f->d_h + (size_t)(nt - 1) * f->hidden;
+    if (ow->mw.kind == KIND_F16 || ow->mw.kind == KIND_F32) {
+        HeadArgs h{};
+        h.W = ow->mw;
+        h.h = hl;
+        h.norm_w = f->out_norm;
+        h.eps = f->eps;
+        h.logits = f->logits;
+        h.argmax_key = argmax ? f->key : nullptr;
+        h.n_arg = vocab_out;
+        HIPCHK(c, launch_head(h, c->s));
+    } else {
+        JobSpec j{ow, f->logits, ow->mw.n, EPI_STORE};
+        if (!run_matvec(c, &j, 1, false, 1, PRO_NORM, nullptr, hl, f->out_norm, f->eps)) return false;
+        if (argmax) HIPCHK(c, launch_argmax(f->logits, vocab_out, f->key, c->s));
+    }
+    return true;
+}
+
+static std::vector<const void*> weight_sig(const hymt2_fused_args* a) {
+    std::vector<const void*> s;
+    for (int li = 0; li < a->n_layer; li++) {
+        const hymt2_fused_layer& L = a->layers[li];
+        for (const void* p : {L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd}) s.push_back(p);
+    }
+    s.push_back(a->outw);
+    return s;
+}
+
+template <typename Fn>
+static bool capture(Ctx* c, hipGraphExec_t* exec, Fn&& body) {
+    hipGraph_t g = nullptr;
+    HIPCHK(c, hipStreamBeginCapture(c->s, hipStreamCaptureModeThreadLocal));
+    const bool ok = body();
+    hipError_t e = hipStreamEndCapture(c->s, &g);
+    if (!ok || e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        if (ok) set_err(c, "graph capture failed: %s", hipGetErrorString(e));
+        return false;
+    }
+    e = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        set_err(c, "graph instantiate failed: %s", hipGetErrorString(e));
+        return false;
+    }
+    return true;
+}
+
+// One forward of a->nt tokens at a->pos0 (reference cu_fused_forward, src/cuda.c:339-421):
+// host h in, logits out when want_logits, KV written at absolute positions; exactly one host
+// synchronisation. Single-token forwards replay a captured graph that reads pos0 from device
+// memory, uploaded together with h in one copy.
+static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !a || !c->f || !same_shape(c->f, a) || a->nt < 1 || a->nt > HY_MAX_BATCH || !a->h ||
+        a->pos0 < 0 || a->pos0 + a->nt > c->f->ctx)
+        return false;
+    Fused* f = c->f;
+    const int nt = a->nt;
+    const size_t hbytes = (size_t)nt * f->hidden * 4;
+    const bool logits = a->want_logits && a->outw && a->logits;
+    memcpy(f->in_host, a->h, hbytes);
+    if (nt == 1) {
+        memcpy(f->in_host + (size_t)HY_MAX_BATCH * f->hidden * 4, &a->pos0, 4);
+        HIPCHK(c, hipMemcpyAsync(f->in_dev, f->in_host, f->in_bytes, hipMemcpyHostToDevice, c->s));
+        if (logits && !ensure_logits(c, f, dw(a->outw)->mw.n)) return false;
+        std::vector<const void*> sig = weight_sig(a);
+        sig.push_back(reinterpret_cast<const void*>((uintptr_t)logits));
+        if (!f->g_fwd || f->sig_fwd != sig) {
+            if (f->g_fwd) (void)hipGraphExecDestroy(f->g_fwd);
+            f->g_fwd = nullptr;
+            if (!capture(c, &f->g_fwd, [&] {
+                    return enqueue_layers(c, a, 1, 0, f->d_pos) && (!logits || enqueue_head(c, a, 1, false, 0));
+                })) {
+                c->broken = true;
+                return false;
+            }
+            f->sig_fwd = sig;
+        }
+        HIPCHK(c, hipGraphLaunch(f->g_fwd, c->s));
+    } else {
+        HIPCHK(c, hipMemcpyAsync(f->d_h, f->in_host, hbytes, hipMemcpyHostToDevice, c->s));
+        if (!enqueue_layers(c, a, nt, a->pos0, nullptr) || (logits && !enqueue_head(c, a, nt, false, 0))) {
+            c->broken = true;
+            return false;
+        }
+    }
+    if (logits) {
+        HIPCHK(c, hipMemcpyAsync(a->logits, f->logits, (size_t)dw(a->outw)->mw.n * 4, hipMemcpyDeviceToHost, c->s));
+    }
+    HIPCHK(c, hipStreamSynchronize(c->s));
+    return true;
+}
+
+// ----------------------------------------------------------------------------------- context
+
+static void hip_destroy_impl(void* impl) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c) return;
+    (void)hipSetDevice(c->dev);
+    if (c->s) (void)hipStreamSynchronize(c->s);
+    free_fused(c->f);
+    if (c->act) (void)hipFree(c->act);
+    if (c->out) (void)hipFree(c->out);
+    for (hipEvent_t e : c->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->s) (void)hipStreamDestroy(c->s);
+    delete c;
+}
+
+static const hymt2_device_ops kOps = {hip_destroy_impl, hip_upload,        hip_release,       hip_matmul,
+                                      hip_is_sw,        hip_weight_out,    hip_fused_prepare, hip_fused_forward};
+
+extern "C" {
+
+int hy_cuda_probe(char* out, int cap) {
+    const int ok = access("/dev/kfd", R_OK | W_OK) == 0 ? 1 : 0;
+    if (out && cap > 0) snprintf(out, (size_t)cap, "%d", ok);
+    return ok;
+}
+
+void* hymt2_hip_open(char* info, size_t cap) {
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+        if (info && cap) snprintf(info, cap, "no HIP device");
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipSetDevice(0) != hipSuccess || hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+        if (info && cap) snprintf(info, cap, "hipSetDevice(0) failed");
+        return nullptr;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        if (info && cap) snprintf(info, cap, "device 0 is %s; this build targets gfx950", prop.gcnArchName);
+        return nullptr;
+    }
+    Ctx* c = new Ctx();
+    c->dev = 0;
+    if (hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking) != hipSuccess) {
+        if (info && cap) snprintf(info, cap, "hipStreamCreate failed");
+        delete c;
+        return nullptr;
+    }
+    for (hipEvent_t& e : c->ev) (void)hipEventCreate(&e);
+    if (info && cap) snprintf(info, cap, "%s (%s, %d CUs)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName,
+                              prop.multiProcessorCount);
+    return c;
+}
+
+const hymt2_device_ops* hymt2_hip_ops(void) { return &kOps; }
+
+hy_device* hy_cuda_create(const char* pref, char* info, size_t cap) {
+    (void)pref;
+    if (!hy_device_wrap) {
+        if (info && cap) snprintf(info, cap, "hy_device_wrap not found: load through the hymt2 host library");
+        return nullptr;
+    }
+    void* impl = hymt2_hip_open(info, cap);
+    if (!impl) return nullptr;
+    hy_device* d = hy_device_wrap(kDevKindCuda, "hip", impl, &kOps, false);
+    if (!d) hip_destroy_impl(impl);
+    return d;
+}
+
+int hymt2_hip_last_error(void* impl, char* out, int cap) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    const char* s = c ? c->err.c_str() : "no context";
+    if (out && cap > 0) snprintf(out, (size_t)cap, "%s", s);
+    return (int)strlen(s);
+}
+
+int hymt2_hip_abi_layout(char* out, int cap) {
+    return snprintf(out, (size_t)cap,
+                    "weight_t=%zu weight_t.row_bytes=%zu weight_t.pk=%zu weight_t.gpu=%zu hy_fused_layer=%zu "
+                    "hy_fused_args=%zu hy_fused_args.eps=%zu hy_fused_args.layers=%zu hy_fused_args.logits=%zu "
+                    "hy_device_ops=%zu q8k_block=%zu",
+                    sizeof(hymt2_weight), offsetof(hymt2_weight, row_bytes), offsetof(hymt2_weight, pk),
+                    offsetof(hymt2_weight, gpu), sizeof(hymt2_fused_layer), sizeof(hymt2_fused_args),
+                    offsetof(hymt2_fused_args, eps), offsetof(hymt2_fused_args, layers),
+                    offsetof(hymt2_fused_args, logits), sizeof(hymt2_device_ops), sizeof(hymt2_q8k_block));
+}
+
+void* hymt2_hip_stream(void* impl) { return impl ? static_cast<Ctx*>(impl)->s : nullptr; }
+
+int hymt2_hip_quantize_q8k(void* impl, const float* x, void* act, int k, int nt) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || k % 256 || nt < 1) return -1;
+    return launch_quantize_q8k(x, k, static_cast<HyQ8K*>(act), k, nt, c->s) == hipSuccess ? 0 : -2;
+}
+
+int hymt2_hip_matvec(void* impl, hy_dweight* w, const void* act, float* out, int nt) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    const DW* d = dw(w);
+    if (!c || c->broken || !d || nt < 1 || nt > HY_MAX_BATCH || !quant_kind(d->mw.kind)) return -1;
+    JobSpec j{d, out, d->mw.n, EPI_STORE};
+    return run_matvec(c, &j, 1, false, nt, PRO_NONE, static_cast<const HyQ8K*>(act), nullptr, nullptr, 0.f) ? 0 : -2;
+}
+
+int hymt2_hip_selftest_f16(void* impl, const uint16_t* src, float* dst, int n) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || n < 0) return -1;
+    return launch_selftest(src, dst, n, 0, c->s) == hipSuccess ? 0 : -2;
+}
+
+int hymt2_hip_selftest_expf(void* impl, const float* src, float* dst, int n) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || n < 0) return -1;
+    return launch_selftest(src, dst, n, 1, c->s) == hipSuccess ? 0 : -2;
+}
+
+int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
+                       int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !shape || !prompt || !out_ids || n_prompt < 1 || n_gen < 1) return -1;
+    if (!hip_fused_prepare(impl, shape)) return -2;
+    Fused* f = c->f;
+    const DW* e = dw(embd);
+    const DW* ow = dw(shape->outw);
+    if (!e || (e->mw.kind != KIND_F16 && e->mw.kind != KIND_F32) || e->mw.k != f->hidden || !ow) {
+        set_err(c, "generate: embedding must be an uploaded F16/F32 [vocab][hidden] weight");
+        return -3;
+    }
+    const int n_total = n_prompt + n_gen;
+    if (n_total > f->ctx || vocab_out < 1 || vocab_out > ow->mw.n) {
+        set_err(c, "generate: %d positions exceed ctx %d (or bad vocab_out)", n_total, f->ctx);
+        return -4;
+    }
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= e->mw.n) {
+            set_err(c, "generate: prompt id %d out of range", prompt[i]);
+            return -5;
+        }
+    if (n_total > f->ids_cap) {
+        if (f->ids) (void)hipFree(f->ids);
+        f->ids = nullptr;
+        f->ids_cap = 0;
+        if (!dalloc(c, &f->ids, (size_t)n_total * 4)) return -6;
+        f->ids_cap = n_total;
+        free_graphs(f);
+    }
+    if (!ensure_logits(c, f, ow->mw.n)) return -6;
+    std::vector<const void*> sig = weight_sig(shape);
+    sig.push_back(embd);
+    sig.push_back(reinterpret_cast<const void*>((intptr_t)vocab_out));
+    sig.push_back(reinterpret_cast<const void*>((intptr_t)n_prompt));
+    sig.push_back(reinterpret_cast<const void*>((intptr_t)n_total));
+    const uint16_t* e16 = e->mw.kind == KIND_F16 ? static_cast<const uint16_t*>(e->mem) : nullptr;
+    const float* e32 = e->mw.kind == KIND_F32 ? static_cast<const float*>(e->mem) : nullptr;
+    if (!f->g_step || f->sig_step != sig) {
+        if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
+        f->g_step = nullptr;
+        FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e16, e32, f->d_h, f->hidden, n_total};
+        if (!capture(c, &f->g_step, [&] {
+                if (!enqueue_layers(c, shape, 1, 0, f->d_pos) || !enqueue_head(c, shape, 1, true, vocab_out))
+                    return false;
+                return launch_finish(fa, c->s) == hipSuccess;
+            }))
+            return -7;
+        f->sig_step = sig;
+    }
+    // start state: ids[0..n_prompt) = prompt, pos = 0, key = 0, h = embedding of ids[0]
+    memset(f->in_host, 0, f->in_bytes);
+    const size_t pos_off = (size_t)HY_MAX_BATCH * f->hidden * 4;
+    if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
+        hipMemcpyAsync(f->in_dev + pos_off, f->in_host + pos_off, 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
+        hipMemcpyAsync(f->key, f->in_host, 8, hipMemcpyHostToDevice, c->s) != hipSuccess ||
+        launch_embed(f->ids, f->d_pos, e16, e32, f->d_h, f->hidden, c->s) != hipSuccess)
+        return -8;
+    (void)hipEventRecord(c->ev[0], c->s);
+    for (int i = 0; i < n_prompt; i++)
+        if (hipGraphLaunch(f->g_step, c->s) != hipSuccess) return -9;
+    (void)hipEventRecord(c->ev[1], c->s);
+    for (int i = 0; i < n_gen - 1; i++)
+        if (hipGraphLaunch(f->g_step, c->s) != hipSuccess) return -9;
+    (void)hipEventRecord(c->ev[2], c->s);
+    if (hipMemcpyAsync(out_ids, f->ids + n_prompt, (size_t)n_gen * 4, hipMemcpyDeviceToHost, c->s) != hipSuccess ||
+        hipStreamSynchronize(c->s) != hipSuccess) {
+        set_err(c, "generate: device loop failed");
+        c->broken = true;
+        return -10;
+    }
+    if (stats) {
+        float a = 0.f, b = 0.f;
+        (void)hipEventElapsedTime(&a, c->ev[0], c->ev[1]);
+        (void)hipEventElapsedTime(&b, c->ev[1], c->ev[2]);
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->prefill_steps = n_prompt;
+        stats->decode_steps = n_gen - 1;
+    }
+    return n_gen;
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// Shared device-side definitions for the gfx950 Hy-MT2 backend.
+//
+// Numerics contract: every kernel reproduces the reference's scalar CPU arithmetic bit for bit.
+// The library is compiled with -ffp-contract=off (no fused multiply-add unless written as
+// fmaf/fma), correctly rounded fp32 divide/sqrt and fp32 denormals preserved, matching the
+// reference's x86-64 baseline build (src/kernels.c, src/model.c).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifndef HY_HD
+#define HY_HD __host__ __device__
+#endif
+
+#define HY_QK 256
+#define HY_MAX_BATCH 16  // src/internal.h:12
+
+// Q8_K activation block, byte-identical to the reference's q8k_block (src/internal.h:29-41).
+struct alignas(64) HyQ8K {
+    int8_t qp[HY_QK];    // reordered copy: qp[l*64 + j*16 + i] = qs[{0,2,1,3}[j]*64 + l*16 + i]
+    float d;
+    int32_t sum;
+    int16_t bsums[HY_QK / 16];
+    uint8_t pad[24];
+    int8_t qs[HY_QK];    // natural order
+};
+static_assert(sizeof(HyQ8K) == 576, "q8k_block is 576 bytes");
+static_assert(__builtin_offsetof(HyQ8K, d) == 256 && __builtin_offsetof(HyQ8K, sum) == 260 &&
+                  __builtin_offsetof(HyQ8K, bsums) == 264 && __builtin_offsetof(HyQ8K, qs) == 320,
+              "q8k_block layout");
+
+// ----------------------------------------------------------------------------------- bits
+
+HY_HD inline uint32_t hy_fbits(float f) { return __builtin_bit_cast(uint32_t, f); }
+HY_HD inline float hy_bitsf(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// IEEE binary16 -> binary32 (exact, hardware conversion; pinned against the reference's
+// software conversion src/kernels.c:76-98 over all 65536 inputs by the GPU tests).
+__device__ inline float hy_f16(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+__device__ inline float hy_bf16(uint16_t h) { return hy_bitsf((uint32_t)h << 16); }
+
+// Round-to-nearest-even bfloat16 (same formula as src/kernels.c:107-111).
+__device__ inline uint16_t hy_to_bf16(float f) {
+    uint32_t u = hy_fbits(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// ----------------------------------------------------------------------------------- expf
+//
+// expf with results identical to glibc 2.35's x86-64 expf (the FMA variant selected on CPUs
+// with FMA), which the reference calls for softmax and SiLU (src/model.c:787, :875). It
+// restates the published method of ARM's optimized-routines exp2f/expf (Szabolcs Nagy, 2017;
+// adopted by glibc): x*N/ln2 = k + r with N = 32, 2^(k/N) from a 32-entry table with the
+// exponent folded in, and a cubic in r evaluated in double precision, rounded once to float.
+// The table entries are 2^(i/32) correctly rounded to double, minus i<<47. The FMA placement
+// matches glibc's FMA build exactly: checked against the host libm on every float in
+// [-105, 90] (tests/test_expf.py), and on the device against libm in the GPU tests.
+HY_HD inline float hy_expf(float x) {
+    constexpr uint64_t T[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    constexpr double kShift = 0x1.8p+52;
+    constexpr double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
+    constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0);
+    constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const uint32_t ux = hy_fbits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
+        if (ux == 0xff800000u) return 0.f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.f;
+    }
+    const double xd = (double)x;
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const uint64_t t = T[ki & 31u] + (ki << 47);
+    const double s = __builtin_bit_cast(double, t);
+    const double z = __builtin_fma(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// ----------------------------------------------------------------------------------- lanes
+
+// DPP quad_perm controls: swap neighbours [1,0,3,2], swap pairs [2,3,0,1].
+#define HY_DPP_QSWAP1 0xB1
+#define HY_DPP_QSWAP2 0x4E
+
+__device__ inline int hy_quad_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, HY_DPP_QSWAP1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, HY_DPP_QSWAP2, 0xF, 0xF, false);
+    return v;
+}
+
+// Sum over aligned groups of 2^log2g lanes (integer, exact in any order).
+template <int G>
+__device__ inline int hy_group_sum(int v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group");
+    if (G >= 2) v += __shfl_xor(v, 1);
+    if (G >= 4) v += __shfl_xor(v, 2);
+    if (G >= 8) v += __shfl_xor(v, 4);
+    if (G >= 16) v += __shfl_xor(v, 8);
+    if (G >= 32) v += __shfl_xor(v, 16);
+    if (G >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ inline float hy_wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ inline int hy_wave_sum_i(int v) { return hy_group_sum<64>(v); }
+
+// 4 bytes of 2-bit codes in field l of each byte of w, as 4 unsigned bytes 0..3.
+__device__ inline int hy_field(uint32_t w, int l) { return (int)((w >> (2 * l)) & 0x03030303u); }
+
+__device__ inline int hy_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Sequential fp32 sum of x[i]*x[i] in index order, the reference's RMSNorm accumulation
+// (src/model.c:721-730, scalar branch). x must be 16-byte aligned (LDS or global).
+__device__ inline float hy_seq_sumsq(const float* x, int n) {
+    float s = 0.f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const float4 a = *reinterpret_cast<const float4*>(x + i);
+        const float4 b = *reinterpret_cast<const float4*>(x + i + 4);
+        s += a.x * a.x; s += a.y * a.y; s += a.z * a.z; s += a.w * a.w;
+        s += b.x * b.x; s += b.y * b.y; s += b.z * b.z; s += b.w * b.w;
+    }
+    for (; i < n; i++) s += x[i] * x[i];
+    return s;
+}
+
+// Sequential fp32 sum in index order.
+__device__ inline float hy_seq_sum(const float* x, int n) {
+    float s = 0.f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const float4 a = *reinterpret_cast<const float4*>(x + i);
+        const float4 b = *reinterpret_cast<const float4*>(x + i + 4);
+        s += a.x; s += a.y; s += a.z; s += a.w;
+        s += b.x; s += b.y; s += b.z; s += b.w;
+    }
+    for (; i < n; i++) s += x[i];
+    return s;
+}

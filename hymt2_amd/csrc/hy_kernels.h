@@ -1,0 +1,111 @@
+// Kernel launch descriptors and launchers (host-visible, C++ linkage, library-internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hy_common.h"
+
+namespace hy {
+
+enum Kind : int { KIND_PANEL = 0, KIND_Q4K = 1, KIND_Q6K = 2, KIND_F16 = 3, KIND_F32 = 4 };
+enum Epi : int { EPI_STORE = 0, EPI_ADD = 1 };
+enum Pro : int { PRO_NONE = 0, PRO_NORM = 1, PRO_QUANT = 2 };
+
+// One weight matrix resident in HBM, in the layout its matvec kernel streams.
+//   PANEL: w = codes [n][nb][64 B], ps = fp32 [n][nb]
+//   Q4K:   w = reference blocks [n][nb][144 B]
+//   Q6K:   planes, all indexed by block id n*nb+b: w = ql [..][128], w2 = qh [..][64],
+//          sc = int8 scales [..][16], dh = f16 d [..] (same 210 bytes per block, aligned)
+//   F16/F32: w = rows [n][k]
+struct MvWeight {
+    int kind, n, k, nb;
+    int pshift, poff;
+    const uint8_t* w;
+    const uint8_t* w2;
+    const int8_t* sc;
+    const uint16_t* dh;
+    const float* ps;
+};
+
+struct MvJob {
+    MvWeight W;
+    float* out;       // out[t * ldo + r]
+    int ldo;
+    int epi;          // EPI_STORE / EPI_ADD (out = out + acc, the reference's residual add)
+    int rows_per_wg;  // tile height
+    int wg_begin;     // first workgroup of this job in the grid
+};
+
+constexpr int kMaxJobs = 3;
+
+struct MvLaunch {
+    MvJob job[kMaxJobs];
+    int njobs;
+    int pair;              // 1: job[0]=gate, job[1]=up share tiles; job[0].out <- silu(g)*u
+    int nt;
+    const HyQ8K* act;      // PRO_NONE: activations [nt][nb]
+    const float* x;        // PRO_NORM: h [nt][K]; PRO_QUANT: vector [nt][K]
+    const float* norm_w;   // PRO_NORM weights [K]
+    float eps;
+    int K;                 // input dim of all jobs
+    int segs;              // 16-byte segments per thread (1, 2 or 4)
+};
+
+// Which (template) variant a matvec launch uses; decided on the host.
+int mv_segments_per_block(int kind);
+
+hipError_t launch_quantize_q8k(const float* x, int ldx, HyQ8K* act, int K, int nt, hipStream_t s);
+hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, int nt, float* xn_out,
+                              HyQ8K* act_out, hipStream_t s);
+hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s);
+
+struct AttnArgs {
+    float* q;              // [nt][qdim]
+    const float* k;        // [nt][kvdim]
+    const float* v;        // [nt][kvdim]
+    uint16_t* kc;          // layer base of K cache [kv_heads][ctx][hdim]
+    uint16_t* vc;          // layer base of V cache
+    float* ao;             // [nt][qdim]
+    const float* q_norm;   // [hdim]
+    const float* k_norm;   // [hdim]
+    const float* rope_cos; // [ctx][rope_half]
+    const float* rope_sin;
+    const int* pos_dev;    // optional: pos0 read from device memory (graph replay)
+    int pos0, nt, heads, kv_heads, hdim, rope_half, ctx;
+    float eps;
+};
+hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+struct HeadArgs {
+    MvWeight W;            // F16 or F32 rows
+    const float* h;        // last token's hidden state [K]
+    const float* norm_w;   // output norm
+    float eps;
+    float* logits;         // [n]
+    unsigned long long* argmax_key;  // optional fused argmax over rows < n_arg
+    int n_arg;
+};
+hipError_t launch_head(const HeadArgs& a, hipStream_t s);
+
+struct FinishArgs {
+    unsigned long long* argmax_key;
+    int* ids;              // token ids [n_total]
+    int* step;             // device step counter (position of the token just processed)
+    int n_prompt;
+    const uint16_t* embd;  // F16 embedding rows [vocab][H]
+    const float* embd32;   // or F32 rows
+    float* h;              // next step's input [H]
+    int H;
+    int n_total;
+};
+hipError_t launch_finish(const FinishArgs& a, hipStream_t s);
+hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16, const float* embd32, float* h,
+                        int H, hipStream_t s);
+
+hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
+hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s);
+hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s);
+
+}  // namespace hy

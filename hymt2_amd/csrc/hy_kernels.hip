@@ -1,0 +1,705 @@
+// gfx950 kernels of the Hy-MT2 token loop. Every kernel reproduces the reference's scalar CPU
+// arithmetic (src/kernels.c, src/model.c; HYMT2_ISA=scalar) bit for bit: integer block dots
+// are exact in any order, and every fp32 reduction runs sequentially in the reference's order
+// in one lane, while the parallel work (loads, int8 dot products, exponentials, elementwise
+// ops) is spread over the wavefronts.
+#include "hy_kernels.h"
+
+namespace hy {
+
+// =========================================================================== Q8_K quantize
+
+// One wavefront quantizes one 256-element block (src/kernels.c:128-165). Lane l owns elements
+// 4l..4l+3. src and dst are flat pointers (LDS or global).
+__device__ void q8k_quantize_wave(const float* src, HyQ8K* dst, int lane) {
+    const float4 v4 = reinterpret_cast<const float4*>(src)[lane];
+    const float e[4] = {v4.x, v4.y, v4.z, v4.w};
+    uint32_t amax = 0;
+    for (int i = 0; i < 4; i++) amax = max(amax, hy_fbits(e[i]) & 0x7fffffffu);
+    for (int o = 32; o >= 1; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
+    uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
+    if (amax == 0) {  // all-zero block -> all-zero record
+        for (int i = lane; i < 576 / 4; i += 64) dw[i] = 0;
+        return;
+    }
+    int first = 256;
+    for (int i = 3; i >= 0; i--)
+        if ((hy_fbits(e[i]) & 0x7fffffffu) == amax) first = 4 * lane + i;
+    for (int o = 32; o >= 1; o >>= 1) first = min(first, __shfl_xor(first, o));
+    const float vmax = src[first];
+    const float iscale = -127.f / vmax;
+    int q[4];
+    for (int i = 0; i < 4; i++) {
+        int r = (int)__builtin_rintf(iscale * e[i]);
+        q[i] = r > 127 ? 127 : (r < -127 ? -127 : r);
+    }
+    const int s4 = q[0] + q[1] + q[2] + q[3];
+    const int s16 = hy_quad_sum(s4);
+    const int total = hy_wave_sum_i(s4);
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    // natural order qs
+    dw[320 / 4 + lane] = packed;
+    // reordered copy: element c*64 + l*16 + i lands at qp[l*64 + {0,2,1,3}[c]*16 + i]
+    const int c = lane >> 4, l = (lane >> 2) & 3, i0 = 4 * (lane & 3);
+    const int seg = (c == 1) ? 2 : (c == 2 ? 1 : c);
+    dw[(l * 64 + seg * 16 + i0) / 4] = packed;
+    if ((lane & 3) == 0) dst->bsums[lane >> 2] = (int16_t)s16;
+    if (lane < 6) dw[296 / 4 + lane] = 0;
+    if (lane == 0) {
+        dst->d = 1.f / iscale;
+        dst->sum = total;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_quantize_q8k(const float* x, int ldx, HyQ8K* act, int nb) {
+    const int b = blockIdx.x, t = blockIdx.y;
+    q8k_quantize_wave(x + (size_t)t * ldx + (size_t)b * HY_QK, act + (size_t)t * nb + b, threadIdx.x);
+}
+
+hipError_t launch_quantize_q8k(const float* x, int ldx, HyQ8K* act, int K, int nt, hipStream_t s) {
+    const int nb = K / HY_QK;
+    k_quantize_q8k<<<dim3(nb, nt), 64, 0, s>>>(x, ldx, act, nb);
+    return hipGetLastError();
+}
+
+// =========================================================================== RMSNorm
+
+// x (LDS, K floats) <- x * (1/sqrtf(sum(x*x)/K + eps)) * w, the scalar RMSNorm of
+// src/model.c:719-739 with its sum taken sequentially by thread 0.
+__device__ void rmsnorm_lds(float* xs, const float* w, int K, float eps, float* scale_slot) {
+    if (threadIdx.x == 0) {
+        const float sum = hy_seq_sumsq(xs, K);
+        *scale_slot = 1.0f / sqrtf(sum / (float)K + eps);
+    }
+    __syncthreads();
+    const float scale = *scale_slot;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = xs[i] * scale * w[i];
+    __syncthreads();
+}
+
+__device__ void load_vec_lds(float* xs, const float* x, int K) {
+    for (int i = threadIdx.x; i < K / 4; i += blockDim.x)
+        reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
+    __syncthreads();
+}
+
+__device__ void quantize_lds_blocks(const float* xs, HyQ8K* act, int K) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    for (int b = wave; b < K / HY_QK; b += nw) q8k_quantize_wave(xs + b * HY_QK, act + b, lane);
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float* w, float eps, int H,
+                                                     float* xn_out, HyQ8K* act_out) {
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float scale_slot;
+    const int t = blockIdx.x;
+    load_vec_lds(xs, h + (size_t)t * H, H);
+    rmsnorm_lds(xs, w, H, eps, &scale_slot);
+    if (xn_out)
+        for (int i = threadIdx.x; i < H; i += blockDim.x) xn_out[(size_t)t * H + i] = xs[i];
+    if (act_out) quantize_lds_blocks(xs, act_out + (size_t)t * (H / HY_QK), H);
+}
+
+hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, int nt, float* xn_out,
+                              HyQ8K* act_out, hipStream_t s) {
+    k_rmsnorm_q8k<<<nt, 256, H * sizeof(float), s>>>(h, w, eps, H, xn_out, act_out);
+    return hipGetLastError();
+}
+
+// =========================================================================== matvec
+
+int mv_segments_per_block(int kind) { return kind == KIND_PANEL ? 4 : 8; }
+
+// Exact integer part of one 16-byte segment, reduced over the lanes of its block.
+struct SegLoad {
+    uint4 a;      // panel codes / Q4_K qs / Q6_K ql
+    uint4 b;      // Q4_K header (d, dmin, scales) / Q6_K qh
+    float ps;     // panel scale
+    int sc;       // Q6_K two int8 scales packed
+    uint16_t dh;  // Q6_K f16 d
+};
+
+__device__ inline void seg_coords(int kind, int nb, int f, int& rl, int& b, int& sub) {
+    const int spb = kind == KIND_PANEL ? 4 : 8;
+    sub = f % spb;
+    const int blk = f / spb;
+    b = blk % nb;
+    rl = blk / nb;
+}
+
+__device__ inline SegLoad seg_load(const MvWeight& W, int row, int b, int sub) {
+    SegLoad L;
+    const size_t blk = (size_t)row * W.nb + b;
+    if (W.kind == KIND_PANEL) {
+        L.a = *reinterpret_cast<const uint4*>(W.w + blk * 64 + sub * 16);
+        L.ps = W.ps[blk];
+    } else if (W.kind == KIND_Q4K) {
+        const uint8_t* base = W.w + blk * 144;
+        L.b = *reinterpret_cast<const uint4*>(base);
+        L.a = *reinterpret_cast<const uint4*>(base + 16 + sub * 16);
+    } else {  // Q6K planes: sub = h*4 + qpair*2 + lq
+        const int h = sub >> 2, qpair = (sub >> 1) & 1, lq = sub & 1;
+        L.a = *reinterpret_cast<const uint4*>(W.w + blk * 128 + 64 * h + 32 * qpair + 16 * lq);
+        L.b = *reinterpret_cast<const uint4*>(W.w2 + blk * 64 + 32 * h + 16 * lq);
+        const int j1 = 8 * h + 2 * qpair + lq;
+        const int8_t* sc = W.sc + blk * 16;
+        L.sc = (int)(uint8_t)sc[j1] | ((int)(uint8_t)sc[j1 + 4] << 8);
+        L.dh = W.dh[blk];
+    }
+    return L;
+}
+
+__device__ inline int q4_scale(const uint8_t* s, int j) {  // src/kernels.c:839-842 (scale)
+    return j < 4 ? (s[j] & 63) : ((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+}
+__device__ inline int q4_min(const uint8_t* s, int j) {  // src/kernels.c:839-842 (min)
+    return j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+}
+
+// fp32 block term of one segment group (valid in every lane of the group). Lanes of invalid
+// segments pass zeros and still join the group reductions.
+template <int KIND>
+__device__ inline float seg_term(const MvWeight& W, const SegLoad& L, const HyQ8K* y, int sub, bool valid) {
+    if (KIND == KIND_PANEL) {
+        int p = 0;
+        if (valid) {
+            const uint32_t w4[4] = {L.a.x, L.a.y, L.a.z, L.a.w};
+            for (int l = 0; l < 4; l++) {
+                const int4 q = *reinterpret_cast<const int4*>(y->qp + l * 64 + sub * 16);
+                p = hy_dot4(hy_field(w4[0], l), q.x, p);
+                p = hy_dot4(hy_field(w4[1], l), q.y, p);
+                p = hy_dot4(hy_field(w4[2], l), q.z, p);
+                p = hy_dot4(hy_field(w4[3], l), q.w, p);
+            }
+        }
+        const int enc = hy_quad_sum(p);
+        if (!valid) return 0.f;
+        // src/kernels.c:576: ps * y.d * float((enc << shift) - off * sum)
+        return L.ps * y->d * (float)((enc << W.pshift) - W.poff * y->sum);
+    } else if (KIND == KIND_Q4K) {
+        int si = 0, sm = 0;
+        float d = 0.f, dmin = 0.f;
+        if (valid) {
+            const uint8_t* hdr = reinterpret_cast<const uint8_t*>(&L.b);
+            const int g = sub >> 1, half = sub & 1;
+            const int4 qlo = *reinterpret_cast<const int4*>(y->qs + 64 * g + 16 * half);
+            const int4 qhi = *reinterpret_cast<const int4*>(y->qs + 64 * g + 32 + 16 * half);
+            const uint32_t w4[4] = {L.a.x, L.a.y, L.a.z, L.a.w};
+            int s0 = 0, s1 = 0;
+            s0 = hy_dot4((int)(w4[0] & 0x0F0F0F0Fu), qlo.x, s0);
+            s0 = hy_dot4((int)(w4[1] & 0x0F0F0F0Fu), qlo.y, s0);
+            s0 = hy_dot4((int)(w4[2] & 0x0F0F0F0Fu), qlo.z, s0);
+            s0 = hy_dot4((int)(w4[3] & 0x0F0F0F0Fu), qlo.w, s0);
+            s1 = hy_dot4((int)((w4[0] >> 4) & 0x0F0F0F0Fu), qhi.x, s1);
+            s1 = hy_dot4((int)((w4[1] >> 4) & 0x0F0F0F0Fu), qhi.y, s1);
+            s1 = hy_dot4((int)((w4[2] >> 4) & 0x0F0F0F0Fu), qhi.z, s1);
+            s1 = hy_dot4((int)((w4[3] >> 4) & 0x0F0F0F0Fu), qhi.w, s1);
+            si = q4_scale(hdr + 4, 2 * g) * s0 + q4_scale(hdr + 4, 2 * g + 1) * s1;
+            sm = q4_min(hdr + 4, sub) * (y->bsums[2 * sub] + y->bsums[2 * sub + 1]);
+            d = hy_f16((uint16_t)(hdr[0] | (hdr[1] << 8)));
+            dmin = hy_f16((uint16_t)(hdr[2] | (hdr[3] << 8)));
+        }
+        const int sumi = hy_group_sum<8>(si);
+        const int summ = hy_group_sum<8>(sm);
+        if (!valid) return 0.f;
+        // src/kernels.c:875: y.d * (d * float(sumi) - dmin * float(summ))
+        return y->d * (d * (float)sumi - dmin * (float)summ);
+    } else {  // Q6K
+        int acc = 0;
+        if (valid) {
+            const int h = sub >> 2, qpair = (sub >> 1) & 1, lq = sub & 1;
+            const int j1 = 8 * h + 2 * qpair + lq, j2 = j1 + 4;
+            const int4 q1 = *reinterpret_cast<const int4*>(y->qs + 16 * j1);
+            const int4 q2 = *reinterpret_cast<const int4*>(y->qs + 16 * j2);
+            const uint32_t wl[4] = {L.a.x, L.a.y, L.a.z, L.a.w};
+            const uint32_t wh[4] = {L.b.x, L.b.y, L.b.z, L.b.w};
+            const int q1a[4] = {q1.x, q1.y, q1.z, q1.w}, q2a[4] = {q2.x, q2.y, q2.z, q2.w};
+            int d1 = 0, d2 = 0;
+            for (int i = 0; i < 4; i++) {
+                const uint32_t lo = (wl[i] & 0x0F0F0F0Fu) | (((wh[i] >> (2 * qpair)) & 0x03030303u) << 4);
+                const uint32_t hi = ((wl[i] >> 4) & 0x0F0F0F0Fu) | (((wh[i] >> (2 * qpair + 4)) & 0x03030303u) << 4);
+                d1 = hy_dot4((int)lo, q1a[i], d1);
+                d2 = hy_dot4((int)hi, q2a[i], d2);
+            }
+            const int sc1 = (int)(int8_t)(L.sc & 0xff), sc2 = (int)(int8_t)((L.sc >> 8) & 0xff);
+            acc = sc1 * (d1 - 32 * y->bsums[j1]) + sc2 * (d2 - 32 * y->bsums[j2]);
+        }
+        const int tot = hy_group_sum<8>(acc);
+        if (!valid) return 0.f;
+        // src/kernels.c:833: f16(d) * y.d * float(acc)
+        return hy_f16(L.dh) * y->d * (float)tot;
+    }
+}
+
+template <int SEGS, int PRO>
+__global__ __launch_bounds__(256) void k_matvec(MvLaunch L) {
+    extern __shared__ __align__(64) unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int wg = blockIdx.x;
+    int j = 0;
+    if (!L.pair)
+        while (j + 1 < L.njobs && wg >= L.job[j + 1].wg_begin) j++;
+    const MvJob& J = L.job[j];
+    const MvWeight& W = J.W;
+    const int nb = W.nb;
+    const int rpw = J.rows_per_wg;
+    const int r0 = (wg - J.wg_begin) * rpw;
+    const int rows = min(rpw, W.n - r0);
+    const int spb = W.kind == KIND_PANEL ? 4 : 8;
+    const int per_w = rows * nb * spb;           // segments of one weight in this tile
+    const int nseg = per_w * (L.pair ? 2 : 1);
+
+    // 1. issue all weight loads of this thread first: they stay in flight through the prologue
+    SegLoad ld[SEGS];
+    int coord[SEGS];
+#pragma unroll
+    for (int s = 0; s < SEGS; s++) {
+        const int f = tid + 256 * s;
+        coord[s] = -1;
+        if (f < nseg) {
+            const int which = L.pair ? f / per_w : 0;
+            int rl, b, sub;
+            seg_coords(W.kind, nb, f - which * per_w, rl, b, sub);
+            const MvWeight& Wi = L.pair ? L.job[which].W : W;
+            ld[s] = seg_load(Wi, r0 + rl, b, sub);
+            coord[s] = f;
+        }
+    }
+
+    // 2. activation block source (prologue builds it in LDS)
+    const HyQ8K* act = L.act;
+    unsigned char* terms_base = smem;
+    if (PRO == PRO_NORM) {
+        HyQ8K* act_lds = reinterpret_cast<HyQ8K*>(smem);
+        float* xs = reinterpret_cast<float*>(smem + (size_t)nb * sizeof(HyQ8K));
+        __shared__ float scale_slot;
+        load_vec_lds(xs, L.x, L.K);
+        rmsnorm_lds(xs, L.norm_w, L.K, L.eps, &scale_slot);
+        quantize_lds_blocks(xs, act_lds, L.K);
+        __syncthreads();
+        act = act_lds;
+        terms_base = smem + (size_t)nb * sizeof(HyQ8K) + (size_t)L.K * sizeof(float);
+    } else if (PRO == PRO_QUANT) {  // quantize the fp32 input straight from global memory
+        HyQ8K* act_lds = reinterpret_cast<HyQ8K*>(smem);
+        quantize_lds_blocks(L.x, act_lds, L.K);
+        __syncthreads();
+        act = act_lds;
+        terms_base = smem + (size_t)nb * sizeof(HyQ8K);
+    }
+    float* terms = reinterpret_cast<float*>(terms_base);  // [which][t][rl][b]
+
+    // 3. exact block terms
+    for (int t = 0; t < L.nt; t++) {
+#pragma unroll
+        for (int s = 0; s < SEGS; s++) {
+            const int f = tid + 256 * s;
+            if (256 * s >= nseg) break;  // uniform: no thread of this WG has segment s
+            const bool valid = coord[s] >= 0;
+            int which = 0, rl = 0, b = 0, sub = f & (spb - 1);
+            if (valid) {
+                which = L.pair ? f / per_w : 0;
+                seg_coords(W.kind, nb, f - which * per_w, rl, b, sub);
+            }
+            const MvWeight& Wi = L.pair ? L.job[which].W : W;
+            const HyQ8K* y = act + (size_t)t * nb + b;
+            float term;
+            if (W.kind == KIND_PANEL) term = seg_term<KIND_PANEL>(Wi, ld[s], y, sub, valid);
+            else if (W.kind == KIND_Q4K) term = seg_term<KIND_Q4K>(Wi, ld[s], y, sub, valid);
+            else term = seg_term<KIND_Q6K>(Wi, ld[s], y, sub, valid);
+            if (valid && sub == 0) terms[(((size_t)which * L.nt + t) * rpw + rl) * nb + b] = term;
+        }
+    }
+    __syncthreads();
+
+    // 4. sequential per-row combine in block order, then the epilogue
+    for (int i = tid; i < rows * L.nt; i += 256) {
+        const int t = i / rows, rl = i % rows;
+        const float* tg = terms + ((size_t)t * rpw + rl) * nb;
+        float acc = 0.f;
+        for (int b = 0; b < nb; b++) acc += tg[b];
+        const size_t o = (size_t)t * J.ldo + r0 + rl;
+        if (L.pair) {
+            const float* tu = terms + (((size_t)L.nt + t) * rpw + rl) * nb;
+            float u = 0.f;
+            for (int b = 0; b < nb; b++) u += tu[b];
+            // SwiGLU, src/model.c:873-876: g / (1 + expf(-g)) * u
+            J.out[o] = acc / (1.0f + hy_expf(-acc)) * u;
+        } else if (J.epi == EPI_ADD) {
+            J.out[o] = J.out[o] + acc;  // residual h += tmp, src/model.c:865-869
+        } else {
+            J.out[o] = acc;
+        }
+    }
+}
+
+template <int PRO>
+static hipError_t launch_mv_pro(const MvLaunch& L, int grid, size_t lds, hipStream_t s) {
+    switch (L.segs) {
+    case 1: k_matvec<1, PRO><<<grid, 256, lds, s>>>(L); break;
+    case 2: k_matvec<2, PRO><<<grid, 256, lds, s>>>(L); break;
+    case 4: k_matvec<4, PRO><<<grid, 256, lds, s>>>(L); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s) {
+    int max_rpw = 0;
+    for (int j = 0; j < L.njobs; j++) max_rpw = max(max_rpw, L.job[j].rows_per_wg);
+    const int nb = L.job[0].W.nb;
+    size_t lds = (size_t)(L.pair ? 2 : 1) * L.nt * max_rpw * nb * sizeof(float);
+    if (pro == PRO_NORM) lds += (size_t)nb * sizeof(HyQ8K) + (size_t)L.K * sizeof(float);
+    if (pro == PRO_QUANT) lds += (size_t)nb * sizeof(HyQ8K);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (pro == PRO_NONE) return launch_mv_pro<PRO_NONE>(L, grid, lds, s);
+    if (pro == PRO_NORM) return launch_mv_pro<PRO_NORM>(L, grid, lds, s);
+    return launch_mv_pro<PRO_QUANT>(L, grid, lds, s);
+}
+
+// =========================================================================== RoPE + q/k norm + KV
+
+// One wavefront per (token, head-slot): slots [0, heads) are q heads, [heads, heads+kv_heads)
+// are kv heads. NeoX RoPE (src/model.c:754-765), then the per-head RMSNorm (src/model.c:840-841),
+// then for kv heads the bf16 RNE store of k and v at the absolute position (src/model.c:842-847).
+__global__ __launch_bounds__(64) void k_rope_norm_store(AttnArgs a) {
+    __shared__ __align__(16) float row[256];
+    __shared__ float scale_slot;
+    const int t = blockIdx.x, slot = blockIdx.y, lane = threadIdx.x;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
+    const int hd = a.hdim, half = a.rope_half;
+    const bool is_q = slot < a.heads;
+    const int head = is_q ? slot : slot - a.heads;
+    const int qdim = a.heads * hd, kvdim = a.kv_heads * hd;
+    const float* src = is_q ? a.q + (size_t)t * qdim + (size_t)head * hd : a.k + (size_t)t * kvdim + (size_t)head * hd;
+    for (int d = lane; d < hd; d += 64) row[d] = src[d];
+    __syncthreads();
+    const float* c = a.rope_cos + (size_t)pos * half;
+    const float* sn = a.rope_sin + (size_t)pos * half;
+    for (int i = lane; i < half; i += 64) {
+        const float x0 = row[i], x1 = row[i + half];
+        row[i] = x0 * c[i] - x1 * sn[i];
+        row[i + half] = x0 * sn[i] + x1 * c[i];
+    }
+    __syncthreads();
+    if (lane == 0) {
+        const float sum = hy_seq_sumsq(row, hd);
+        scale_slot = 1.0f / sqrtf(sum / (float)hd + a.eps);
+    }
+    __syncthreads();
+    const float scale = scale_slot;
+    const float* nw = is_q ? a.q_norm : a.k_norm;
+    for (int d = lane; d < hd; d += 64) row[d] = row[d] * scale * nw[d];
+    __syncthreads();
+    if (is_q) {
+        float* dst = a.q + (size_t)t * qdim + (size_t)head * hd;
+        for (int d = lane; d < hd; d += 64) dst[d] = row[d];
+    } else {
+        const size_t off = ((size_t)head * a.ctx + pos) * hd;
+        const float* v = a.v + (size_t)t * kvdim + (size_t)head * hd;
+        for (int d = lane; d < hd; d += 64) {
+            a.kc[off + d] = hy_to_bf16(row[d]);
+            a.vc[off + d] = hy_to_bf16(v[d]);
+        }
+    }
+}
+
+hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s) {
+    if (a.hdim > 256 || a.hdim % 4 || 2 * a.rope_half > a.hdim) return hipErrorInvalidValue;
+    k_rope_norm_store<<<dim3(a.nt, a.heads + a.kv_heads), 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// =========================================================================== attention
+
+// One workgroup per (token, q head): causal GQA attention over the bf16 cache, the
+// reference's attn_task (src/model.c:767-795) with dot_bf16_scalar (src/kernels.c:1111-1121)
+// and axpy_bf16_scalar (:1122-1124). Scores live in LDS; the softmax sum and the output
+// accumulation run sequentially over positions, as in the reference.
+template <int DPL>
+__global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[8];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hd = a.hdim;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
+    const int n = pos + 1;
+    const int kvh = h / (a.heads / a.kv_heads);
+    const int qdim = a.heads * hd;
+    float* qs = sm;          // [hd]
+    float* sc = sm + 256;    // [n]
+    for (int d = tid; d < hd; d += 256) qs[d] = a.q[(size_t)t * qdim + (size_t)h * hd + d];
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)hd);
+    const uint16_t* K = a.kc + (size_t)kvh * a.ctx * hd;
+    const uint16_t* V = a.vc + (size_t)kvh * a.ctx * hd;
+    float mx = -__builtin_inff();
+    for (int jj = tid; jj < n; jj += 256) {
+        const uint16_t* kr = K + (size_t)jj * hd;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        for (int d = 0; d < hd; d += 8) {
+            const uint4 kv = *reinterpret_cast<const uint4*>(kr + d);
+            a0 += qs[d + 0] * hy_bitsf(kv.x << 16);
+            a1 += qs[d + 1] * hy_bitsf(kv.x & 0xffff0000u);
+            a2 += qs[d + 2] * hy_bitsf(kv.y << 16);
+            a3 += qs[d + 3] * hy_bitsf(kv.y & 0xffff0000u);
+            a0 += qs[d + 4] * hy_bitsf(kv.z << 16);
+            a1 += qs[d + 5] * hy_bitsf(kv.z & 0xffff0000u);
+            a2 += qs[d + 6] * hy_bitsf(kv.w << 16);
+            a3 += qs[d + 7] * hy_bitsf(kv.w & 0xffff0000u);
+        }
+        const float s = ((a0 + a1) + (a2 + a3)) * scale;
+        sc[jj] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = hy_wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int jj = tid; jj < n; jj += 256) sc[jj] = hy_expf(sc[jj] - mx);
+    __syncthreads();
+    if (tid == 0) red[4] = 1.0f / hy_seq_sum(sc, n);
+    __syncthreads();
+    const float inv = red[4];
+    for (int jj = tid; jj < n; jj += 256) sc[jj] = sc[jj] * inv;
+    __syncthreads();
+    if (wave == 0) {
+        float o[DPL];
+        for (int i = 0; i < DPL; i++) o[i] = 0.f;
+        const int d0 = lane * DPL;
+        for (int jj = 0; jj < n; jj++) {
+            const float p = sc[jj];
+            const uint16_t* vr = V + (size_t)jj * hd + d0;
+            if (DPL == 2) {
+                const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vr);
+                o[0] += p * hy_bitsf(v2 << 16);
+                o[DPL - 1] += p * hy_bitsf(v2 & 0xffff0000u);
+            } else {
+                for (int i = 0; i < DPL; i++) o[i] += p * hy_bf16(vr[i]);
+            }
+        }
+        float* dst = a.ao + (size_t)t * qdim + (size_t)h * hd + d0;
+        for (int i = 0; i < DPL; i++) dst[i] = o[i];
+    }
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+    const size_t lds = (256 + (size_t)a.ctx) * sizeof(float);
+    if (lds > 160 * 1024 || a.heads % a.kv_heads) return hipErrorInvalidValue;
+    const dim3 grid(a.nt, a.heads);
+    switch (a.hdim) {
+    case 64: k_attention<1><<<grid, 256, lds, s>>>(a); break;
+    case 128: k_attention<2><<<grid, 256, lds, s>>>(a); break;
+    case 256: k_attention<4><<<grid, 256, lds, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// =========================================================================== LM head
+
+__device__ inline unsigned long long argmax_key(float v, int idx) {
+    uint32_t u = hy_fbits(v);
+    if (u == 0x80000000u) u = 0;                       // -0 ties with +0 (first index wins)
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0;     // NaN never wins
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+
+__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// One lane per vocabulary row: logits[r] = sum_j f16(W[r][j]) * xn[j] accumulated sequentially
+// (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). Rows are staged
+// through LDS 64 bytes at a time so each lane reads its own row without uncoalesced loads.
+// Optionally folds the greedy argmax (first index on ties, src/model.c:945-948) into a
+// 64-bit atomicMax key.
+template <bool F16>
+__global__ __launch_bounds__(256) void k_head(HeadArgs a) {
+    extern __shared__ __align__(16) float xs[];    // [K] normalized input
+    __shared__ __align__(16) uint32_t tile[2][256 * 20];
+    __shared__ float scale_slot;
+    const int tid = threadIdx.x;
+    const int K = a.W.k, n = a.W.n;
+    const int r0 = blockIdx.x * 256;
+    const int rowb = F16 ? 2 * K : 4 * K;
+    const int nstage = rowb / 64;
+    // first stage loads before the prologue
+    uint4 pre[4];
+    auto load_stage = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int f = tid + 256 * i;
+            const int rr = f >> 2, part = f & 3;
+            const int row = min(r0 + rr, n - 1);
+            pre[i] = *reinterpret_cast<const uint4*>(a.W.w + (size_t)row * rowb + (size_t)st * 64 + part * 16);
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int f = tid + 256 * i;
+            const int rr = f >> 2, part = f & 3;
+            *reinterpret_cast<uint4*>(&tile[buf][rr * 20 + part * 4]) = pre[i];
+        }
+    };
+    load_stage(0);
+    load_vec_lds(xs, a.h, K);
+    rmsnorm_lds(xs, a.norm_w, K, a.eps, &scale_slot);
+    store_stage(0);
+    __syncthreads();
+    float acc = 0.f;
+    for (int st = 0; st < nstage; st++) {
+        const int buf = st & 1;
+        if (st + 1 < nstage) load_stage(st + 1);
+        const uint32_t* tr = &tile[buf][tid * 20];
+        if (F16) {
+            const float* xk = xs + st * 32;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 v = *reinterpret_cast<const uint4*>(tr + 4 * q);
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    acc += hy_f16((uint16_t)(w[e] & 0xffffu)) * xk[8 * q + 2 * e];
+                    acc += hy_f16((uint16_t)(w[e] >> 16)) * xk[8 * q + 2 * e + 1];
+                }
+            }
+        } else {
+            const float* xk = xs + st * 16;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 v = *reinterpret_cast<const uint4*>(tr + 4 * q);
+                acc += hy_bitsf(v.x) * xk[4 * q + 0];
+                acc += hy_bitsf(v.y) * xk[4 * q + 1];
+                acc += hy_bitsf(v.z) * xk[4 * q + 2];
+                acc += hy_bitsf(v.w) * xk[4 * q + 3];
+            }
+        }
+        if (st + 1 < nstage) {
+            store_stage(buf ^ 1);
+        }
+        __syncthreads();
+    }
+    const int r = r0 + tid;
+    if (r < n) a.logits[r] = acc;
+    if (a.argmax_key) {
+        unsigned long long key = (r < a.n_arg) ? argmax_key(acc, r) : 0ull;
+        key = wave_max_u64(key);
+        if ((tid & 63) == 0 && key) atomicMax(a.argmax_key, key);
+    }
+}
+
+hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
+    const int grid = (a.W.n + 255) / 256;
+    const size_t lds = (size_t)a.W.k * sizeof(float);
+    if (a.W.kind == KIND_F16) {
+        if (a.W.k % 32) return hipErrorInvalidValue;
+        k_head<true><<<grid, 256, lds, s>>>(a);
+    } else if (a.W.kind == KIND_F32) {
+        if (a.W.k % 16) return hipErrorInvalidValue;
+        k_head<false><<<grid, 256, lds, s>>>(a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// =========================================================================== step finish
+
+__device__ void embed_row(const uint16_t* e16, const float* e32, int tok, float* h, int H) {
+    for (int i = threadIdx.x; i < H; i += blockDim.x)
+        h[i] = e16 ? hy_f16(e16[(size_t)tok * H + i]) : e32[(size_t)tok * H + i];
+}
+
+// Greedy step tail: token = argmax key; the next input is the next prompt id while the prompt
+// lasts, else the argmax (recorded in ids). Embeds the next token's row into h, advances the
+// device step counter and clears the key.
+__global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
+    __shared__ int next_tok, next_pos;
+    if (threadIdx.x == 0) {
+        const unsigned long long key = *a.argmax_key;
+        const int best = key ? (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull)) : 0;
+        const int step = *a.step;
+        const int nx = step + 1;
+        int tok;
+        if (nx < a.n_prompt) {
+            tok = a.ids[nx];
+        } else {
+            tok = best;
+            if (nx < a.n_total) a.ids[nx] = best;
+        }
+        next_tok = tok;
+        next_pos = nx;
+    }
+    __syncthreads();
+    embed_row(a.embd, a.embd32, next_tok, a.h, a.H);
+    if (threadIdx.x == 0) {
+        *a.step = next_pos;
+        *a.argmax_key = 0ull;
+    }
+}
+
+hipError_t launch_finish(const FinishArgs& a, hipStream_t s) {
+    k_finish<<<1, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_embed(const int* ids, const int* step, const uint16_t* e16,
+                                               const float* e32, float* h, int H) {
+    embed_row(e16, e32, ids[*step], h, H);
+}
+
+hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16, const float* embd32, float* h,
+                        int H, hipStream_t s) {
+    k_embed<<<1, 256, 0, s>>>(ids, step, embd16, embd32, h, H);
+    return hipGetLastError();
+}
+
+// =========================================================================== small kernels
+
+// Greedy argmax over rows [0, n) of fp32 logits into a 64-bit key (first index on ties).
+__global__ __launch_bounds__(256) void k_argmax(const float* v, int n, unsigned long long* key) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    unsigned long long k = i < n ? argmax_key(v[i], i) : 0ull;
+    k = wave_max_u64(k);
+    if ((threadIdx.x & 63) == 0 && k) atomicMax(key, k);
+}
+
+hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s) {
+    k_argmax<<<(n + 255) / 256, 256, 0, s>>>(v, n, key);
+    return hipGetLastError();
+}
+
+// g <- g / (1 + expf(-g)) * u (src/model.c:873-876), for gate/up pairs that cannot share tiles.
+__global__ void k_silu_mul(float* g, const float* u, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        const float x = g[i];
+        g[i] = x / (1.0f + hy_expf(-x)) * u[i];
+    }
+}
+
+hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s) {
+    k_silu_mul<<<(n + 255) / 256, 256, 0, s>>>(g, u, n);
+    return hipGetLastError();
+}
+
+__global__ void k_selftest(const void* src, float* dst, int n, int what) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    if (what == 0) dst[i] = hy_f16(reinterpret_cast<const uint16_t*>(src)[i]);
+    else dst[i] = hy_expf(reinterpret_cast<const float*>(src)[i]);
+}
+
+hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s) {
+    k_selftest<<<(n + 255) / 256, 256, 0, s>>>(src, dst, n, what);
+    return hipGetLastError();
+}
+
+}  // namespace hy

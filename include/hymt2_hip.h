@@ -1,0 +1,150 @@
+/* hymt2_hip.h: C ABI of the MI355X (gfx950) HIP backend for the Hy-MT2 token loop.
+ *
+ * libhymt2_hip.so plugs into the reference host (zhangbo8418/hymt2) exactly where its CUDA
+ * backend does: the host's device layer calls hy_cuda_create / hy_cuda_probe as extern symbols
+ * (src/device.c:8-9, :79, :168), so linking this library instead of src/cuda.c selects it with
+ * HYMT2_DEVICE=cuda (or auto) and leaves model.c, device.c, gguf.c, tokenizer.c and hymt2.h
+ * unchanged. The device it reports is named "hip".
+ *
+ * The structs below are byte-for-byte mirrors of the reference's interface types; the library
+ * checks their sizes and offsets at compile time and reports them through
+ * hymt2_hip_abi_layout() for the ABI tests.
+ *
+ * Numerics: every result equals the reference's scalar CPU path (HYMT2_ISA=scalar,
+ * HYMT2_REPACK=1) bit for bit: int32 block dots, fp32 matvec outputs, norms, RoPE, attention,
+ * SwiGLU, logits and greedy token ids.
+ */
+#ifndef HYMT2_HIP_H
+#define HYMT2_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HYMT2_HIP_API __attribute__((visibility("default")))
+
+/* ---------------------------------------------------------------- reference ABI mirrors */
+
+typedef struct hy_device hy_device;   /* opaque, owned by the host (src/device.c:18-24) */
+typedef struct hy_dweight hy_dweight; /* opaque device weight, owned by this backend */
+
+/* == weight_t, src/internal.h:48-61 (64 bytes on LP64) */
+typedef struct hymt2_weight {
+    const uint8_t *data;  /* raw GGUF rows */
+    int type;             /* ggml type: 0 F32, 1 F16, 12 Q4_K, 14 Q6_K, 40 Q2_0C, 43 STQ1_0 */
+    int k;                /* input dim */
+    int n;                /* rows */
+    size_t row_bytes;
+    const uint8_t *pk;    /* panel codes n*(k/256)*64 B (STQ1_0 / Q2_0C) */
+    const float *ps;      /* panel scales n*(k/256) */
+    int pshift, poff;
+    void *gpu;
+} hymt2_weight;
+
+/* == q8k_block, src/internal.h:29-41 (576 bytes, 64-byte aligned) */
+typedef struct hymt2_q8k_block {
+    int8_t qp[256];
+    float d;
+    int32_t sum;
+    int16_t bsums[16];
+    uint8_t pad[24];
+    int8_t qs[256];
+} hymt2_q8k_block;
+
+/* == hy_fused_layer, src/device.h:44-47 */
+typedef struct hymt2_fused_layer {
+    hy_dweight *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+} hymt2_fused_layer;
+
+/* == hy_fused_args, src/device.h:49-59 */
+typedef struct hymt2_fused_args {
+    int n_layer, hidden, ffn, heads, kv_heads, hdim, qdim, kvdim, ctx, rope_half, nt, pos0;
+    float eps;
+    int want_logits;
+    hymt2_fused_layer *layers;
+    hy_dweight *outw;
+    const float *out_norm;
+    const float *rope_cos, *rope_sin; /* [ctx * rope_half] */
+    float *h;      /* in: [nt * hidden] after the host embedding */
+    float *logits; /* out when want_logits: [outw->n] */
+} hymt2_fused_args;
+
+/* == hy_device_ops, src/device.h:70-80 */
+typedef struct hymt2_device_ops {
+    void (*destroy_impl)(void *impl);
+    hy_dweight *(*upload)(void *impl, const hymt2_weight *w);
+    void (*release)(hy_dweight *w);
+    bool (*matmul)(void *impl, hy_dweight *const *ws, float *const *outs, int cnt, const hymt2_q8k_block *xq, int nt);
+    bool (*is_software)(const void *impl);
+    float *(*weight_out)(hy_dweight *w);
+    bool (*fused_prepare)(void *impl, const hymt2_fused_args *shape);
+    bool (*fused_forward)(void *impl, hymt2_fused_args *a);
+} hymt2_device_ops;
+
+/* ---------------------------------------------------------------- drop-in entry points */
+
+/* Replaces hy_cuda_create, src/cuda.c:151-183. Creates the HIP context on device 0 and wraps
+ * it with the host's hy_device_wrap (src/device.c:25-35) under the name "hip". Returns NULL
+ * with a message in info when no gfx950 device is usable or when the library is loaded
+ * without the reference host (hy_device_wrap absent). */
+HYMT2_HIP_API hy_device *hy_cuda_create(const char *pref, char *info, size_t cap);
+
+/* Replaces hy_cuda_probe, src/cuda.c:18-34: writes "1" when the HIP runtime reports at least
+ * one GPU, else "0"; returns the same as an int. Never initialises a device context. */
+HYMT2_HIP_API int hy_cuda_probe(char *out, int cap);
+
+/* ---------------------------------------------------------------- extensions (no counterpart
+ * in the reference interface) */
+
+/* The backend context and vtable without the reference host: the same impl pointer and
+ * hy_device_ops table that hy_cuda_create hands to hy_device_wrap. For callers that drive the
+ * backend directly (benchmarks, tests, FFI users without the C host). */
+HYMT2_HIP_API void *hymt2_hip_open(char *info, size_t cap);
+HYMT2_HIP_API const hymt2_device_ops *hymt2_hip_ops(void);
+
+/* Last error message of a context ("" if none); returns its length. */
+HYMT2_HIP_API int hymt2_hip_last_error(void *impl, char *out, int cap);
+
+/* "name=value" list of the ABI struct sizes and offsets this library was compiled with. */
+HYMT2_HIP_API int hymt2_hip_abi_layout(char *out, int cap);
+
+/* The context's HIP stream (hipStream_t), on which every kernel of the context runs. */
+HYMT2_HIP_API void *hymt2_hip_stream(void *impl);
+
+/* Kernel-level entry points on device pointers, enqueued on the context stream (asynchronous;
+ * 0 on success, negative on error):
+ *   quantize_q8k: x[nt][k] fp32 -> act[nt][k/256] q8k_block (quantize_q8k, src/kernels.c:128)
+ *   matvec:       out[t*n + r] = row r of an uploaded weight . act[t] (matmul_rows,
+ *                 src/kernels.c:1241), panel / Q4_K / Q6_K weights, 1 <= nt <= 16 */
+HYMT2_HIP_API int hymt2_hip_quantize_q8k(void *impl, const float *x_dev, void *act_dev, int k, int nt);
+HYMT2_HIP_API int hymt2_hip_matvec(void *impl, hy_dweight *w, const void *act_dev, float *out_dev, int nt);
+
+/* Device self-checks of the scalar conversions the kernels use (same device functions):
+ * f16 -> f32 and expf over n inputs. */
+HYMT2_HIP_API int hymt2_hip_selftest_f16(void *impl, const uint16_t *src_dev, float *dst_dev, int n);
+HYMT2_HIP_API int hymt2_hip_selftest_expf(void *impl, const float *src_dev, float *dst_dev, int n);
+
+/* Device-resident greedy generation (no host round trip per token): prompt ids are run one
+ * position per step through the fused forward, then greedy decode continues on the device,
+ * the argmax (first index on ties over the first vocab_out rows) feeding the next step's
+ * embedding row. `shape` is a prepared hy_fused_args (layers, outw, norms, rope tables);
+ * `embd` is the uploaded F16/F32 token embedding (the tied head is allowed). Writes n_gen ids.
+ * Stop tokens are not checked. Timings come from HIP events on the context stream. */
+typedef struct hymt2_gen_stats {
+    double prefill_ms;  /* steps that consume prompt ids */
+    double decode_ms;   /* steps that consume generated ids */
+    int prefill_steps, decode_steps;
+} hymt2_gen_stats;
+HYMT2_HIP_API int hymt2_hip_generate(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
+                                     const int *prompt, int n_prompt, int n_gen, int *out_ids,
+                                     hymt2_gen_stats *stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -69,6 +69,12 @@ size_t oc_row_bytes(int type, int k) { /* src/kernels.c:113-124 */
 
 static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
+/* libm expf over an array: the exact function the reference calls in softmax and SiLU
+ * (src/model.c:787, :875). */
+void oc_expf_n(const float *x, float *y, int n) {
+    for (int i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
 /* ------------------------------------------------------------------ Q8_K */
 
 /* Q8_K activation quantization, src/kernels.c:128-165: the signed value of the first element

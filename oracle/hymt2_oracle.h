@@ -71,6 +71,7 @@ float oc_f16_to_f32(uint16_t h);
 uint16_t oc_f32_to_bf16(float f);
 float oc_bf16_to_f32(uint16_t h);
 size_t oc_row_bytes(int type, int k);
+void oc_expf_n(const float *x, float *y, int n);
 
 /* ---- activation quantization ---- */
 void oc_quantize_q8k(const float *x, int k, oc_q8k *y);

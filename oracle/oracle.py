@@ -57,7 +57,7 @@ def lib():
             "oc_state_new": (vp, [C.POINTER(OcModel)]), "oc_state_free": (None, [vp]),
             "oc_forward": (None, [vp, vp, i, i, i, vp]), "oc_state_hidden": (vp, [vp]),
             "oc_argmax": (i, [vp, i]), "oc_generate": (i, [vp, vp, i, i, i, vp]),
-            "oc_set_threads": (None, [i]),
+            "oc_set_threads": (None, [i]), "oc_expf_n": (None, [vp, vp, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -68,6 +68,13 @@ def lib():
 
 def _p(a):
     return None if a is None else a.ctypes.data
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().oc_expf_n(x.ctypes.data, y.ctypes.data, x.size)
+    return y
 
 
 def q8k_empty(nblocks: int) -> np.ndarray:
@@ -150,9 +157,12 @@ class OracleModel:
         self.vocab_n = model["outw"].n
 
     def __del__(self):
-        if getattr(self, "state", None):
-            lib().oc_state_free(self.state)
-            self.state = None
+        try:
+            if getattr(self, "state", None):
+                lib().oc_state_free(self.state)
+                self.state = None
+        except Exception:  # interpreter shutdown
+            pass
 
     def forward(self, toks, pos0: int, want_logits=True):
         toks = np.ascontiguousarray(toks, dtype=np.int32)
