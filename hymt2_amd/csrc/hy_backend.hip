@@ -67,6 +67,8 @@ struct Fused {
     unsigned long long* key = nullptr;
     int* ids = nullptr;
     int ids_cap = 0;
+    int gen_total = 0;   // positions of the current device loop (0: no loop begun)
+    int gen_steps = 0;   // steps enqueued so far
     hipGraphExec_t g_fwd = nullptr, g_step = nullptr;
     std::vector<const void*> sig_fwd, sig_step;
     float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
@@ -226,25 +228,24 @@ struct JobSpec {
     int epi;
 };
 
-// Tile the jobs over workgroups: the smallest segments-per-thread whose grid stays within
-// about four resident workgroups per CU.
-static bool build_launch(const JobSpec* js, int njobs, bool pair, int nt, MvLaunch& L, int& grid) {
+// Tile the jobs over workgroups of `threads` lanes: the smallest segments-per-thread whose grid
+// stays within a few resident workgroups per CU.
+static bool build_launch(const JobSpec* js, int njobs, bool pair, int nt, int threads, MvLaunch& L, int& grid) {
     memset(&L, 0, sizeof L);
     L.njobs = njobs;
     L.pair = pair ? 1 : 0;
     L.nt = nt;
+    L.threads = threads;
     const int K = js[0].w->mw.k;
+    const int max_wgs = threads == 1024 ? 128 : 1024;
     for (int segs : {1, 2, 4}) {
         int wgs = 0;
         bool ok = true;
-        for (int j = 0; j < njobs; j++) {
+        for (int j = 0; j < njobs && ok; j++) {
             const MvWeight& m = js[j].w->mw;
             const int spr = m.nb * mv_segments_per_block(m.kind) * (pair ? 2 : 1);
-            const int rpw = (256 * segs) / spr;
-            if (rpw < 1) {
-                ok = false;
-                break;
-            }
+            const int rpw = (threads * segs) / spr;
+            if (rpw < 1) ok = false;
             L.job[j].rows_per_wg = rpw;
             L.job[j].wg_begin = wgs;
             if (!pair || j == 0) wgs += (m.n + rpw - 1) / rpw;
@@ -252,7 +253,7 @@ static bool build_launch(const JobSpec* js, int njobs, bool pair, int nt, MvLaun
         if (!ok) continue;
         L.segs = segs;
         grid = wgs;
-        if (wgs <= 1024 || segs == 4) break;
+        if (wgs <= max_wgs) break;
     }
     if (!L.segs) return false;
     for (int j = 0; j < njobs; j++) {
@@ -271,19 +272,27 @@ static bool build_launch(const JobSpec* js, int njobs, bool pair, int nt, MvLaun
     return true;
 }
 
-static bool run_matvec(Ctx* c, const JobSpec* js, int njobs, bool pair, int nt, int pro, const HyQ8K* act,
-                       const float* x, const float* norm_w, float eps) {
+struct MvOpts {
+    int pro = PRO_NONE;
+    int threads = 256;
+    const HyQ8K* act = nullptr;
+    const float* x = nullptr;
+    const float* norm_w = nullptr;
+    float eps = 0.f;
+};
+
+static bool run_matvec(Ctx* c, const JobSpec* js, int njobs, bool pair, int nt, const MvOpts& o) {
     MvLaunch L;
     int grid = 0;
-    if (!build_launch(js, njobs, pair, nt, L, grid)) {
+    if (!build_launch(js, njobs, pair, nt, o.threads, L, grid)) {
         set_err(c, "matvec: unsupported job combination");
         return false;
     }
-    L.act = act;
-    L.x = x;
-    L.norm_w = norm_w;
-    L.eps = eps;
-    HIPCHK(c, launch_matvec(L, pro, grid, c->s));
+    L.act = o.act;
+    L.x = o.x;
+    L.norm_w = o.norm_w;
+    L.eps = o.eps;
+    HIPCHK(c, launch_matvec(L, o.pro, grid, c->s));
     return true;
 }
 
@@ -331,7 +340,9 @@ static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, in
     for (int i = 0; i < cnt; i++) {
         const DW* w = reinterpret_cast<const DW*>(ws[i]);
         JobSpec j{w, c->out + off, w->mw.n, EPI_STORE};
-        if (!run_matvec(c, &j, 1, false, nt, PRO_NONE, static_cast<const HyQ8K*>(c->act), nullptr, nullptr, 0.f)) {
+        MvOpts o;
+        o.act = static_cast<const HyQ8K*>(c->act);
+        if (!run_matvec(c, &j, 1, false, nt, o)) {
             c->broken = true;
             return false;
         }
@@ -461,10 +472,12 @@ static bool ensure_logits(Ctx* c, Fused* f, int n) {
 
 static const DW* dw(hy_dweight* p) { return reinterpret_cast<const DW*>(p); }
 
-// Enqueues all layers of one forward of nt tokens (the order of src/model.c:822-886). nt == 1
-// uses the fused single-token kernels (RMSNorm / quantization folded into the matvec
-// prologues, SwiGLU and residual adds into their epilogues); nt > 1 quantizes each token's
-// activations once into global memory and runs the same matvec kernels over all tokens.
+// Enqueues all layers of one forward of nt tokens (the order of src/model.c:822-886).
+// nt == 1, per layer: [qkv matvec with the RMSNorm + Q8_K prologue] -> [attention block: RoPE,
+// q/k norm, KV store, attention, Q8_K of the output] -> [o matvec + residual] -> [gate/up
+// matvec with the RMSNorm prologue, SwiGLU and Q8_K epilogue] -> [down matvec + residual].
+// nt > 1 quantizes each token's activations once into global memory and runs the general
+// RoPE / attention kernels and the same matvec kernels over all tokens.
 static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, const int* pos_dev) {
     Fused* f = c->f;
     const int H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
@@ -478,60 +491,102 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
         }
         const float* attn_norm = f->norm_ptr(li, 0);
         const float* ffn_norm = f->norm_ptr(li, 1);
+        uint16_t* kc = f->kc + (size_t)li * f->ctx * KV;
+        uint16_t* vc = f->vc + (size_t)li * f->ctx * KV;
         // ---- attention block
         JobSpec qkv[3] = {{wq, f->q, Q, EPI_STORE}, {wk, f->k, KV, EPI_STORE}, {wv, f->v, KV, EPI_STORE}};
+        MvOpts o1;
         if (nt == 1) {
-            if (!run_matvec(c, qkv, 3, false, 1, PRO_NORM, nullptr, f->d_h, attn_norm, f->eps)) return false;
+            o1.pro = PRO_NORM;
+            o1.threads = 1024;
+            o1.x = f->d_h;
+            o1.norm_w = attn_norm;
+            o1.eps = f->eps;
         } else {
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, attn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
-            if (!run_matvec(c, qkv, 3, false, nt, PRO_NONE, f->act_h, nullptr, nullptr, 0.f)) return false;
+            o1.act = f->act_h;
         }
-        AttnArgs at{};
-        at.q = f->q;
-        at.k = f->k;
-        at.v = f->v;
-        at.kc = f->kc + (size_t)li * f->ctx * KV;
-        at.vc = f->vc + (size_t)li * f->ctx * KV;
-        at.ao = f->ao;
-        at.q_norm = f->norm_ptr(li, 2);
-        at.k_norm = f->norm_ptr(li, 3);
-        at.rope_cos = f->rope_c;
-        at.rope_sin = f->rope_s;
-        at.pos_dev = pos_dev;
-        at.pos0 = pos0;
-        at.nt = nt;
-        at.heads = f->heads;
-        at.kv_heads = f->kv_heads;
-        at.hdim = f->hdim;
-        at.rope_half = f->rope_half;
-        at.ctx = f->ctx;
-        at.eps = f->eps;
-        HIPCHK(c, launch_rope_norm_store(at, c->s));
-        HIPCHK(c, launch_attention(at, c->s));
-        JobSpec o{wo, f->d_h, H, EPI_ADD};
-        if (nt == 1) {
-            if (!run_matvec(c, &o, 1, false, 1, PRO_QUANT, nullptr, f->ao, nullptr, 0.f)) return false;
+        if (!run_matvec(c, qkv, 3, false, nt, o1)) return false;
+        const bool fused_attn = nt == 1 && 256 % f->hdim == 0 && (f->heads / f->kv_heads) % (256 / f->hdim) == 0 &&
+                                attn_decode_lds(f->hdim, f->ctx) <= 96 * 1024;
+        if (fused_attn) {
+            AttnDecodeArgs ad{};
+            ad.q = f->q;
+            ad.k = f->k;
+            ad.v = f->v;
+            ad.kc = kc;
+            ad.vc = vc;
+            ad.q_norm = f->norm_ptr(li, 2);
+            ad.k_norm = f->norm_ptr(li, 3);
+            ad.rope_cos = f->rope_c;
+            ad.rope_sin = f->rope_s;
+            ad.pos_dev = pos_dev;
+            ad.pos0 = pos0;
+            ad.act_out = f->act_q;
+            ad.ao_out = nullptr;
+            ad.heads = f->heads;
+            ad.kv_heads = f->kv_heads;
+            ad.hdim = f->hdim;
+            ad.rope_half = f->rope_half;
+            ad.ctx = f->ctx;
+            ad.eps = f->eps;
+            HIPCHK(c, launch_attn_decode(ad, c->s));
         } else {
+            AttnArgs at{};
+            at.q = f->q;
+            at.k = f->k;
+            at.v = f->v;
+            at.kc = kc;
+            at.vc = vc;
+            at.ao = f->ao;
+            at.q_norm = f->norm_ptr(li, 2);
+            at.k_norm = f->norm_ptr(li, 3);
+            at.rope_cos = f->rope_c;
+            at.rope_sin = f->rope_s;
+            at.pos_dev = pos_dev;
+            at.pos0 = pos0;
+            at.nt = nt;
+            at.heads = f->heads;
+            at.kv_heads = f->kv_heads;
+            at.hdim = f->hdim;
+            at.rope_half = f->rope_half;
+            at.ctx = f->ctx;
+            at.eps = f->eps;
+            HIPCHK(c, launch_rope_norm_store(at, c->s));
+            HIPCHK(c, launch_attention(at, c->s));
             HIPCHK(c, launch_quantize_q8k(f->ao, Q, f->act_q, Q, nt, c->s));
-            if (!run_matvec(c, &o, 1, false, nt, PRO_NONE, f->act_q, nullptr, nullptr, 0.f)) return false;
         }
+        JobSpec o{wo, f->d_h, H, EPI_ADD};
+        MvOpts o2;
+        o2.act = f->act_q;
+        if (!run_matvec(c, &o, 1, false, nt, o2)) return false;
         // ---- feed-forward block
         const bool pair = wg->mw.kind == wu->mw.kind && wg->mw.n == wu->mw.n;
         JobSpec gu[2] = {{wg, f->g, F, EPI_STORE}, {wu, f->u, F, EPI_STORE}};
+        MvOpts o3;
         if (nt == 1) {
-            if (!run_matvec(c, gu, 2, pair, 1, PRO_NORM, nullptr, f->d_h, ffn_norm, f->eps)) return false;
+            o3.pro = PRO_NORM;
+            o3.threads = 1024;
+            o3.x = f->d_h;
+            o3.norm_w = ffn_norm;
+            o3.eps = f->eps;
         } else {
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, ffn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
-            if (!run_matvec(c, gu, 2, pair, nt, PRO_NONE, f->act_h, nullptr, nullptr, 0.f)) return false;
+            o3.act = f->act_h;
         }
+        if (!run_matvec(c, gu, 2, pair, nt, o3)) return false;
         if (!pair) HIPCHK(c, launch_silu_mul(f->g, f->u, nt * F, c->s));
         JobSpec dn{wd, f->d_h, H, EPI_ADD};
+        MvOpts o4;
         if (nt == 1) {
-            if (!run_matvec(c, &dn, 1, false, 1, PRO_QUANT, nullptr, f->g, nullptr, 0.f)) return false;
+            o4.pro = PRO_QUANT;
+            o4.threads = 1024;
+            o4.x = f->g;
         } else {
             HIPCHK(c, launch_quantize_q8k(f->g, F, f->act_f, F, nt, c->s));
-            if (!run_matvec(c, &dn, 1, false, nt, PRO_NONE, f->act_f, nullptr, nullptr, 0.f)) return false;
+            o4.act = f->act_f;
         }
+        if (!run_matvec(c, &dn, 1, false, nt, o4)) return false;
     }
     return true;
 }
@@ -559,7 +614,12 @@ static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax,
         HIPCHK(c, launch_head(h, c->s));
     } else {
         JobSpec j{ow, f->logits, ow->mw.n, EPI_STORE};
-        if (!run_matvec(c, &j, 1, false, 1, PRO_NORM, nullptr, hl, f->out_norm, f->eps)) return false;
+        MvOpts o;
+        o.pro = PRO_NORM;
+        o.x = hl;
+        o.norm_w = f->out_norm;
+        o.eps = f->eps;
+        if (!run_matvec(c, &j, 1, false, 1, o)) return false;
         if (argmax) HIPCHK(c, launch_argmax(f->logits, vocab_out, f->key, c->s));
     }
     return true;
@@ -742,7 +802,9 @@ int hymt2_hip_matvec(void* impl, hy_dweight* w, const void* act, float* out, int
     const DW* d = dw(w);
     if (!c || c->broken || !d || nt < 1 || nt > HY_MAX_BATCH || !quant_kind(d->mw.kind)) return -1;
     JobSpec j{d, out, d->mw.n, EPI_STORE};
-    return run_matvec(c, &j, 1, false, nt, PRO_NONE, static_cast<const HyQ8K*>(act), nullptr, nullptr, 0.f) ? 0 : -2;
+    MvOpts o;
+    o.act = static_cast<const HyQ8K*>(act);
+    return run_matvec(c, &j, 1, false, nt, o) ? 0 : -2;
 }
 
 int hymt2_hip_selftest_f16(void* impl, const uint16_t* src, float* dst, int n) {
@@ -757,26 +819,26 @@ int hymt2_hip_selftest_expf(void* impl, const float* src, float* dst, int n) {
     return launch_selftest(src, dst, n, 1, c->s) == hipSuccess ? 0 : -2;
 }
 
-int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
-                       int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
+int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out,
+                        const int* prompt, int n_prompt, int n_total) {
     Ctx* c = static_cast<Ctx*>(impl);
-    if (!c || c->broken || !shape || !prompt || !out_ids || n_prompt < 1 || n_gen < 1) return -1;
+    if (!c || c->broken || !shape || !prompt || n_prompt < 1 || n_total <= n_prompt) return -1;
     if (!hip_fused_prepare(impl, shape)) return -2;
     Fused* f = c->f;
+    f->gen_total = 0;
     const DW* e = dw(embd);
     const DW* ow = dw(shape->outw);
     if (!e || (e->mw.kind != KIND_F16 && e->mw.kind != KIND_F32) || e->mw.k != f->hidden || !ow) {
-        set_err(c, "generate: embedding must be an uploaded F16/F32 [vocab][hidden] weight");
+        set_err(c, "gen_begin: embedding must be an uploaded F16/F32 [vocab][hidden] weight");
         return -3;
     }
-    const int n_total = n_prompt + n_gen;
     if (n_total > f->ctx || vocab_out < 1 || vocab_out > ow->mw.n) {
-        set_err(c, "generate: %d positions exceed ctx %d (or bad vocab_out)", n_total, f->ctx);
+        set_err(c, "gen_begin: %d positions exceed ctx %d (or bad vocab_out)", n_total, f->ctx);
         return -4;
     }
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= e->mw.n) {
-            set_err(c, "generate: prompt id %d out of range", prompt[i]);
+            set_err(c, "gen_begin: prompt id %d out of range", prompt[i]);
             return -5;
         }
     if (n_total > f->ids_cap) {
@@ -813,21 +875,61 @@ int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* em
     if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->in_dev + pos_off, f->in_host + pos_off, 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->key, f->in_host, 8, hipMemcpyHostToDevice, c->s) != hipSuccess ||
-        launch_embed(f->ids, f->d_pos, e16, e32, f->d_h, f->hidden, c->s) != hipSuccess)
-        return -8;
-    (void)hipEventRecord(c->ev[0], c->s);
-    for (int i = 0; i < n_prompt; i++)
-        if (hipGraphLaunch(f->g_step, c->s) != hipSuccess) return -9;
-    (void)hipEventRecord(c->ev[1], c->s);
-    for (int i = 0; i < n_gen - 1; i++)
-        if (hipGraphLaunch(f->g_step, c->s) != hipSuccess) return -9;
-    (void)hipEventRecord(c->ev[2], c->s);
-    if (hipMemcpyAsync(out_ids, f->ids + n_prompt, (size_t)n_gen * 4, hipMemcpyDeviceToHost, c->s) != hipSuccess ||
+        launch_embed(f->ids, f->d_pos, e16, e32, f->d_h, f->hidden, c->s) != hipSuccess ||
         hipStreamSynchronize(c->s) != hipSuccess) {
-        set_err(c, "generate: device loop failed");
+        set_err(c, "gen_begin: device setup failed");
         c->broken = true;
-        return -10;
+        return -8;
     }
+    f->gen_total = n_total;
+    f->gen_steps = 0;
+    return 0;
+}
+
+int hymt2_hip_gen_steps(void* impl, int n) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !c->f || !c->f->gen_total || n < 0) return -1;
+    Fused* f = c->f;
+    if (f->gen_steps + n > f->gen_total - 1) {
+        set_err(c, "gen_steps: %d + %d steps exceed the %d positions of this loop", f->gen_steps, n, f->gen_total);
+        return -2;
+    }
+    for (int i = 0; i < n; i++)
+        if (hipGraphLaunch(f->g_step, c->s) != hipSuccess) {
+            set_err(c, "gen_steps: hipGraphLaunch failed");
+            c->broken = true;
+            return -3;
+        }
+    f->gen_steps += n;
+    return 0;
+}
+
+int hymt2_hip_gen_read(void* impl, int* ids, int first, int count) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !c->f || !c->f->gen_total || !ids || first < 0 || count < 0 ||
+        first + count > c->f->gen_total)
+        return -1;
+    if (hipMemcpyAsync(ids, c->f->ids + first, (size_t)count * 4, hipMemcpyDeviceToHost, c->s) != hipSuccess ||
+        hipStreamSynchronize(c->s) != hipSuccess) {
+        set_err(c, "gen_read: copy failed");
+        c->broken = true;
+        return -2;
+    }
+    return count;
+}
+
+int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
+                       int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || !out_ids || n_gen < 1) return -1;
+    int rc = hymt2_hip_gen_begin(impl, shape, embd, vocab_out, prompt, n_prompt, n_prompt + n_gen);
+    if (rc) return rc;
+    (void)hipEventRecord(c->ev[0], c->s);
+    if ((rc = hymt2_hip_gen_steps(impl, n_prompt))) return rc;
+    (void)hipEventRecord(c->ev[1], c->s);
+    if ((rc = hymt2_hip_gen_steps(impl, n_gen - 1))) return rc;
+    (void)hipEventRecord(c->ev[2], c->s);
+    if ((rc = hymt2_hip_gen_read(impl, out_ids, n_prompt, n_gen)) != n_gen) return rc;
     if (stats) {
         float a = 0.f, b = 0.f;
         (void)hipEventElapsedTime(&a, c->ev[0], c->ev[1]);
@@ -838,6 +940,22 @@ int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* em
         stats->decode_steps = n_gen - 1;
     }
     return n_gen;
+}
+
+int hymt2_hip_head(void* impl, hy_dweight* w, const float* h, const float* norm_w, float eps, float* logits,
+                   int n_arg, unsigned long long* key) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    const DW* d = dw(w);
+    if (!c || c->broken || !d || (d->mw.kind != KIND_F16 && d->mw.kind != KIND_F32) || n_arg > d->mw.n) return -1;
+    HeadArgs a{};
+    a.W = d->mw;
+    a.h = h;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.logits = logits;
+    a.argmax_key = key;
+    a.n_arg = n_arg;
+    return launch_head(a, c->s) == hipSuccess ? 0 : -2;
 }
 
 }  // extern "C"

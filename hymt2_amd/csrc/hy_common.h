@@ -97,66 +97,109 @@ HY_HD inline float hy_expf(float x) {
 
 // ----------------------------------------------------------------------------------- lanes
 
-// DPP quad_perm controls: swap neighbours [1,0,3,2], swap pairs [2,3,0,1].
+// DPP row controls (gfx9 encoding): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror. All four read a lane of the same 16-lane row, so every lane has a valid source.
 #define HY_DPP_QSWAP1 0xB1
 #define HY_DPP_QSWAP2 0x4E
+#define HY_DPP_HMIRROR 0x141
+#define HY_DPP_MIRROR 0x140
+
+template <int CTRL>
+__device__ inline int hy_dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
 
 __device__ inline int hy_quad_sum(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, HY_DPP_QSWAP1, 0xF, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, HY_DPP_QSWAP2, 0xF, 0xF, false);
+    v += hy_dpp<HY_DPP_QSWAP1>(v);
+    v += hy_dpp<HY_DPP_QSWAP2>(v);
     return v;
 }
 
-// Sum over aligned groups of 2^log2g lanes (integer, exact in any order).
+// Sum over aligned groups of G lanes (integer, exact in any order). G <= 16 stays in DPP.
 template <int G>
 __device__ inline int hy_group_sum(int v) {
-    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group");
-    if (G >= 2) v += __shfl_xor(v, 1);
-    if (G >= 4) v += __shfl_xor(v, 2);
-    if (G >= 8) v += __shfl_xor(v, 4);
-    if (G >= 16) v += __shfl_xor(v, 8);
-    if (G >= 32) v += __shfl_xor(v, 16);
-    if (G >= 64) v += __shfl_xor(v, 32);
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group");
+    if (G >= 2) v += hy_dpp<HY_DPP_QSWAP1>(v);
+    if (G >= 4) v += hy_dpp<HY_DPP_QSWAP2>(v);
+    if (G >= 8) v += hy_dpp<HY_DPP_HMIRROR>(v);
+    if (G >= 16) v += hy_dpp<HY_DPP_MIRROR>(v);
     return v;
+}
+
+// Whole-wave reductions: DPP inside each 16-lane row, then the four row results through
+// readlane. The result is wave-uniform. Requires all 64 lanes active.
+__device__ inline int hy_wave_sum_i(int v) {
+    v = hy_group_sum<16>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
+
+__device__ inline uint32_t hy_wave_max_u(uint32_t v) {
+    int x = (int)v;
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP1>(x));
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP2>(x));
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_HMIRROR>(x));
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane(x, 0), b = (uint32_t)__builtin_amdgcn_readlane(x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane(x, 32), d = (uint32_t)__builtin_amdgcn_readlane(x, 48);
+    return max(max(a, b), max(c, d));
+}
+
+__device__ inline int hy_wave_min_i(int x) {
+    x = min(x, hy_dpp<HY_DPP_QSWAP1>(x));
+    x = min(x, hy_dpp<HY_DPP_QSWAP2>(x));
+    x = min(x, hy_dpp<HY_DPP_HMIRROR>(x));
+    x = min(x, hy_dpp<HY_DPP_MIRROR>(x));
+    const int a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
+    const int c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
+    return min(min(a, b), min(c, d));
 }
 
 __device__ inline float hy_wave_max(float v) {
+    // fmax is exact and order-free; NaN-free inputs assumed
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;
 }
-
-__device__ inline int hy_wave_sum_i(int v) { return hy_group_sum<64>(v); }
 
 // 4 bytes of 2-bit codes in field l of each byte of w, as 4 unsigned bytes 0..3.
 __device__ inline int hy_field(uint32_t w, int l) { return (int)((w >> (2 * l)) & 0x03030303u); }
 
 __device__ inline int hy_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// Sequential fp32 sum of x[i]*x[i] in index order, the reference's RMSNorm accumulation
-// (src/model.c:721-730, scalar branch). x must be 16-byte aligned (LDS or global).
-__device__ inline float hy_seq_sumsq(const float* x, int n) {
+// Sequential fp32 sum p[0] + p[1] + ... + p[n-1] in index order, computed by one whole
+// wavefront (all 64 lanes active; the result is wave-uniform). p may be LDS or global, 16-byte
+// aligned. Lane L loads elements [32L, 32L + 32) of each 2048-element round into registers;
+// then, for L = 0, 1, ..., every lane adds its 32 registers in order to the running sum and
+// the running sum of lane L is broadcast to all lanes (readlane). Only lane L's additions
+// matter in step L, so the result is exactly the one-lane sequential sum, while the chain runs
+// from registers at the add latency. Elements past n are read as +0.0f, which leaves the sum
+// unchanged bit for bit because every sum taken here (squares, exponentials) is non-negative,
+// so the running sum is never -0.
+__device__ inline float hy_wave_seq_sum(const float* p, int n, int lane) {
     float s = 0.f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-        const float4 a = *reinterpret_cast<const float4*>(x + i);
-        const float4 b = *reinterpret_cast<const float4*>(x + i + 4);
-        s += a.x * a.x; s += a.y * a.y; s += a.z * a.z; s += a.w * a.w;
-        s += b.x * b.x; s += b.y * b.y; s += b.z * b.z; s += b.w * b.w;
+    for (int base = 0; base < n; base += 64 * 32) {
+        float v[32];
+        const int e0 = base + 32 * lane;
+        if (e0 + 32 <= n) {
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const float4 q = *reinterpret_cast<const float4*>(p + e0 + i);
+                v[i] = q.x;
+                v[i + 1] = q.y;
+                v[i + 2] = q.z;
+                v[i + 3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? p[e0 + i] : 0.f;
+        }
+        const int nl = min(64, (n - base + 31) / 32);
+        for (int L = 0; L < nl; L++) {
+            float t = s;
+#pragma unroll
+            for (int i = 0; i < 32; i++) t += v[i];
+            s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), L));
+        }
     }
-    for (; i < n; i++) s += x[i] * x[i];
-    return s;
-}
-
-// Sequential fp32 sum in index order.
-__device__ inline float hy_seq_sum(const float* x, int n) {
-    float s = 0.f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-        const float4 a = *reinterpret_cast<const float4*>(x + i);
-        const float4 b = *reinterpret_cast<const float4*>(x + i + 4);
-        s += a.x; s += a.y; s += a.z; s += a.w;
-        s += b.x; s += b.y; s += b.z; s += b.w;
-    }
-    for (; i < n; i++) s += x[i];
     return s;
 }

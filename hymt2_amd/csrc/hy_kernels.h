@@ -8,7 +8,7 @@
 
 namespace hy {
 
-enum Kind : int { KIND_PANEL = 0, KIND_Q4K = 1, KIND_Q6K = 2, KIND_F16 = 3, KIND_F32 = 4 };
+enum Kind : int { KIND_PANEL = 0, KIND_Q4K = 1, KIND_Q6K = 2, KIND_F16 = 3, KIND_F32 = 4, KIND_ANY = 7 };
 enum Epi : int { EPI_STORE = 0, EPI_ADD = 1 };
 enum Pro : int { PRO_NONE = 0, PRO_NORM = 1, PRO_QUANT = 2 };
 
@@ -45,11 +45,12 @@ struct MvLaunch {
     int pair;              // 1: job[0]=gate, job[1]=up share tiles; job[0].out <- silu(g)*u
     int nt;
     const HyQ8K* act;      // PRO_NONE: activations [nt][nb]
-    const float* x;        // PRO_NORM: h [nt][K]; PRO_QUANT: vector [nt][K]
+    const float* x;        // PRO_NORM: h [K]; PRO_QUANT: vector [K] (nt == 1 for both)
     const float* norm_w;   // PRO_NORM weights [K]
     float eps;
     int K;                 // input dim of all jobs
     int segs;              // 16-byte segments per thread (1, 2 or 4)
+    int threads;           // workgroup size: 256 (PRO_NONE / PRO_NORM) or 1024 (PRO_NORM / PRO_QUANT)
 };
 
 // Which (template) variant a matvec launch uses; decided on the host.
@@ -59,6 +60,7 @@ hipError_t launch_quantize_q8k(const float* x, int ldx, HyQ8K* act, int K, int n
 hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, int nt, float* xn_out,
                               HyQ8K* act_out, hipStream_t s);
 hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s);
+size_t matvec_lds_bytes(const MvLaunch& L, int pro);
 
 struct AttnArgs {
     float* q;              // [nt][qdim]
@@ -76,6 +78,26 @@ struct AttnArgs {
     float eps;
 };
 hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s);
+
+struct AttnDecodeArgs {
+    const float* q;        // [qdim] fp32 (before RoPE)
+    const float* k;        // [kvdim]
+    const float* v;        // [kvdim]
+    uint16_t* kc;          // layer base of K cache [kv_heads][ctx][hdim]
+    uint16_t* vc;
+    const float* q_norm;
+    const float* k_norm;
+    const float* rope_cos;
+    const float* rope_sin;
+    const int* pos_dev;    // optional: position read from device memory (graph replay)
+    int pos0;
+    HyQ8K* act_out;        // [qdim / 256] Q8_K blocks of the attention output
+    float* ao_out;         // optional fp32 copy of the attention output [qdim]
+    int heads, kv_heads, hdim, rope_half, ctx;
+    float eps;
+};
+hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s);
+size_t attn_decode_lds(int hdim, int ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 struct HeadArgs {

@@ -16,7 +16,7 @@ __device__ void q8k_quantize_wave(const float* src, HyQ8K* dst, int lane) {
     const float e[4] = {v4.x, v4.y, v4.z, v4.w};
     uint32_t amax = 0;
     for (int i = 0; i < 4; i++) amax = max(amax, hy_fbits(e[i]) & 0x7fffffffu);
-    for (int o = 32; o >= 1; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
+    amax = hy_wave_max_u(amax);
     uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
     if (amax == 0) {  // all-zero block -> all-zero record
         for (int i = lane; i < 576 / 4; i += 64) dw[i] = 0;
@@ -25,7 +25,7 @@ __device__ void q8k_quantize_wave(const float* src, HyQ8K* dst, int lane) {
     int first = 256;
     for (int i = 3; i >= 0; i--)
         if ((hy_fbits(e[i]) & 0x7fffffffu) == amax) first = 4 * lane + i;
-    for (int o = 32; o >= 1; o >>= 1) first = min(first, __shfl_xor(first, o));
+    first = hy_wave_min_i(first);
     const float vmax = src[first];
     const float iscale = -127.f / vmax;
     int q[4];
@@ -66,11 +66,14 @@ hipError_t launch_quantize_q8k(const float* x, int ldx, HyQ8K* act, int K, int n
 // =========================================================================== RMSNorm
 
 // x (LDS, K floats) <- x * (1/sqrtf(sum(x*x)/K + eps)) * w, the scalar RMSNorm of
-// src/model.c:719-739 with its sum taken sequentially by thread 0.
-__device__ void rmsnorm_lds(float* xs, const float* w, int K, float eps, float* scale_slot) {
-    if (threadIdx.x == 0) {
-        const float sum = hy_seq_sumsq(xs, K);
-        *scale_slot = 1.0f / sqrtf(sum / (float)K + eps);
+// src/model.c:719-739: the squares are formed in parallel (sq: K floats of LDS scratch) and
+// summed sequentially in index order by wavefront 0.
+__device__ void rmsnorm_lds(float* xs, float* sq, const float* w, int K, float eps, float* scale_slot) {
+    for (int i = threadIdx.x; i < K; i += blockDim.x) sq[i] = xs[i] * xs[i];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const float sum = hy_wave_seq_sum(sq, K, threadIdx.x);
+        if (threadIdx.x == 0) *scale_slot = 1.0f / sqrtf(sum / (float)K + eps);
     }
     __syncthreads();
     const float scale = *scale_slot;
@@ -91,11 +94,11 @@ __device__ void quantize_lds_blocks(const float* xs, HyQ8K* act, int K) {
 
 __global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float* w, float eps, int H,
                                                      float* xn_out, HyQ8K* act_out) {
-    extern __shared__ __align__(16) float xs[];
+    extern __shared__ __align__(16) float xs[];  // [H] values, [H] squares
     __shared__ float scale_slot;
     const int t = blockIdx.x;
     load_vec_lds(xs, h + (size_t)t * H, H);
-    rmsnorm_lds(xs, w, H, eps, &scale_slot);
+    rmsnorm_lds(xs, xs + H, w, H, eps, &scale_slot);
     if (xn_out)
         for (int i = threadIdx.x; i < H; i += blockDim.x) xn_out[(size_t)t * H + i] = xs[i];
     if (act_out) quantize_lds_blocks(xs, act_out + (size_t)t * (H / HY_QK), H);
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float
 
 hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, int nt, float* xn_out,
                               HyQ8K* act_out, hipStream_t s) {
-    k_rmsnorm_q8k<<<nt, 256, H * sizeof(float), s>>>(h, w, eps, H, xn_out, act_out);
+    k_rmsnorm_q8k<<<nt, 256, (2 * H) * sizeof(float), s>>>(h, w, eps, H, xn_out, act_out);
     return hipGetLastError();
 }
 
@@ -115,26 +118,34 @@ int mv_segments_per_block(int kind) { return kind == KIND_PANEL ? 4 : 8; }
 struct SegLoad {
     uint4 a;      // panel codes / Q4_K qs / Q6_K ql
     uint4 b;      // Q4_K header (d, dmin, scales) / Q6_K qh
-    float ps;     // panel scale
     int sc;       // Q6_K two int8 scales packed
     uint16_t dh;  // Q6_K f16 d
 };
 
-__device__ inline void seg_coords(int kind, int nb, int f, int& rl, int& b, int& sub) {
-    const int spb = kind == KIND_PANEL ? 4 : 8;
-    sub = f % spb;
-    const int blk = f / spb;
-    b = blk % nb;
-    rl = blk / nb;
+// Segment f of a tile -> (row in tile, block, 16-byte segment of the block). spr = nb * spb
+// segments per row, rcp = 1.0f / spr (both uniform): the float quotient is off by at most one
+// for f < 2^24 and is corrected exactly, avoiding an integer division.
+__device__ __forceinline__ void seg_coords(int spb_log2, int spr, float rcp, int f, int& rl, int& b, int& sub) {
+    int q = (int)((float)f * rcp);
+    int r = f - q * spr;
+    if (r < 0) {
+        q--;
+        r += spr;
+    } else if (r >= spr) {
+        q++;
+        r -= spr;
+    }
+    rl = q;
+    b = r >> spb_log2;
+    sub = r & ((1 << spb_log2) - 1);
 }
 
-__device__ inline SegLoad seg_load(const MvWeight& W, int row, int b, int sub) {
+__device__ __forceinline__ SegLoad seg_load(const MvWeight W, int kind, int row, int b, int sub) {
     SegLoad L;
     const size_t blk = (size_t)row * W.nb + b;
-    if (W.kind == KIND_PANEL) {
+    if (kind == KIND_PANEL) {
         L.a = *reinterpret_cast<const uint4*>(W.w + blk * 64 + sub * 16);
-        L.ps = W.ps[blk];
-    } else if (W.kind == KIND_Q4K) {
+    } else if (kind == KIND_Q4K) {
         const uint8_t* base = W.w + blk * 144;
         L.b = *reinterpret_cast<const uint4*>(base);
         L.a = *reinterpret_cast<const uint4*>(base + 16 + sub * 16);
@@ -150,17 +161,24 @@ __device__ inline SegLoad seg_load(const MvWeight& W, int row, int b, int sub) {
     return L;
 }
 
-__device__ inline int q4_scale(const uint8_t* s, int j) {  // src/kernels.c:839-842 (scale)
-    return j < 4 ? (s[j] & 63) : ((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+// 6-bit scale and min j (0..7) of a Q4_K block (src/kernels.c:839-842), from the header words
+// y, z, w (bytes 4..15) with variable shifts of fixed words, so the header stays in registers.
+__device__ __forceinline__ int q4_scale(const uint4& hdr, int j) {
+    const int lo = (int)((hdr.y >> (8 * (j & 3))) & 63u);
+    const int hi = (int)(((hdr.w >> (8 * (j & 3))) & 0xFu) | (((hdr.y >> (8 * (j & 3) + 6)) & 3u) << 4));
+    return j < 4 ? lo : hi;
 }
-__device__ inline int q4_min(const uint8_t* s, int j) {  // src/kernels.c:839-842 (min)
-    return j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+__device__ __forceinline__ int q4_min(const uint4& hdr, int j) {
+    const int lo = (int)((hdr.z >> (8 * (j & 3))) & 63u);
+    const int hi = (int)(((hdr.w >> (8 * (j & 3) + 4)) & 0xFu) | (((hdr.z >> (8 * (j & 3) + 6)) & 3u) << 4));
+    return j < 4 ? lo : hi;
 }
 
 // fp32 block term of one segment group (valid in every lane of the group). Lanes of invalid
 // segments pass zeros and still join the group reductions.
 template <int KIND>
-__device__ inline float seg_term(const MvWeight& W, const SegLoad& L, const HyQ8K* y, int sub, bool valid) {
+__device__ __forceinline__ float seg_term(int pshift, int poff, float ps, const SegLoad L, const HyQ8K* y, int sub,
+                                          bool valid) {
     if (KIND == KIND_PANEL) {
         int p = 0;
         if (valid) {
@@ -176,12 +194,11 @@ __device__ inline float seg_term(const MvWeight& W, const SegLoad& L, const HyQ8
         const int enc = hy_quad_sum(p);
         if (!valid) return 0.f;
         // src/kernels.c:576: ps * y.d * float((enc << shift) - off * sum)
-        return L.ps * y->d * (float)((enc << W.pshift) - W.poff * y->sum);
+        return ps * y->d * (float)((enc << pshift) - poff * y->sum);
     } else if (KIND == KIND_Q4K) {
         int si = 0, sm = 0;
         float d = 0.f, dmin = 0.f;
         if (valid) {
-            const uint8_t* hdr = reinterpret_cast<const uint8_t*>(&L.b);
             const int g = sub >> 1, half = sub & 1;
             const int4 qlo = *reinterpret_cast<const int4*>(y->qs + 64 * g + 16 * half);
             const int4 qhi = *reinterpret_cast<const int4*>(y->qs + 64 * g + 32 + 16 * half);
@@ -195,10 +212,10 @@ __device__ inline float seg_term(const MvWeight& W, const SegLoad& L, const HyQ8
             s1 = hy_dot4((int)((w4[1] >> 4) & 0x0F0F0F0Fu), qhi.y, s1);
             s1 = hy_dot4((int)((w4[2] >> 4) & 0x0F0F0F0Fu), qhi.z, s1);
             s1 = hy_dot4((int)((w4[3] >> 4) & 0x0F0F0F0Fu), qhi.w, s1);
-            si = q4_scale(hdr + 4, 2 * g) * s0 + q4_scale(hdr + 4, 2 * g + 1) * s1;
-            sm = q4_min(hdr + 4, sub) * (y->bsums[2 * sub] + y->bsums[2 * sub + 1]);
-            d = hy_f16((uint16_t)(hdr[0] | (hdr[1] << 8)));
-            dmin = hy_f16((uint16_t)(hdr[2] | (hdr[3] << 8)));
+            si = q4_scale(L.b, 2 * g) * s0 + q4_scale(L.b, 2 * g + 1) * s1;
+            sm = q4_min(L.b, sub) * (y->bsums[2 * sub] + y->bsums[2 * sub + 1]);
+            d = hy_f16((uint16_t)(L.b.x & 0xffffu));
+            dmin = hy_f16((uint16_t)(L.b.x >> 16));
         }
         const int sumi = hy_group_sum<8>(si);
         const int summ = hy_group_sum<8>(sm);
@@ -232,55 +249,67 @@ __device__ inline float seg_term(const MvWeight& W, const SegLoad& L, const HyQ8
     }
 }
 
-template <int SEGS, int PRO>
-__global__ __launch_bounds__(256) void k_matvec(MvLaunch L) {
+// Job fields read with constant indices only: a runtime index into the by-value kernel
+// argument would make the compiler copy the whole argument to scratch memory.
+__device__ inline MvJob mv_job(const MvLaunch& L, int j) {
+    return j == 0 ? L.job[0] : (j == 1 ? L.job[1] : L.job[2]);
+}
+__device__ inline MvWeight mv_weight(const MvLaunch& L, int j) { return j == 0 ? L.job[0].W : L.job[1].W; }
+
+// KIND is the weight kind of every job of the launch, or KIND_ANY for launches that mix kinds
+// (then selected per workgroup at run time, with every segment field live).
+template <int NT, int SEGS, int PRO, int KIND>
+__global__ __launch_bounds__(NT) void k_matvec(MvLaunch L) {
     extern __shared__ __align__(64) unsigned char smem[];
     const int tid = threadIdx.x;
     const int wg = blockIdx.x;
     int j = 0;
-    if (!L.pair)
-        while (j + 1 < L.njobs && wg >= L.job[j + 1].wg_begin) j++;
-    const MvJob& J = L.job[j];
-    const MvWeight& W = J.W;
+    if (!L.pair) {
+        if (L.njobs > 1 && wg >= L.job[1].wg_begin) j = 1;
+        if (L.njobs > 2 && wg >= L.job[2].wg_begin) j = 2;
+    }
+    const MvJob J = mv_job(L, j);
+    const MvWeight W = J.W;
+    const MvWeight W1 = L.job[1].W;  // the up weight in pair mode
+    const int kind = KIND == KIND_ANY ? W.kind : KIND;
     const int nb = W.nb;
     const int rpw = J.rows_per_wg;
     const int r0 = (wg - J.wg_begin) * rpw;
     const int rows = min(rpw, W.n - r0);
-    const int spb = W.kind == KIND_PANEL ? 4 : 8;
-    const int per_w = rows * nb * spb;           // segments of one weight in this tile
+    const int spb = kind == KIND_PANEL ? 4 : 8;
+    const int spb_log2 = kind == KIND_PANEL ? 2 : 3;
+    const int spr = nb * spb;
+    const float rcp = 1.0f / (float)spr;
+    const int per_w = rows * spr;                // segments of one weight in this tile
     const int nseg = per_w * (L.pair ? 2 : 1);
 
     // 1. issue all weight loads of this thread first: they stay in flight through the prologue
     SegLoad ld[SEGS];
-    int coord[SEGS];
 #pragma unroll
     for (int s = 0; s < SEGS; s++) {
-        const int f = tid + 256 * s;
-        coord[s] = -1;
+        const int f = tid + NT * s;
         if (f < nseg) {
-            const int which = L.pair ? f / per_w : 0;
+            const int which = L.pair ? (f >= per_w) : 0;
             int rl, b, sub;
-            seg_coords(W.kind, nb, f - which * per_w, rl, b, sub);
-            const MvWeight& Wi = L.pair ? L.job[which].W : W;
-            ld[s] = seg_load(Wi, r0 + rl, b, sub);
-            coord[s] = f;
+            seg_coords(spb_log2, spr, rcp, f - which * per_w, rl, b, sub);
+            ld[s] = seg_load(which ? W1 : W, kind, r0 + rl, b, sub);
         }
     }
 
-    // 2. activation block source (prologue builds it in LDS)
+    // 2. activation block source (the prologue builds it in LDS)
     const HyQ8K* act = L.act;
     unsigned char* terms_base = smem;
+    __shared__ float scale_slot;
     if (PRO == PRO_NORM) {
         HyQ8K* act_lds = reinterpret_cast<HyQ8K*>(smem);
         float* xs = reinterpret_cast<float*>(smem + (size_t)nb * sizeof(HyQ8K));
-        __shared__ float scale_slot;
         load_vec_lds(xs, L.x, L.K);
-        rmsnorm_lds(xs, L.norm_w, L.K, L.eps, &scale_slot);
+        rmsnorm_lds(xs, xs + L.K, L.norm_w, L.K, L.eps, &scale_slot);
         quantize_lds_blocks(xs, act_lds, L.K);
         __syncthreads();
         act = act_lds;
-        terms_base = smem + (size_t)nb * sizeof(HyQ8K) + (size_t)L.K * sizeof(float);
-    } else if (PRO == PRO_QUANT) {  // quantize the fp32 input straight from global memory
+        terms_base = smem + (size_t)nb * sizeof(HyQ8K) + (2 * (size_t)L.K) * sizeof(float);
+    } else if (PRO == PRO_QUANT) {  // quantize the fp32 input (one token) straight from global memory
         HyQ8K* act_lds = reinterpret_cast<HyQ8K*>(smem);
         quantize_lds_blocks(L.x, act_lds, L.K);
         __syncthreads();
@@ -293,68 +322,101 @@ __global__ __launch_bounds__(256) void k_matvec(MvLaunch L) {
     for (int t = 0; t < L.nt; t++) {
 #pragma unroll
         for (int s = 0; s < SEGS; s++) {
-            const int f = tid + 256 * s;
-            if (256 * s >= nseg) break;  // uniform: no thread of this WG has segment s
-            const bool valid = coord[s] >= 0;
-            int which = 0, rl = 0, b = 0, sub = f & (spb - 1);
-            if (valid) {
-                which = L.pair ? f / per_w : 0;
-                seg_coords(W.kind, nb, f - which * per_w, rl, b, sub);
+            if (NT * s < nseg) {  // uniform: some thread of this WG has segment s
+                const int f = tid + NT * s;
+                const bool valid = f < nseg;
+                int which = 0, rl = 0, b = 0, sub = f & (spb - 1);
+                if (valid) {
+                    which = L.pair ? (f >= per_w) : 0;
+                    seg_coords(spb_log2, spr, rcp, f - which * per_w, rl, b, sub);
+                }
+                const int psh = which ? W1.pshift : W.pshift, pof = which ? W1.poff : W.poff;
+                const HyQ8K* y = act + (size_t)t * nb + b;
+                float term;
+                if (kind == KIND_PANEL) {
+                    const float* psp = which ? W1.ps : W.ps;
+                    const float ps = valid && sub == 0 ? psp[(size_t)(r0 + rl) * nb + b] : 0.f;
+                    term = seg_term<KIND_PANEL>(psh, pof, ps, ld[s], y, sub, valid);
+                } else if (kind == KIND_Q4K) {
+                    term = seg_term<KIND_Q4K>(psh, pof, 0.f, ld[s], y, sub, valid);
+                } else {
+                    term = seg_term<KIND_Q6K>(psh, pof, 0.f, ld[s], y, sub, valid);
+                }
+                if (valid && sub == 0) terms[(((size_t)which * L.nt + t) * rpw + rl) * nb + b] = term;
             }
-            const MvWeight& Wi = L.pair ? L.job[which].W : W;
-            const HyQ8K* y = act + (size_t)t * nb + b;
-            float term;
-            if (W.kind == KIND_PANEL) term = seg_term<KIND_PANEL>(Wi, ld[s], y, sub, valid);
-            else if (W.kind == KIND_Q4K) term = seg_term<KIND_Q4K>(Wi, ld[s], y, sub, valid);
-            else term = seg_term<KIND_Q6K>(Wi, ld[s], y, sub, valid);
-            if (valid && sub == 0) terms[(((size_t)which * L.nt + t) * rpw + rl) * nb + b] = term;
         }
     }
     __syncthreads();
 
     // 4. sequential per-row combine in block order, then the epilogue
-    for (int i = tid; i < rows * L.nt; i += 256) {
+    for (int i = tid; i < rows * L.nt; i += NT) {
         const int t = i / rows, rl = i % rows;
         const float* tg = terms + ((size_t)t * rpw + rl) * nb;
         float acc = 0.f;
         for (int b = 0; b < nb; b++) acc += tg[b];
         const size_t o = (size_t)t * J.ldo + r0 + rl;
+        float y;
         if (L.pair) {
             const float* tu = terms + (((size_t)L.nt + t) * rpw + rl) * nb;
             float u = 0.f;
             for (int b = 0; b < nb; b++) u += tu[b];
             // SwiGLU, src/model.c:873-876: g / (1 + expf(-g)) * u
-            J.out[o] = acc / (1.0f + hy_expf(-acc)) * u;
+            y = acc / (1.0f + hy_expf(-acc)) * u;
         } else if (J.epi == EPI_ADD) {
-            J.out[o] = J.out[o] + acc;  // residual h += tmp, src/model.c:865-869
+            y = J.out[o] + acc;  // residual h += tmp, src/model.c:865-869
         } else {
-            J.out[o] = acc;
+            y = acc;
         }
+        J.out[o] = y;
     }
 }
 
-template <int PRO>
-static hipError_t launch_mv_pro(const MvLaunch& L, int grid, size_t lds, hipStream_t s) {
+template <int NT, int PRO, int KIND>
+static hipError_t launch_mv_kind(const MvLaunch& L, int grid, size_t lds, hipStream_t s) {
     switch (L.segs) {
-    case 1: k_matvec<1, PRO><<<grid, 256, lds, s>>>(L); break;
-    case 2: k_matvec<2, PRO><<<grid, 256, lds, s>>>(L); break;
-    case 4: k_matvec<4, PRO><<<grid, 256, lds, s>>>(L); break;
+    case 1: k_matvec<NT, 1, PRO, KIND><<<grid, NT, lds, s>>>(L); break;
+    case 2: k_matvec<NT, 2, PRO, KIND><<<grid, NT, lds, s>>>(L); break;
+    case 4: k_matvec<NT, 4, PRO, KIND><<<grid, NT, lds, s>>>(L); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s) {
+template <int NT, int PRO>
+static hipError_t launch_mv_nt(const MvLaunch& L, int grid, size_t lds, hipStream_t s) {
+    int kind = L.job[0].W.kind;
+    for (int j = 1; j < L.njobs; j++)
+        if (L.job[j].W.kind != kind) kind = KIND_ANY;
+    switch (kind) {
+    case KIND_PANEL: return launch_mv_kind<NT, PRO, KIND_PANEL>(L, grid, lds, s);
+    case KIND_Q4K: return launch_mv_kind<NT, PRO, KIND_Q4K>(L, grid, lds, s);
+    case KIND_Q6K: return launch_mv_kind<NT, PRO, KIND_Q6K>(L, grid, lds, s);
+    default: return launch_mv_kind<NT, PRO, KIND_ANY>(L, grid, lds, s);
+    }
+}
+
+size_t matvec_lds_bytes(const MvLaunch& L, int pro) {
     int max_rpw = 0;
     for (int j = 0; j < L.njobs; j++) max_rpw = max(max_rpw, L.job[j].rows_per_wg);
     const int nb = L.job[0].W.nb;
     size_t lds = (size_t)(L.pair ? 2 : 1) * L.nt * max_rpw * nb * sizeof(float);
-    if (pro == PRO_NORM) lds += (size_t)nb * sizeof(HyQ8K) + (size_t)L.K * sizeof(float);
+    if (pro == PRO_NORM) lds += (size_t)nb * sizeof(HyQ8K) + (2 * (size_t)L.K) * sizeof(float);
     if (pro == PRO_QUANT) lds += (size_t)nb * sizeof(HyQ8K);
+    return lds;
+}
+
+hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s) {
+    const size_t lds = matvec_lds_bytes(L, pro);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    if (pro == PRO_NONE) return launch_mv_pro<PRO_NONE>(L, grid, lds, s);
-    if (pro == PRO_NORM) return launch_mv_pro<PRO_NORM>(L, grid, lds, s);
-    return launch_mv_pro<PRO_QUANT>(L, grid, lds, s);
+    if (pro != PRO_NONE && L.nt != 1) return hipErrorInvalidValue;
+    if (L.threads == 1024) {
+        if (pro == PRO_NORM) return launch_mv_nt<1024, PRO_NORM>(L, grid, lds, s);
+        if (pro == PRO_QUANT) return launch_mv_nt<1024, PRO_QUANT>(L, grid, lds, s);
+        return hipErrorInvalidValue;
+    }
+    if (pro == PRO_NONE) return launch_mv_nt<256, PRO_NONE>(L, grid, lds, s);
+    if (pro == PRO_NORM) return launch_mv_nt<256, PRO_NORM>(L, grid, lds, s);
+    return hipErrorInvalidValue;
 }
 
 // =========================================================================== RoPE + q/k norm + KV
@@ -364,6 +426,7 @@ hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s) {
 // then for kv heads the bf16 RNE store of k and v at the absolute position (src/model.c:842-847).
 __global__ __launch_bounds__(64) void k_rope_norm_store(AttnArgs a) {
     __shared__ __align__(16) float row[256];
+    __shared__ __align__(16) float sq[256];
     __shared__ float scale_slot;
     const int t = blockIdx.x, slot = blockIdx.y, lane = threadIdx.x;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
@@ -382,9 +445,11 @@ __global__ __launch_bounds__(64) void k_rope_norm_store(AttnArgs a) {
         row[i + half] = x0 * sn[i] + x1 * c[i];
     }
     __syncthreads();
-    if (lane == 0) {
-        const float sum = hy_seq_sumsq(row, hd);
-        scale_slot = 1.0f / sqrtf(sum / (float)hd + a.eps);
+    for (int d = lane; d < hd; d += 64) sq[d] = row[d] * row[d];
+    __syncthreads();
+    {
+        const float sum = hy_wave_seq_sum(sq, hd, lane);
+        if (lane == 0) scale_slot = 1.0f / sqrtf(sum / (float)hd + a.eps);
     }
     __syncthreads();
     const float scale = scale_slot;
@@ -412,10 +477,50 @@ hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s) {
 
 // =========================================================================== attention
 
-// One workgroup per (token, q head): causal GQA attention over the bf16 cache, the
-// reference's attn_task (src/model.c:767-795) with dot_bf16_scalar (src/kernels.c:1111-1121)
-// and axpy_bf16_scalar (:1122-1124). Scores live in LDS; the softmax sum and the output
-// accumulation run sequentially over positions, as in the reference.
+__device__ __forceinline__ void bf16x8(const uint4& v, float* f) {
+    f[0] = hy_bitsf(v.x << 16); f[1] = hy_bitsf(v.x & 0xffff0000u);
+    f[2] = hy_bitsf(v.y << 16); f[3] = hy_bitsf(v.y & 0xffff0000u);
+    f[4] = hy_bitsf(v.z << 16); f[5] = hy_bitsf(v.z & 0xffff0000u);
+    f[6] = hy_bitsf(v.w << 16); f[7] = hy_bitsf(v.w & 0xffff0000u);
+}
+
+// Sequential accumulation o[i] += p[j] * bf16(V[j][d0 + i]) over j in [0, cnt), V rows of hd
+// bf16 values in LDS. Loads run 8 positions ahead of the dependent adds.
+template <int DPL>
+__device__ __forceinline__ void v_accumulate(float* o, const float* p, const uint16_t* V, int hd, int d0, int cnt) {
+    int j = 0;
+    for (; j + 8 <= cnt; j += 8) {
+        float pj[8], vf[8][DPL];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            pj[k] = p[j + k];
+            const uint16_t* vr = V + (size_t)(j + k) * hd + d0;
+            if (DPL == 2) {
+                const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vr);
+                vf[k][0] = hy_bitsf(v2 << 16);
+                vf[k][DPL - 1] = hy_bitsf(v2 & 0xffff0000u);
+            } else {
+#pragma unroll
+                for (int i = 0; i < DPL; i++) vf[k][i] = hy_bf16(vr[i]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int i = 0; i < DPL; i++) o[i] += pj[k] * vf[k][i];
+    }
+    for (; j < cnt; j++) {
+        const float pj = p[j];
+        const uint16_t* vr = V + (size_t)j * hd + d0;
+#pragma unroll
+        for (int i = 0; i < DPL; i++) o[i] += pj * hy_bf16(vr[i]);
+    }
+}
+
+// General attention (any nt): one workgroup per (token, q head), the reference's attn_task
+// (src/model.c:767-795) with dot_bf16_scalar (src/kernels.c:1111-1121) and axpy_bf16_scalar
+// (:1122-1124). Scores live in LDS; the softmax sum and the output accumulation run
+// sequentially over positions. K/V of the chunk were stored by k_rope_norm_store.
 template <int DPL>
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];
@@ -438,15 +543,16 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
         const uint16_t* kr = K + (size_t)jj * hd;
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
         for (int d = 0; d < hd; d += 8) {
-            const uint4 kv = *reinterpret_cast<const uint4*>(kr + d);
-            a0 += qs[d + 0] * hy_bitsf(kv.x << 16);
-            a1 += qs[d + 1] * hy_bitsf(kv.x & 0xffff0000u);
-            a2 += qs[d + 2] * hy_bitsf(kv.y << 16);
-            a3 += qs[d + 3] * hy_bitsf(kv.y & 0xffff0000u);
-            a0 += qs[d + 4] * hy_bitsf(kv.z << 16);
-            a1 += qs[d + 5] * hy_bitsf(kv.z & 0xffff0000u);
-            a2 += qs[d + 6] * hy_bitsf(kv.w << 16);
-            a3 += qs[d + 7] * hy_bitsf(kv.w & 0xffff0000u);
+            float kf[8];
+            bf16x8(*reinterpret_cast<const uint4*>(kr + d), kf);
+            a0 += qs[d + 0] * kf[0];
+            a1 += qs[d + 1] * kf[1];
+            a2 += qs[d + 2] * kf[2];
+            a3 += qs[d + 3] * kf[3];
+            a0 += qs[d + 4] * kf[4];
+            a1 += qs[d + 5] * kf[5];
+            a2 += qs[d + 6] * kf[6];
+            a3 += qs[d + 7] * kf[7];
         }
         const float s = ((a0 + a1) + (a2 + a3)) * scale;
         sc[jj] = s;
@@ -458,39 +564,235 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int jj = tid; jj < n; jj += 256) sc[jj] = hy_expf(sc[jj] - mx);
     __syncthreads();
-    if (tid == 0) red[4] = 1.0f / hy_seq_sum(sc, n);
+    if (wave == 0) {
+        const float sum = hy_wave_seq_sum(sc, n, lane);
+        if (lane == 0) red[4] = 1.0f / sum;
+    }
     __syncthreads();
     const float inv = red[4];
     for (int jj = tid; jj < n; jj += 256) sc[jj] = sc[jj] * inv;
     __syncthreads();
     if (wave == 0) {
         float o[DPL];
+#pragma unroll
         for (int i = 0; i < DPL; i++) o[i] = 0.f;
         const int d0 = lane * DPL;
-        for (int jj = 0; jj < n; jj++) {
-            const float p = sc[jj];
-            const uint16_t* vr = V + (size_t)jj * hd + d0;
-            if (DPL == 2) {
-                const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vr);
-                o[0] += p * hy_bitsf(v2 << 16);
-                o[DPL - 1] += p * hy_bitsf(v2 & 0xffff0000u);
-            } else {
-                for (int i = 0; i < DPL; i++) o[i] += p * hy_bf16(vr[i]);
-            }
-        }
+        v_accumulate<DPL>(o, sc, V, hd, d0, n);
         float* dst = a.ao + (size_t)t * qdim + (size_t)h * hd + d0;
+#pragma unroll
         for (int i = 0; i < DPL; i++) dst[i] = o[i];
     }
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-    const size_t lds = (256 + (size_t)a.ctx) * sizeof(float);
+    const size_t lds = (256 + (size_t)a.ctx + 4) * sizeof(float);
     if (lds > 160 * 1024 || a.heads % a.kv_heads) return hipErrorInvalidValue;
     const dim3 grid(a.nt, a.heads);
     switch (a.hdim) {
     case 64: k_attention<1><<<grid, 256, lds, s>>>(a); break;
     case 128: k_attention<2><<<grid, 256, lds, s>>>(a); break;
     case 256: k_attention<4><<<grid, 256, lds, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Single-token attention block: one workgroup per 256 query dims (256/HD heads sharing one KV
+// head). Does RoPE + per-head RMSNorm of its q heads and of the KV head's k, the bf16 rounding
+// of k and v (stored at `pos` by the group's first workgroup; the others use the same bits from
+// LDS for that position), causal attention over positions 0..pos with the reference's exact
+// operation order, and quantizes its 256 outputs to one Q8_K block for the o-projection.
+constexpr int kAttnThreads = 512;
+constexpr int kVTile = 64;
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnDecodeArgs a) {
+    constexpr int HPW = 256 / HD;     // heads per workgroup
+    constexpr int DPL = HD / 64;      // output dims per lane
+    constexpr int NW = kAttnThreads / 64;
+    extern __shared__ __align__(16) float sm[];
+    __shared__ __align__(16) float rows[HPW + 2][HD];   // q heads, k, v
+    __shared__ __align__(16) float sq[(HPW + 1) * HD];
+    __shared__ __align__(16) uint16_t kb[HD];
+    __shared__ __align__(16) uint16_t vb[HD];
+    __shared__ __align__(16) float ao[256];
+    __shared__ float scal[HPW + 1];
+    __shared__ float red[HPW][NW];
+    __shared__ float stat[HPW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h0 = blockIdx.x * HPW;
+    const int group = a.heads / a.kv_heads;
+    const int kvh = h0 / group;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
+    const int n = pos + 1;
+    const int half = a.rope_half;
+    const int npad = ((a.ctx + 3) & ~3);
+    float* sc = sm;                                                   // [HPW][npad]
+    uint16_t* vt = reinterpret_cast<uint16_t*>(sm + HPW * npad);      // [2][kVTile][HD]
+
+    // 1. q heads, k and v rows of this token
+    for (int i = tid; i < (HPW + 2) * HD; i += kAttnThreads) {
+        const int r = i / HD, d = i % HD;
+        rows[r][d] = r < HPW ? a.q[(size_t)(h0 + r) * HD + d]
+                             : (r == HPW ? a.k[(size_t)kvh * HD + d] : a.v[(size_t)kvh * HD + d]);
+    }
+    __syncthreads();
+    // 2. NeoX RoPE of q heads and k (src/model.c:754-765)
+    const float* cs = a.rope_cos + (size_t)pos * half;
+    const float* sn = a.rope_sin + (size_t)pos * half;
+    for (int i = tid; i < (HPW + 1) * half; i += kAttnThreads) {
+        const int r = i / half, jx = i % half;
+        const float x0 = rows[r][jx], x1 = rows[r][jx + half];
+        rows[r][jx] = x0 * cs[jx] - x1 * sn[jx];
+        rows[r][jx + half] = x0 * sn[jx] + x1 * cs[jx];
+    }
+    __syncthreads();
+    // 3. per-head RMSNorm (src/model.c:840-841): squares in parallel, one sequential sum per row
+    for (int i = tid; i < (HPW + 1) * HD; i += kAttnThreads) sq[i] = rows[i / HD][i % HD] * rows[i / HD][i % HD];
+    __syncthreads();
+    if (wave <= HPW) {
+        const float sum = hy_wave_seq_sum(sq + wave * HD, HD, lane);
+        if (lane == 0) scal[wave] = 1.0f / sqrtf(sum / (float)HD + a.eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < (HPW + 1) * HD; i += kAttnThreads) {
+        const int r = i / HD, d = i % HD;
+        rows[r][d] = rows[r][d] * scal[r] * (r < HPW ? a.q_norm[d] : a.k_norm[d]);
+    }
+    __syncthreads();
+    // 4. bf16 k, v of this position (src/model.c:842-847)
+    for (int d = tid; d < HD; d += kAttnThreads) {
+        kb[d] = hy_to_bf16(rows[HPW][d]);
+        vb[d] = hy_to_bf16(rows[HPW + 1][d]);
+    }
+    __syncthreads();
+    if (h0 % group == 0) {
+        const size_t off = ((size_t)kvh * a.ctx + pos) * HD;
+        for (int d = tid; d < HD; d += kAttnThreads) {
+            a.kc[off + d] = kb[d];
+            a.vc[off + d] = vb[d];
+        }
+    }
+    // 5. scores s[r][j] = dot_bf16(q_r, K_j) * (1/sqrtf(hd)), four interleaved partial sums
+    const float scale = 1.0f / sqrtf((float)HD);
+    const uint16_t* K = a.kc + (size_t)kvh * a.ctx * HD;
+    const uint16_t* V = a.vc + (size_t)kvh * a.ctx * HD;
+    float lmax[HPW];
+#pragma unroll
+    for (int r = 0; r < HPW; r++) lmax[r] = -__builtin_inff();
+    for (int jx = tid; jx < n; jx += kAttnThreads) {
+        const uint16_t* kr = jx == pos ? kb : K + (size_t)jx * HD;
+        float acc[HPW][4];
+#pragma unroll
+        for (int r = 0; r < HPW; r++) acc[r][0] = acc[r][1] = acc[r][2] = acc[r][3] = 0.f;
+        // q stays in LDS (read next to its use): hoisting all HPW*HD values would overflow VGPRs
+#pragma unroll 2
+        for (int d = 0; d < HD; d += 8) {
+            float kf[8];
+            bf16x8(*reinterpret_cast<const uint4*>(kr + d), kf);
+#pragma unroll
+            for (int r = 0; r < HPW; r++) {
+                const float* q = rows[r] + d;
+                acc[r][0] += q[0] * kf[0];
+                acc[r][1] += q[1] * kf[1];
+                acc[r][2] += q[2] * kf[2];
+                acc[r][3] += q[3] * kf[3];
+                acc[r][0] += q[4] * kf[4];
+                acc[r][1] += q[5] * kf[5];
+                acc[r][2] += q[6] * kf[6];
+                acc[r][3] += q[7] * kf[7];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < HPW; r++) {
+            const float s = ((acc[r][0] + acc[r][1]) + (acc[r][2] + acc[r][3])) * scale;
+            sc[r * npad + jx] = s;
+            lmax[r] = fmaxf(lmax[r], s);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < HPW; r++) {
+        const float m = hy_wave_max(lmax[r]);
+        if (lane == 0) red[r][wave] = m;
+    }
+    __syncthreads();
+    if (tid < HPW) {
+        float m = red[tid][0];
+        for (int w = 1; w < NW; w++) m = fmaxf(m, red[tid][w]);
+        stat[tid] = m;
+    }
+    __syncthreads();
+    // 6. softmax: exp (parallel), sum (sequential per head, src/model.c:785-789), normalise
+    for (int i = tid; i < HPW * n; i += kAttnThreads) {
+        const int r = i / n, jx = i % n;
+        sc[r * npad + jx] = hy_expf(sc[r * npad + jx] - stat[r]);
+    }
+    __syncthreads();
+    if (wave < HPW) {
+        const float sum = hy_wave_seq_sum(sc + wave * npad, n, lane);
+        if (lane == 0) stat[wave] = 1.0f / sum;
+    }
+    __syncthreads();
+    for (int i = tid; i < HPW * n; i += kAttnThreads) {
+        const int r = i / n, jx = i % n;
+        sc[r * npad + jx] = sc[r * npad + jx] * stat[r];
+    }
+    // 7. o[r][d] = sum_j p[r][j] * V[j][d] in position order: waves < HPW accumulate while the
+    // other waves stage the next tile of V rows into LDS
+    const int ntile = (n + kVTile - 1) / kVTile;
+    auto stage = [&](int tile, int buf) {
+        const int st = tid - HPW * 64, nst = kAttnThreads - HPW * 64;
+        uint16_t* dst = vt + (size_t)buf * kVTile * HD;
+        constexpr int per_row = HD / 8;
+        for (int i = st; i < kVTile * per_row; i += nst) {
+            const int jj = i / per_row, part = i % per_row, jx = tile * kVTile + jj;
+            uint4 val = make_uint4(0, 0, 0, 0);
+            if (jx < pos) val = *reinterpret_cast<const uint4*>(V + (size_t)jx * HD + part * 8);
+            else if (jx == pos) val = *reinterpret_cast<const uint4*>(vb + part * 8);
+            *reinterpret_cast<uint4*>(dst + jj * HD + part * 8) = val;
+        }
+    };
+    if (wave >= HPW) stage(0, 0);
+    __syncthreads();
+    float o[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; i++) o[i] = 0.f;
+    for (int tl = 0; tl < ntile; tl++) {
+        if (wave >= HPW) {
+            if (tl + 1 < ntile) stage(tl + 1, (tl + 1) & 1);
+        } else {
+            const int cnt = min(kVTile, n - tl * kVTile);
+            v_accumulate<DPL>(o, sc + wave * npad + tl * kVTile, vt + (size_t)(tl & 1) * kVTile * HD, HD,
+                              lane * DPL, cnt);
+        }
+        __syncthreads();
+    }
+    if (wave < HPW) {
+#pragma unroll
+        for (int i = 0; i < DPL; i++) ao[wave * HD + lane * DPL + i] = o[i];
+    }
+    __syncthreads();
+    if (a.ao_out)
+        for (int i = tid; i < 256; i += kAttnThreads) a.ao_out[(size_t)h0 * HD + i] = ao[i];
+    // 8. Q8_K block of this workgroup's 256 outputs (quantize_q8k, src/kernels.c:128-165)
+    if (tid < 64) q8k_quantize_wave(ao, a.act_out + blockIdx.x, tid);
+}
+
+size_t attn_decode_lds(int hdim, int ctx) {
+    const int hpw = 256 / hdim;
+    return (size_t)hpw * (((ctx + 3) & ~3)) * sizeof(float) + 2 * (size_t)kVTile * hdim * sizeof(uint16_t);
+}
+
+hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
+    const int hpw = 256 / a.hdim;
+    if (256 % a.hdim || (a.heads / a.kv_heads) % hpw || a.heads % hpw) return hipErrorInvalidValue;
+    const size_t lds = attn_decode_lds(a.hdim, a.ctx);
+    if (lds > 96 * 1024) return hipErrorInvalidValue;
+    const int grid = a.heads / hpw;
+    switch (a.hdim) {
+    case 64: k_attn_decode<64><<<grid, kAttnThreads, lds, s>>>(a); break;
+    case 128: k_attn_decode<128><<<grid, kAttnThreads, lds, s>>>(a); break;
+    case 256: k_attn_decode<256><<<grid, kAttnThreads, lds, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -515,13 +817,13 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long v) {
 }
 
 // One lane per vocabulary row: logits[r] = sum_j f16(W[r][j]) * xn[j] accumulated sequentially
-// (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). Rows are staged
-// through LDS 64 bytes at a time so each lane reads its own row without uncoalesced loads.
-// Optionally folds the greedy argmax (first index on ties, src/model.c:945-948) into a
-// 64-bit atomicMax key.
+// (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). Rows stream
+// through LDS 64 bytes per row per stage, two stages in flight ahead of the one being summed,
+// so each lane reads its own row without uncoalesced global loads. Optionally folds the greedy
+// argmax (first index on ties, src/model.c:945-948) into a 64-bit atomicMax key.
 template <bool F16>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
-    extern __shared__ __align__(16) float xs[];    // [K] normalized input
+    extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
     __shared__ __align__(16) uint32_t tile[2][256 * 20];
     __shared__ float scale_slot;
     const int tid = threadIdx.x;
@@ -529,34 +831,41 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     const int r0 = blockIdx.x * 256;
     const int rowb = F16 ? 2 * K : 4 * K;
     const int nstage = rowb / 64;
-    // first stage loads before the prologue
-    uint4 pre[4];
-    auto load_stage = [&](int st) {
+    // this thread's 4 x 16 bytes of every stage: rows (tid + 256 i) / 4, 16-byte part tid % 4
+    const uint8_t* src[4];
+    int dst[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int f = tid + 256 * i;
-            const int rr = f >> 2, part = f & 3;
-            const int row = min(r0 + rr, n - 1);
-            pre[i] = *reinterpret_cast<const uint4*>(a.W.w + (size_t)row * rowb + (size_t)st * 64 + part * 16);
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int f = tid + 256 * i;
-            const int rr = f >> 2, part = f & 3;
-            *reinterpret_cast<uint4*>(&tile[buf][rr * 20 + part * 4]) = pre[i];
-        }
-    };
-    load_stage(0);
+    for (int i = 0; i < 4; i++) {
+        const int f = tid + 256 * i;
+        const int rr = f >> 2, part = f & 3;
+        src[i] = a.W.w + (size_t)min(r0 + rr, n - 1) * rowb + part * 16;
+        dst[i] = rr * 20 + part * 4;
+    }
+#define HY_LOAD_STAGE(st, p0, p1, p2, p3)                                          \
+    do {                                                                           \
+        p0 = *reinterpret_cast<const uint4*>(src[0] + (size_t)(st) * 64);          \
+        p1 = *reinterpret_cast<const uint4*>(src[1] + (size_t)(st) * 64);          \
+        p2 = *reinterpret_cast<const uint4*>(src[2] + (size_t)(st) * 64);          \
+        p3 = *reinterpret_cast<const uint4*>(src[3] + (size_t)(st) * 64);          \
+    } while (0)
+#define HY_STORE_STAGE(buf, p0, p1, p2, p3)                                        \
+    do {                                                                           \
+        *reinterpret_cast<uint4*>(&tile[buf][dst[0]]) = p0;                        \
+        *reinterpret_cast<uint4*>(&tile[buf][dst[1]]) = p1;                        \
+        *reinterpret_cast<uint4*>(&tile[buf][dst[2]]) = p2;                        \
+        *reinterpret_cast<uint4*>(&tile[buf][dst[3]]) = p3;                        \
+    } while (0)
+    uint4 a0, a1, a2, a3, b0, b1, b2, b3;
+    HY_LOAD_STAGE(0, a0, a1, a2, a3);
+    if (nstage > 1) HY_LOAD_STAGE(1, b0, b1, b2, b3);
     load_vec_lds(xs, a.h, K);
-    rmsnorm_lds(xs, a.norm_w, K, a.eps, &scale_slot);
-    store_stage(0);
+    rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);
+    HY_STORE_STAGE(0, a0, a1, a2, a3);
     __syncthreads();
     float acc = 0.f;
     for (int st = 0; st < nstage; st++) {
         const int buf = st & 1;
-        if (st + 1 < nstage) load_stage(st + 1);
+        if (st + 2 < nstage) HY_LOAD_STAGE(st + 2, a0, a1, a2, a3);  // two stages ahead
         const uint32_t* tr = &tile[buf][tid * 20];
         if (F16) {
             const float* xk = xs + st * 32;
@@ -581,11 +890,15 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
                 acc += hy_bitsf(v.w) * xk[4 * q + 3];
             }
         }
-        if (st + 1 < nstage) {
-            store_stage(buf ^ 1);
-        }
+        if (st + 1 < nstage) HY_STORE_STAGE(buf ^ 1, b0, b1, b2, b3);
         __syncthreads();
+        b0 = a0;
+        b1 = a1;
+        b2 = a2;
+        b3 = a3;
     }
+#undef HY_LOAD_STAGE
+#undef HY_STORE_STAGE
     const int r = r0 + tid;
     if (r < n) a.logits[r] = acc;
     if (a.argmax_key) {
@@ -597,7 +910,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
 
 hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
     const int grid = (a.W.n + 255) / 256;
-    const size_t lds = (size_t)a.W.k * sizeof(float);
+    const size_t lds = (2 * (size_t)a.W.k) * sizeof(float);
     if (a.W.kind == KIND_F16) {
         if (a.W.k % 32) return hipErrorInvalidValue;
         k_head<true><<<grid, 256, lds, s>>>(a);

@@ -55,6 +55,10 @@ def load():
         "hymt2_hip_selftest_f16": (i, [vp, vp, vp, i]),
         "hymt2_hip_selftest_expf": (i, [vp, vp, vp, i]),
         "hymt2_hip_generate": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i, vp, C.POINTER(GenStats)]),
+        "hymt2_hip_gen_begin": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i]),
+        "hymt2_hip_gen_steps": (i, [vp, i]),
+        "hymt2_hip_gen_read": (i, [vp, vp, i, i]),
+        "hymt2_hip_head": (i, [vp, vp, vp, vp, C.c_float, vp, i, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -65,7 +69,8 @@ def load():
 
 EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops", "hymt2_hip_last_error",
            "hymt2_hip_abi_layout", "hymt2_hip_stream", "hymt2_hip_quantize_q8k", "hymt2_hip_matvec",
-           "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_generate"]
+           "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_generate", "hymt2_hip_gen_begin",
+           "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head"]
 
 
 def abi_layout() -> dict:
@@ -228,6 +233,26 @@ class FusedModel:
         if rc != n_gen:
             raise RuntimeError(f"hymt2_hip_generate failed ({rc}): {self.b.last_error()}")
         return out, st
+
+    def gen_begin(self, prompt, n_total: int):
+        if self.embd_dev is None:
+            raise ValueError("device generation needs an F16/F32 embedding table")
+        self._prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        rc = self.b.L.hymt2_hip_gen_begin(self.b.impl, C.byref(self.args), self.embd_dev, self.vocab_out,
+                                          self._prompt.ctypes.data, len(self._prompt), n_total)
+        if rc != 0:
+            raise RuntimeError(f"gen_begin failed ({rc}): {self.b.last_error()}")
+
+    def gen_steps(self, n: int):
+        rc = self.b.L.hymt2_hip_gen_steps(self.b.impl, n)
+        if rc != 0:
+            raise RuntimeError(f"gen_steps failed ({rc}): {self.b.last_error()}")
+
+    def gen_read(self, first: int, count: int) -> np.ndarray:
+        out = np.zeros(count, dtype=np.int32)
+        if self.b.L.hymt2_hip_gen_read(self.b.impl, out.ctypes.data, first, count) != count:
+            raise RuntimeError(f"gen_read failed: {self.b.last_error()}")
+        return out
 
     def close(self):
         for h in self.handles:

@@ -63,8 +63,8 @@ def panel_to_codes(pk: np.ndarray) -> np.ndarray:
     """Inverse of :func:`codes_to_panel`: panel bytes [n, nb, 64] -> codes [n, nb, 256]."""
     n, nb, _ = pk.shape
     seg = pk.reshape(n, nb, 4, 16)[:, :, SEG_OF_CHUNK, :]  # [chunk, o]
-    c = np.stack([(seg >> (2 * l)) & 3 for l in range(4)], axis=3)  # [chunk, o, l]
-    return c.transpose(0, 1, 2, 4, 3).reshape(n, nb, 256)
+    c = np.stack([(seg >> (2 * l)) & 3 for l in range(4)], axis=3)  # [chunk, l, o]
+    return c.reshape(n, nb, 256)
 
 
 def stq_codes(blocks: np.ndarray) -> np.ndarray:
@@ -81,6 +81,25 @@ def stq_codes(blocks: np.ndarray) -> np.ndarray:
     return out.reshape(n, nb, 256)
 
 
+# Panel byte position of STQ1_0 group g: chunk g>>4 goes to segment {0,2,1,3}[chunk].
+_STQ_PANEL_POS = SEG_OF_CHUNK[np.arange(64) >> 4] * 16 + (np.arange(64) & 15)
+
+
+def stq_panel(blocks: np.ndarray) -> np.ndarray:
+    """STQ1_0 blocks [n, nb, 42] -> panel bytes [n, nb, 64]: the codebook byte of group g
+    (src/kernels.c:184-188) already holds lanes 0..3 in panel bit order, so each group's byte
+    is written straight to its panel position."""
+    qs = blocks[:, :, :32]
+    slots = np.empty(blocks.shape[:2] + (64,), dtype=np.uint8)
+    slots[:, :, 0::2] = qs & 15
+    slots[:, :, 1::2] = qs >> 4
+    signs = np.unpackbits(blocks[:, :, 32:40], axis=2, bitorder="little")
+    cb = STQ_CODEBOOK[(signs.astype(np.intp) << 4) | slots]
+    out = np.empty_like(cb)
+    out[:, :, _STQ_PANEL_POS] = cb
+    return out
+
+
 def q2c_codes(blocks: np.ndarray) -> np.ndarray:
     """Q2_0C blocks [n, nb512, 130] -> codes [n, 2*nb512, 256] (value (2c-3)*d)."""
     qs = blocks[:, :, 2:]
@@ -93,9 +112,8 @@ def panel_from_blocks(gtype: int, data: np.ndarray, n: int, k: int):
     """Host-side panel repack (the reference's build_panel, src/model.c:642-660)."""
     if gtype == abi.GT_STQ1_0:
         blocks = data.reshape(n, k // QK, 42)
-        codes = stq_codes(blocks)
         ps = f16_value(blocks[:, :, 40:42].copy().view(np.uint16)[..., 0])
-        return codes_to_panel(codes), ps.astype(np.float32), 0, 1
+        return stq_panel(blocks), ps.astype(np.float32), 0, 1
     if gtype == abi.GT_Q2_0C:
         blocks = data.reshape(n, k // 512, 130)
         codes = q2c_codes(blocks)
@@ -190,7 +208,9 @@ def quantize_q6_k(x: np.ndarray) -> np.ndarray:
 
 
 def f16_matrix(g: np.random.Generator, n: int, k: int, sigma=0.02) -> np.ndarray:
-    return f16_bits(g.normal(0.0, sigma, size=(n, k))).view(np.uint8).reshape(n, 2 * k)
+    x = g.standard_normal(size=(n, k), dtype=np.float32)
+    x *= np.float32(sigma)
+    return f16_bits(x).view(np.uint8).reshape(n, 2 * k)
 
 
 # ----------------------------------------------------------------------------- weights / models

@@ -94,8 +94,9 @@ typedef struct hymt2_device_ops {
  * without the reference host (hy_device_wrap absent). */
 HYMT2_HIP_API hy_device *hy_cuda_create(const char *pref, char *info, size_t cap);
 
-/* Replaces hy_cuda_probe, src/cuda.c:18-34: writes "1" when the HIP runtime reports at least
- * one GPU, else "0"; returns the same as an int. Never initialises a device context. */
+/* Replaces hy_cuda_probe, src/cuda.c:18-34: writes "1" when the amdgpu compute node /dev/kfd
+ * is accessible, else "0"; returns the same as an int. Like the reference's probe (which only
+ * dlopens the runtime), it never initialises the GPU. */
 HYMT2_HIP_API int hy_cuda_probe(char *out, int cap);
 
 /* ---------------------------------------------------------------- extensions (no counterpart
@@ -129,20 +130,40 @@ HYMT2_HIP_API int hymt2_hip_matvec(void *impl, hy_dweight *w, const void *act_de
 HYMT2_HIP_API int hymt2_hip_selftest_f16(void *impl, const uint16_t *src_dev, float *dst_dev, int n);
 HYMT2_HIP_API int hymt2_hip_selftest_expf(void *impl, const float *src_dev, float *dst_dev, int n);
 
-/* Device-resident greedy generation (no host round trip per token): prompt ids are run one
- * position per step through the fused forward, then greedy decode continues on the device,
- * the argmax (first index on ties over the first vocab_out rows) feeding the next step's
- * embedding row. `shape` is a prepared hy_fused_args (layers, outw, norms, rope tables);
- * `embd` is the uploaded F16/F32 token embedding (the tied head is allowed). Writes n_gen ids.
- * Stop tokens are not checked. Timings come from HIP events on the context stream. */
+/* Device-resident greedy generation (no host round trip per token). Each step runs one
+ * position through the fused forward and the LM head; the argmax (first index on ties over
+ * the first vocab_out rows, src/model.c:945-948) becomes the next step's token, whose
+ * embedding row the device gathers itself. While the prompt lasts, its next id is used
+ * instead. Stop tokens are not checked. `shape` is a hy_fused_args carrying layers, outw,
+ * norms and RoPE tables (prepared on first use); `embd` is the uploaded F16/F32 token
+ * embedding (the tied head weight is allowed).
+ *   gen_begin: uploads the prompt, resets position/argmax state, embeds prompt[0]; n_total is
+ *              the number of positions the loop may fill (<= ctx).
+ *   gen_steps: enqueues n steps (asynchronous; replays of one captured graph); at most
+ *              n_total - 1 steps in all.
+ *   gen_read:  waits for the stream and copies ids[first .. first + count).
+ *   generate:  begin + n_prompt steps + (n_gen - 1) steps + read of the n_gen generated ids,
+ *              with HIP-event timings of the two phases. Returns n_gen. */
 typedef struct hymt2_gen_stats {
     double prefill_ms;  /* steps that consume prompt ids */
     double decode_ms;   /* steps that consume generated ids */
     int prefill_steps, decode_steps;
 } hymt2_gen_stats;
+HYMT2_HIP_API int hymt2_hip_gen_begin(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
+                                      const int *prompt, int n_prompt, int n_total);
+HYMT2_HIP_API int hymt2_hip_gen_steps(void *impl, int n);
+HYMT2_HIP_API int hymt2_hip_gen_read(void *impl, int *ids, int first, int count);
 HYMT2_HIP_API int hymt2_hip_generate(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
                                      const int *prompt, int n_prompt, int n_gen, int *out_ids,
                                      hymt2_gen_stats *stats);
+
+/* LM head on device pointers (enqueued on the context stream): logits[r] = row r of an
+ * uploaded F16/F32 weight . rmsnorm(h; norm_w, eps), each row summed sequentially in the
+ * reference's order (src/model.c:887-900, src/kernels.c:1279-1300). With key != NULL also
+ * folds the first-index greedy argmax over rows < n_arg into *key with atomicMax (the caller
+ * zeroes *key first; token = 0xffffffff - (key & 0xffffffff)). */
+HYMT2_HIP_API int hymt2_hip_head(void *impl, hy_dweight *w, const float *h_dev, const float *norm_dev, float eps,
+                                 float *logits_dev, int n_arg, unsigned long long *key_dev);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,11 @@ def load(path: str = REF_LIB):
         "hymt2_debug_device_matmul": (i, [C.c_char_p, C.c_uint, vp, i, i, vp, i, vp]),
         "hymt2_debug_matmul": (i, [C.c_uint, vp, i, i, vp, i, vp, i]),
         "hy_physical_cpu_count": (i, []),
+        "hymt2_debug_generate_ids": (i, [vp, C.c_char_p, vp, i]),
+        "hymt2_debug_encode": (i, [vp, C.c_char_p, C.POINTER(C.POINTER(C.c_int))]),
+        "hymt2_model_stats": (None, [vp, C.POINTER(i), C.POINTER(i), C.POINTER(C.c_double), C.POINTER(i),
+                                     C.POINTER(C.c_double)]),
+        "hymt2_isa": (C.c_char_p, []),
     }
     for name, (res, args) in sig.items():
         if hasattr(L, name):
@@ -144,6 +149,17 @@ class RefModel:
             out.append(best)
             ids.append(best)
         return np.array(out, dtype=np.int32)
+
+    def generate_text(self, text: str, max_tokens: int):
+        """The reference's own greedy loop (gen_ids via hymt2_debug_generate_ids) and its
+        timing counters (hymt2_model_stats)."""
+        ids = np.zeros(max_tokens, dtype=np.int32)
+        n = self.L.hymt2_debug_generate_ids(self.m, text.encode(), ids.ctypes.data, max_tokens)
+        pt, ct, dt = C.c_int(), C.c_int(), C.c_int()
+        pms, dms = C.c_double(), C.c_double()
+        self.L.hymt2_model_stats(self.m, C.byref(pt), C.byref(ct), C.byref(pms), C.byref(dt), C.byref(dms))
+        return ids[:max(n, 0)], dict(prefill_tokens=pt.value, cached_tokens=ct.value, prefill_ms=pms.value,
+                                     decode_tokens=dt.value, decode_ms=dms.value)
 
     def close(self):
         if self.m:
