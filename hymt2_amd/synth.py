@@ -370,4 +370,30 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
+
+
+def model_digest(model: dict) -> str:
+    """sha256 over every buffer of a synthetic model in a fixed order; golden fixtures record
+    it so a test can tell that the generator still reproduces the model they were made from."""
+    import hashlib
+    h = hashlib.sha256()
+    s = model["shape"]
+    h.update(repr(dataclasses.astuple(s)).encode())
+
+    def add(a):
+        if a is not None:
+            h.update(np.ascontiguousarray(a).tobytes())
+
+    for L in model["layers"]:
+        for nm in ("attn_norm", "ffn_norm", "q_norm", "k_norm"):
+            add(L[nm])
+        for nm in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"):
+            w = L[nm]
+            h.update(repr((w.type, w.k, w.n, w.pshift, w.poff)).encode())
+            add(w.data), add(w.pk), add(w.ps)
+    for a in (model["embd"].data, model["out_norm"], model["rope_cos"], model["rope_sin"]):
+        add(a)
+    return h.hexdigest()
+
+
 __all__ = [n for n in dir() if not n.startswith("_") and n not in ("math",)]

@@ -532,7 +532,9 @@ void oc_state_free(oc_state *s) {
 const float *oc_state_hidden(const oc_state *s) { return s->h; }
 
 /* RMSNorm, scalar branch of src/model.c:719-739. y may alias x. */
-static void rmsnorm(const float *x, const float *w, float *y, int dim, float eps) {
+/* RMSNorm, src/model.c:719-739: sequential sum of squares, one reciprocal square root, then
+ * x * scale * w per element. */
+void oc_rmsnorm(const float *x, const float *w, float *y, int dim, float eps) {
     float sum = 0.f;
     for (int i = 0; i < dim; i++) sum += x[i] * x[i];
     const float scale = 1.0f / sqrtf(sum / (float)dim + eps);
@@ -586,13 +588,16 @@ static void quantize_rows(const float *x, int nt, int k, oc_q8k *y) {
 }
 
 /* forward_batch, CPU branch of src/model.c:798-901 (the order of every operation is kept). */
-void oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits, float *logits) {
+int oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits, float *logits) {
     const oc_model *m = &s->m;
     const int H = m->hidden;
+    if (nt < 1 || nt > s->cap_nt || pos0 < 0 || pos0 + nt > m->ctx) return -1;
+    for (int t = 0; t < nt; t++)
+        if (toks[t] < 0 || toks[t] >= m->embd.n) return -1;
     for (int t = 0; t < nt; t++) oc_dequant_row(&m->embd, toks[t], s->h + (size_t)t * H);
     for (int li = 0; li < m->n_layer; li++) {
         const oc_layer *L = &m->layers[li];
-        for (int t = 0; t < nt; t++) rmsnorm(s->h + (size_t)t * H, L->attn_norm, s->xn + (size_t)t * H, H, m->eps);
+        for (int t = 0; t < nt; t++) oc_rmsnorm(s->h + (size_t)t * H, L->attn_norm, s->xn + (size_t)t * H, H, m->eps);
         quantize_rows(s->xn, nt, H, s->xq_h);
         oc_matvec(&L->wq, s->xn, s->xq_h, nt, s->q);
         oc_matvec(&L->wk, s->xn, s->xq_h, nt, s->k);
@@ -601,8 +606,8 @@ void oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits,
             float *q = s->q + (size_t)t * s->qdim, *k = s->k + (size_t)t * s->kvdim, *v = s->v + (size_t)t * s->kvdim;
             rope(s, q, m->heads, pos0 + t);
             rope(s, k, m->kv_heads, pos0 + t);
-            for (int h = 0; h < m->heads; h++) rmsnorm(q + (size_t)h * m->hdim, L->q_norm, q + (size_t)h * m->hdim, m->hdim, m->eps);
-            for (int h = 0; h < m->kv_heads; h++) rmsnorm(k + (size_t)h * m->hdim, L->k_norm, k + (size_t)h * m->hdim, m->hdim, m->eps);
+            for (int h = 0; h < m->heads; h++) oc_rmsnorm(q + (size_t)h * m->hdim, L->q_norm, q + (size_t)h * m->hdim, m->hdim, m->eps);
+            for (int h = 0; h < m->kv_heads; h++) oc_rmsnorm(k + (size_t)h * m->hdim, L->k_norm, k + (size_t)h * m->hdim, m->hdim, m->eps);
             const size_t off = ((size_t)li * m->ctx + (size_t)(pos0 + t)) * s->kvdim;
             for (int d = 0; d < s->kvdim; d++) {
                 s->kc[off + d] = oc_f32_to_bf16(k[d]);
@@ -615,7 +620,7 @@ void oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits,
         oc_matvec(&L->wo, s->ao, s->xq_q, nt, s->tmp);
         for (size_t i = 0; i < (size_t)nt * H; i++) s->h[i] += s->tmp[i];
 
-        for (int t = 0; t < nt; t++) rmsnorm(s->h + (size_t)t * H, L->ffn_norm, s->xn + (size_t)t * H, H, m->eps);
+        for (int t = 0; t < nt; t++) oc_rmsnorm(s->h + (size_t)t * H, L->ffn_norm, s->xn + (size_t)t * H, H, m->eps);
         quantize_rows(s->xn, nt, H, s->xq_h);
         oc_matvec(&L->wg, s->xn, s->xq_h, nt, s->gate);
         oc_matvec(&L->wu, s->xn, s->xq_h, nt, s->up);
@@ -629,10 +634,11 @@ void oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits,
     }
     if (want_logits) {
         const float *last = s->h + (size_t)(nt - 1) * H;
-        rmsnorm(last, m->out_norm, s->xn, H, m->eps);
+        oc_rmsnorm(last, m->out_norm, s->xn, H, m->eps);
         quantize_rows(s->xn, 1, H, s->xq_h);
         oc_matvec(&m->outw, s->xn, s->xq_h, 1, logits);
     }
+    return 0;
 }
 
 /* Greedy pick with first-index tie-break, src/model.c:945-948. */
@@ -655,14 +661,20 @@ int oc_generate(oc_state *s, const int *prompt, int n_prompt, int n_gen, int bat
     if (batch > s->cap_nt) batch = s->cap_nt;
     for (int i = 0; i < n_prompt; i += batch) {
         const int nt = n_prompt - i < batch ? n_prompt - i : batch;
-        oc_forward(s, prompt + i, nt, i, i + nt == n_prompt, logits);
+        if (oc_forward(s, prompt + i, nt, i, i + nt == n_prompt, logits)) {
+            free(logits);
+            return -1;
+        }
     }
     int pos = n_prompt;
     for (int i = 0; i < n_gen; i++) {
         const int best = oc_argmax(logits, s->m.vocab_out);
         out[i] = best;
         if (i + 1 == n_gen) break;
-        oc_forward(s, &best, 1, pos, 1, logits);
+        if (oc_forward(s, &best, 1, pos, 1, logits)) {
+            free(logits);
+            return -1;
+        }
         pos++;
     }
     free(logits);

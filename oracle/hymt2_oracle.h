@@ -95,9 +95,12 @@ void oc_axpy_bf16(float *o, const uint16_t *v, float p, int n);
 void oc_rope_tables(int ctx, int rope_half, int hdim, float base, float alpha, float *cosv, float *sinv);
 oc_state *oc_state_new(const oc_model *m);
 void oc_state_free(oc_state *s);
-void oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits, float *logits);
+/* Returns 0, or -1 (nothing computed) unless 1 <= nt <= 16, 0 <= pos0, pos0 + nt <= ctx and
+ * every token id is a row of the embedding. */
+int oc_forward(oc_state *s, const int *toks, int nt, int pos0, int want_logits, float *logits);
 const float *oc_state_hidden(const oc_state *s);
 int oc_argmax(const float *logits, int n);
+void oc_rmsnorm(const float *x, const float *w, float *y, int dim, float eps);
 /* greedy loop: prompt ids -> n_gen ids written to out; stop ids ignored. Returns n_gen. */
 int oc_generate(oc_state *s, const int *prompt, int n_prompt, int n_gen, int batch, int *out);
 void oc_set_threads(int n);

@@ -55,9 +55,9 @@ def lib():
             "oc_dot_bf16": (f, [vp, vp, i]), "oc_axpy_bf16": (None, [vp, vp, f, i]),
             "oc_rope_tables": (None, [i, i, i, f, f, vp, vp]),
             "oc_state_new": (vp, [C.POINTER(OcModel)]), "oc_state_free": (None, [vp]),
-            "oc_forward": (None, [vp, vp, i, i, i, vp]), "oc_state_hidden": (vp, [vp]),
+            "oc_forward": (i, [vp, vp, i, i, i, vp]), "oc_state_hidden": (vp, [vp]),
             "oc_argmax": (i, [vp, i]), "oc_generate": (i, [vp, vp, i, i, i, vp]),
-            "oc_set_threads": (None, [i]), "oc_expf_n": (None, [vp, vp, i]),
+            "oc_set_threads": (None, [i]), "oc_rmsnorm": (None, [vp, vp, vp, i, f]), "oc_expf_n": (None, [vp, vp, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -74,6 +74,14 @@ def expf(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().oc_expf_n(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().oc_rmsnorm(x.ctypes.data, w.ctypes.data, y.ctypes.data, x.size, eps)
     return y
 
 
@@ -167,7 +175,8 @@ class OracleModel:
     def forward(self, toks, pos0: int, want_logits=True):
         toks = np.ascontiguousarray(toks, dtype=np.int32)
         logits = np.zeros(self.vocab_n, dtype=np.float32)
-        lib().oc_forward(self.state, toks.ctypes.data, len(toks), pos0, int(want_logits), logits.ctypes.data)
+        if lib().oc_forward(self.state, toks.ctypes.data, len(toks), pos0, int(want_logits), logits.ctypes.data):
+            raise ValueError(f"oc_forward rejected nt={len(toks)} pos0={pos0} (1 <= nt <= 16, pos0 + nt <= ctx)")
         return logits
 
     def hidden(self, nt: int) -> np.ndarray:
@@ -178,5 +187,6 @@ class OracleModel:
     def generate(self, prompt, n_gen: int, batch: int = 1) -> np.ndarray:
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
-        lib().oc_generate(self.state, prompt.ctypes.data, len(prompt), n_gen, batch, out.ctypes.data)
+        if lib().oc_generate(self.state, prompt.ctypes.data, len(prompt), n_gen, batch, out.ctypes.data) < 0:
+            raise ValueError("oc_generate: prompt + generated ids exceed ctx, or an id is out of range")
         return out

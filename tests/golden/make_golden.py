@@ -1,0 +1,110 @@
+"""Writes the golden vectors under tests/golden/ from the reference library.
+
+The reference (zhangbo8418/hymt2) commits no golden vectors: its tests draw seeded random
+inputs (tests/test_kernels.c, seed 12345) and compare its SIMD paths with its scalar path. The
+fixtures here are therefore made by running the reference's own C code, compiled from its
+sources by oracle/Makefile into oracle/_ref/libhymt2_ref.so, on small seeded inputs at the
+scalar ISA (the bit-exact contract of the HIP backend):
+
+* q8k.npz         quantize_q8k (src/kernels.c:128-165) on edge-case rows
+* panel_<t>.npz   panel_repack_rows (src/kernels.c:535-561) of STQ1_0 / Q2_0C rows
+* matvec_<t>.npz  matmul_rows (src/kernels.c:1241-1329) for every weight type the backend
+                  accepts, nt = 3, plus dequant_row (src/kernels.c:1099-1109) of 4 rows
+* bf16.npz        dot_bf16 / axpy_bf16 (src/kernels.c:1111-1124) and f32_to_bf16 (:107-111)
+* model_<m>.npz   whole-model logits (hymt2_debug_logits) and 8 greedy ids of a tiny
+                  synthetic model loaded from a GGUF by the reference host (src/model.c)
+
+Inputs are stored in the fixtures (or, for the models, regenerated from a seed and checked
+against a stored digest). Run from the repository root: python tests/golden/make_golden.py
+"""
+import os
+import sys
+import tempfile
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from hymt2_amd import abi, gguf, synth  # noqa: E402
+from oracle import refbind as R  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+TYPE_NAMES = {abi.GT_STQ1_0: "stq1_0", abi.GT_Q2_0C: "q2_0c", abi.GT_Q4_K: "q4_k", abi.GT_Q6_K: "q6_k",
+              abi.GT_F16: "f16", abi.GT_F32: "f32"}
+
+# Tiny Hy-MT2-shaped models: every layer op, GQA (4 q heads over 2 kv heads), tied F16 head.
+TINY = dict(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=2, hdim=128, vocab=1000, ctx=64)
+MODEL_SEED, PROMPT_SEED, N_PROMPT, N_GREEDY = 11, 5, 20, 8
+
+
+def q8k_inputs() -> np.ndarray:
+    """Rows of 2 blocks each that hit quantize_q8k's branches."""
+    g = synth.rng(101)
+    x = synth.activations(g, 6, 512)
+    x[0, :256] = 0.0                     # all-zero block -> zeroed record
+    x[1, 5], x[1, 77] = 3.0, -3.0        # |max| tie: the first index sets the sign
+    x[1, 300], x[1, 301] = -7.0, 7.0     # tie, negative first
+    x[2, 256:] = 1e-30                   # tiny (denormal scale) block
+    x[3, 10] = 1e30                      # huge outlier
+    x[4, :] = -1.0                       # constant block
+    x[5, ::2] *= 1e-3                    # wide dynamic range
+    return x
+
+
+def main():
+    R.set_isa("scalar")
+    L = R.load()
+    g = synth.rng(202)
+
+    x = q8k_inputs()
+    np.savez(os.path.join(OUT, "q8k.npz"), x=x, q8k=R.quantize_q8k(x).view(np.uint8))
+
+    for gt, name in TYPE_NAMES.items():
+        n, k, nt = 32, 512, 3
+        w = synth.make_weight(g, gt, n, k)
+        xf = synth.activations(g, nt, k)
+        xq = R.quantize_q8k(xf)
+        out = R.matvec(w, xf, xq, nt, use_panel=True)
+        deq = R.dequant(synth.Weight(w.type, w.k, 4, w.data[:4]))
+        np.savez(os.path.join(OUT, f"matvec_{name}.npz"), type=gt, n=n, k=k, nt=nt, data=w.data, x=xf,
+                 q8k=xq.view(np.uint8), out=out, dequant4=deq)
+        if w.pk is not None:
+            pk, ps = R.panel_repack(w)
+            np.savez(os.path.join(OUT, f"panel_{name}.npz"), type=gt, n=n, k=k, data=w.data, pk=pk, ps=ps)
+
+    n = 300
+    q = synth.activations(g, 1, n)[0]
+    kv = (synth.activations(g, 1, n)[0].view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits
+    o = synth.activations(g, 1, n)[0]
+    o2 = o.copy()
+    L.axpy_bf16(o2.ctypes.data, kv.ctypes.data, np.float32(0.37), n)
+    vals = np.concatenate([synth.activations(g, 1, 256)[0],
+                           np.array([0.0, -0.0, 1.0, 65504.0, 1e-40, -3.4e38, 1.00390625, 1.01171875],
+                                    dtype=np.float32)])
+    np.savez(os.path.join(OUT, "bf16.npz"), q=q, kv=kv, dot=np.float32(L.dot_bf16(q.ctypes.data, kv.ctypes.data, n)),
+             o=o, p=np.float32(0.37), axpy=o2, vals=vals,
+             to_bf16=np.array([L.f32_to_bf16(float(v)) for v in vals], dtype=np.uint16))
+
+    os.environ.update(HYMT2_DEVICE="cpu", HYMT2_ISA="scalar", HYMT2_REPACK="1", HYMT2_PREFAULT="0")
+    with tempfile.TemporaryDirectory() as td:
+        for mode in ("stq", "q2", "q4km"):
+            shape = synth.ModelShape(**TINY)
+            model = synth.make_model(shape, mode=mode, seed=MODEL_SEED)
+            path = os.path.join(td, f"tiny_{mode}.gguf")
+            gguf.write_model(path, model)
+            rm = R.RefModel(path, threads=1, ctx=shape.ctx)
+            prompt = synth.rand_prompt(synth.rng(PROMPT_SEED), N_PROMPT, shape.vocab)
+            logits = rm.logits(prompt)
+            ids = rm.greedy(prompt, N_GREEDY)
+            rm.close()
+            np.savez(os.path.join(OUT, f"model_{mode}.npz"), mode=mode, seed=MODEL_SEED,
+                     digest=synth.model_digest(model), prompt=prompt, logits=logits, greedy=ids,
+                     **{f"shape_{k}": v for k, v in TINY.items()})
+            print(mode, "greedy", ids)
+    print("golden vectors written to", OUT)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,48 @@
+"""The drop-in: the reference's own C host, unchanged, with libhymt2_hip.so linked in place of
+its CUDA backend (oracle/Makefile `host`), selects the HIP device through hy_cuda_create
+(HYMT2_DEVICE=cuda, src/model.c:424-450), uploads every weight, enables the fused path and
+produces the same logits and greedy ids, bit for bit, as the same host on the CPU at the scalar
+ISA. Each leg runs in a fresh process (the backend's weak reference to the host's
+hy_device_wrap binds when the host library loads it)."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from hymt2_amd import gguf, synth
+from oracle import refbind
+
+pytestmark = pytest.mark.gpu
+
+RUNNER = os.path.join(ROOT, "tests", "helpers", "dropin_run.py")
+
+
+def run_leg(env_extra, path, ctx, out, prompt, text, max_tokens):
+    env = dict(os.environ, HYMT2_ISA="scalar", HYMT2_REPACK="1", HYMT2_PREFAULT="0", HYMT2_THREADS="4",
+               HYMT2_VERBOSE="1", **env_extra)
+    r = subprocess.run([sys.executable, RUNNER, path, str(ctx), out, ",".join(str(int(t)) for t in prompt), text,
+                        str(max_tokens)], capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    return np.load(out, allow_pickle=False), r.stderr
+
+
+@pytest.mark.parametrize("mode", ["stq", "q2", "q4km"])
+def test_reference_host_on_hip_backend(tmp_path, mode):
+    if not (refbind.available(refbind.HOST_LIB) and refbind.available(refbind.REF_LIB)):
+        pytest.skip("oracle/_ref host libraries not built (needs the reference tree at build time)")
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=2, hdim=128, vocab=1000, ctx=128)
+    model = synth.make_model(shape, mode=mode, seed=51)
+    path = str(tmp_path / f"m_{mode}.gguf")
+    gguf.write_model(path, model)
+    prompt = synth.rand_prompt(synth.rng(52), 21, shape.vocab)
+    text = "t5 t17 t300 t42"
+    gpu, log = run_leg({"HYMT2_DEVICE": "cuda"}, path, shape.ctx, str(tmp_path / "gpu.npz"), prompt, text, 24)
+    cpu, _ = run_leg({"HYMT2_DEVICE": "cpu-ref"}, path, shape.ctx, str(tmp_path / "cpu.npz"), prompt, text, 24)
+    assert "gpu=hip+fused" in str(gpu["info"]), str(gpu["info"]) + log[-2000:]
+    assert "gpu=off" in str(cpu["info"])
+    for key in ("logits", "stepwise"):
+        assert np.array_equal(gpu[key].view(np.uint32), cpu[key].view(np.uint32)), key
+    assert len(cpu["ids"]) > 0 and np.array_equal(gpu["ids"], cpu["ids"])

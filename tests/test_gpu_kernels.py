@@ -1,0 +1,230 @@
+"""HIP kernels against the oracle and the golden vectors, bit for bit, through the C-ABI.
+
+Covers the scalar conversions the kernels share (f16 -> f32 over every input, expf), Q8_K
+activation quantization (src/kernels.c:128-165) with its edge cases, the panel / Q4_K / Q6_K
+matvec (src/kernels.c:565-581, :808-877) at the layer shapes of BASELINE configs 0-2 and at
+ragged row counts, the per-op `matmul` vtable entry (src/cuda.c:258-279 semantics), the F16
+LM head with its fused argmax (src/kernels.c:1279-1289, src/model.c:945-948) and the entry
+points' argument checks."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+from hymt2_amd import abi, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def empty_f32(n):
+    import torch
+    return torch.zeros(n, dtype=torch.float32, device="cuda:0")
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def q8k_dev(backend, x):
+    """Quantize fp32 rows on the device; returns (device act tensor, host copy as Q8K records)."""
+    import torch
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nt, k = x.shape
+    act = torch.zeros(nt * (k // 256) * abi.Q8K_BYTES, dtype=torch.uint8, device="cuda:0")
+    xd = dev(x)
+    backend.quantize_q8k(xd.data_ptr(), act.data_ptr(), k, nt)
+    sync()
+    return act, act.cpu().numpy().view(O.Q8K_DTYPE)
+
+
+# ----------------------------------------------------------------------------- conversions
+
+def test_f16_to_f32_all_inputs(backend):
+    src = np.arange(65536, dtype=np.uint16)
+    out = empty_f32(65536)
+    assert backend.L.hymt2_hip_selftest_f16(backend.impl, dev(src.view(np.int16)).data_ptr(), out.data_ptr(), 65536) == 0
+    sync()
+    got = out.cpu().numpy()
+    ref = np.array([O.lib().oc_f16_to_f32(int(h)) for h in src], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan) and np.array_equal(bits(got)[~nan], bits(ref)[~nan])
+
+
+def test_expf_matches_libm(backend):
+    g = np.random.default_rng(0)
+    x = np.concatenate([g.uniform(-104, 89, 1 << 21), g.uniform(-1, 1, 1 << 19), g.uniform(-20, 0, 1 << 19),
+                        [0.0, -0.0, 88.72, 88.8, -103.9, -104.0, -200.0, 1e-30, -1e-30, np.inf, -np.inf]]
+                       ).astype(np.float32)
+    out = empty_f32(len(x))
+    assert backend.L.hymt2_hip_selftest_expf(backend.impl, dev(x).data_ptr(), out.data_ptr(), len(x)) == 0
+    sync()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(O.expf(x)))
+
+
+# ----------------------------------------------------------------------------- Q8_K
+
+def test_q8k_golden(backend):
+    f = np.load(os.path.join(GOLDEN, "q8k.npz"), allow_pickle=False)
+    _, got = q8k_dev(backend, f["x"])
+    assert np.array_equal(got.view(np.uint8).ravel(), f["q8k"].ravel())
+
+
+@pytest.mark.parametrize("k,nt", [(256, 1), (2048, 1), (2048, 16), (6144, 3), (6144, 16)])
+def test_q8k_vs_oracle(backend, k, nt):
+    g = synth.rng(k + nt)
+    x = synth.activations(g, nt, k)
+    x[0, :256] = 0.0
+    x[-1, 11], x[-1, 40] = -4.0, 4.0
+    x[nt // 2, 300 % k] = 1e25
+    _, got = q8k_dev(backend, x)
+    assert got.tobytes() == O.quantize_q8k(x).tobytes()
+
+
+# ----------------------------------------------------------------------------- matvec
+
+def run_matvec(backend, w, x):
+    """Device quantize + matvec of an uploaded weight; returns out [nt, n] and the act."""
+    nt = x.shape[0]
+    h = backend.upload(w)
+    try:
+        act, xq = q8k_dev(backend, x)
+        out = empty_f32(nt * w.n)
+        backend.matvec(h, act.data_ptr(), out.data_ptr(), nt)
+        sync()
+        return out.cpu().numpy().reshape(nt, w.n), xq
+    finally:
+        backend.release(h)
+
+
+@pytest.mark.parametrize("name", ["stq1_0", "q2_0c", "q4_k", "q6_k"])
+def test_matvec_golden(backend, name):
+    f = np.load(os.path.join(GOLDEN, f"matvec_{name}.npz"), allow_pickle=False)
+    w = synth.Weight(int(f["type"]), int(f["k"]), int(f["n"]), f["data"]).with_panel()
+    out, xq = run_matvec(backend, w, f["x"])
+    assert np.array_equal(xq.view(np.uint8).ravel(), f["q8k"].ravel())
+    assert np.array_equal(bits(out), bits(f["out"]))
+
+
+SHAPES = [
+    (abi.GT_STQ1_0, 12288, 2048),  # config 0: gate+up panel
+    (abi.GT_STQ1_0, 3072, 2048),   # qkv
+    (abi.GT_STQ1_0, 2048, 6144),   # down
+    (abi.GT_Q2_0C, 2048, 2048),    # config 1: o
+    (abi.GT_Q2_0C, 2048, 6144),
+    (abi.GT_Q4_K, 3072, 2048),     # config 2: q/k
+    (abi.GT_Q6_K, 2048, 6144),     # config 2: down
+    (abi.GT_Q4_K, 37, 1536),       # ragged rows, odd block count
+    (abi.GT_Q6_K, 65, 512),
+    (abi.GT_STQ1_0, 1, 256),       # one row, one block
+    (abi.GT_Q2_0C, 129, 512),
+]
+
+
+@pytest.mark.parametrize("gt,n,k", SHAPES)
+def test_matvec_vs_oracle(backend, gt, n, k):
+    g = synth.rng(gt * 7 + n + k)
+    w = synth.make_weight(g, gt, n, k)
+    for nt in (1, 2, 5, 16):
+        x = synth.activations(g, nt, k)
+        out, xq = run_matvec(backend, w, x)
+        assert np.array_equal(bits(out), bits(O.matvec(w, x, xq, nt))), f"nt={nt}"
+
+
+def test_config0_uniform_codes_panel(backend):
+    """Config 0's panel (i.i.d. uniform codes 0..2, fp32 scales U(0.005, 0.05)) handed straight
+    to upload as pk/ps, as the reference host does after its load-time repack."""
+    g = synth.rng(0xC0DE0)
+    n, k = 12288, 2048
+    pk, ps = synth.panel_uniform_codes(g, n, k)
+    w = synth.Weight(abi.GT_STQ1_0, k, n, np.zeros((n, abi.row_bytes(abi.GT_STQ1_0, k)), np.uint8), pk, ps, 0, 1)
+    x = synth.activations(g, 1, k)
+    out, xq = run_matvec(backend, w, x)
+    assert np.array_equal(bits(out), bits(O.matvec(w, x, xq, 1)))
+
+
+def test_per_op_matmul_groups(backend):
+    """matmul() with q/k/v sharing one Q8_K activation (src/model.c:697-713 groups)."""
+    g = synth.rng(77)
+    ws = [synth.make_weight(g, abi.GT_Q4_K, 256, 2048), synth.make_weight(g, abi.GT_Q4_K, 128, 2048),
+          synth.make_weight(g, abi.GT_Q6_K, 128, 2048)]
+    hs = [backend.upload(w) for w in ws]
+    try:
+        for nt in (1, 7, 16):
+            x = synth.activations(g, nt, 2048)
+            xq = O.quantize_q8k(x)
+            outs = backend.matmul(hs, [w.n for w in ws], xq, nt)
+            for w, o in zip(ws, outs):
+                assert np.array_equal(bits(o), bits(O.matvec(w, x, xq, nt)))
+    finally:
+        for h in hs:
+            backend.release(h)
+
+
+# ----------------------------------------------------------------------------- LM head
+
+@pytest.mark.parametrize("gt,n", [(abi.GT_F16, 120818), (abi.GT_F16, 1000), (abi.GT_F32, 777)])
+def test_head_and_argmax(backend, gt, n):
+    import torch
+    g = synth.rng(n)
+    k = 2048
+    w = synth.make_weight(g, gt, n, k, sigma=0.02)
+    hvec = synth.activations(g, 1, k)[0]
+    nw = g.uniform(0.9, 1.1, k).astype(np.float32)
+    eps = 1e-5
+    h = backend.upload(w)
+    try:
+        logits = empty_f32(n)
+        key = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+        n_arg = n - 3
+        assert backend.L.hymt2_hip_head(backend.impl, h, dev(hvec).data_ptr(), dev(nw).data_ptr(), C.c_float(eps),
+                                        logits.data_ptr(), n_arg, key.data_ptr()) == 0
+        sync()
+        got = logits.cpu().numpy()
+        xn = O.rmsnorm(hvec, nw, eps)
+        ref = O.matvec(w, xn[None, :], None, 1)[0]
+        assert np.array_equal(bits(got), bits(ref))
+        tok = 0xFFFFFFFF - (int(key.cpu().numpy()[0]) & 0xFFFFFFFF)
+        assert tok == int(np.argmax(ref[:n_arg]))
+    finally:
+        backend.release(h)
+
+
+# ----------------------------------------------------------------------------- argument checks
+
+def test_entry_points_reject_bad_arguments(backend):
+    L = backend.L
+    g = synth.rng(5)
+    w = synth.make_weight(g, abi.GT_STQ1_0, 64, 512)
+    h = backend.upload(w)
+    try:
+        act, _ = q8k_dev(backend, synth.activations(g, 1, 512))
+        out = empty_f32(64 * 17)
+        assert L.hymt2_hip_matvec(backend.impl, h, act.data_ptr(), out.data_ptr(), 0) < 0
+        assert L.hymt2_hip_matvec(backend.impl, h, act.data_ptr(), out.data_ptr(), 17) < 0
+        assert L.hymt2_hip_quantize_q8k(backend.impl, out.data_ptr(), act.data_ptr(), 300, 1) < 0
+        xq = O.quantize_q8k(synth.activations(g, 1, 512))
+        ws = (C.c_void_p * 1)(h)
+        outs = (C.c_void_p * 1)(np.zeros(64, np.float32).ctypes.data)
+        assert not backend.ops.matmul(backend.impl, ws, outs, 1, xq.ctypes.data, 17)
+        # an unsupported tensor type is refused at upload (NULL), as the reference backend does
+        bad = abi.WeightT(w.data.ctypes.data, abi.GT_Q8_0, 512, 64, abi.row_bytes(abi.GT_Q8_0, 512), None, None, 0, 0,
+                          None)
+        assert not backend.ops.upload(backend.impl, C.byref(bad))
+        # the context is still usable afterwards
+        backend.matvec(h, act.data_ptr(), out.data_ptr(), 1)
+        sync()
+    finally:
+        backend.release(h)

@@ -1,0 +1,135 @@
+"""The fused token loop on the GPU against the golden vectors and the oracle, bit for bit.
+
+Each model runs through the backend's hy_device_ops vtable exactly as the reference host
+drives it (upload, fused_prepare, fused_forward per chunk of <= 16 tokens with the host
+embedding; src/model.c:384-406, :325-381, :798-909), and through the device-resident greedy
+loop (hymt2_hip_generate / gen_begin / gen_steps). Logits are compared as bit patterns and
+greedy ids exactly."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+from hymt2_amd import lib, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def golden_model(mode):
+    f = np.load(os.path.join(GOLDEN, f"model_{mode}.npz"), allow_pickle=False)
+    shape = synth.ModelShape(**{k[6:]: int(f[k]) for k in f.files if k.startswith("shape_")})
+    model = synth.make_model(shape, mode=str(f["mode"]), seed=int(f["seed"]))
+    assert synth.model_digest(model) == str(f["digest"])
+    return f, model
+
+
+@pytest.mark.parametrize("mode", ["stq", "q2", "q4km"])
+def test_golden_models(backend, mode):
+    f, model = golden_model(mode)
+    fm = lib.FusedModel(backend, model)
+    try:
+        prompt = f["prompt"]
+        lg = fm.prefill(list(prompt), batch=8)  # the reference's scalar-ISA chunking
+        assert np.array_equal(bits(lg), bits(f["logits"]))
+        n = len(f["greedy"])
+        assert np.array_equal(fm.generate_host(prompt, n, batch=8), f["greedy"])
+        ids, st = fm.generate_device(prompt, n)
+        assert np.array_equal(ids, f["greedy"])
+        assert st.prefill_steps == len(prompt) and st.decode_steps == n - 1
+    finally:
+        fm.close()
+
+
+SHAPE = synth.ModelShape(n_layer=3, hidden=512, ffn=1536, heads=8, kv_heads=2, hdim=64, vocab=900, ctx=320)
+
+
+@pytest.mark.parametrize("mode", ["stq", "q2", "q4km"])
+def test_chunking_and_prefix_reuse(backend, mode):
+    """Chunks of 16, 5 and 1 tokens all give the oracle's logits; re-running a suffix over a warm
+    cache (positions overwritten) equals a cold run (tests/test_model.py:369-374, :394-399)."""
+    model = synth.make_model(SHAPE, mode=mode, seed=41)
+    prompt = synth.rand_prompt(synth.rng(42), 37, SHAPE.vocab)
+    om = O.OracleModel(model, threads=8)
+    ref = None
+    for i in range(0, len(prompt), 16):
+        c = prompt[i:i + 16]
+        ref = om.forward(c, i, want_logits=(i + len(c) == len(prompt)))
+    fm = lib.FusedModel(backend, model)
+    try:
+        for batch in (16, 5, 1):
+            assert np.array_equal(bits(fm.prefill(list(prompt), batch=batch)), bits(ref)), f"batch={batch}"
+        fm.forward([1, 2, 3, 4], 30, False)           # scribble over positions 30..33
+        lg = fm.forward(list(prompt[30:]), 30, True)  # then recompute them from the warm prefix
+        assert np.array_equal(bits(lg), bits(ref))
+    finally:
+        fm.close()
+
+
+@pytest.mark.parametrize("mode", ["stq", "q4km"])
+def test_long_greedy_device_vs_oracle(backend, mode):
+    """A 300-position greedy run (attention past several 64-key tiles; softmax over > 256 keys)."""
+    model = synth.make_model(SHAPE, mode=mode, seed=43)
+    prompt = synth.rand_prompt(synth.rng(44), 40, SHAPE.vocab)
+    n_gen = SHAPE.ctx - len(prompt)
+    want = O.OracleModel(model, threads=8).generate(prompt, n_gen, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        ids, _ = fm.generate_device(prompt, n_gen)
+        assert np.array_equal(ids, want)
+        # the step API: begin, steps in pieces, read back
+        fm.gen_begin(prompt, len(prompt) + 20)
+        fm.gen_steps(len(prompt))
+        fm.gen_steps(19)
+        assert np.array_equal(fm.gen_read(len(prompt), 20), want[:20])
+    finally:
+        fm.close()
+
+
+def test_generate_rejects_overlong_runs(backend):
+    model = synth.make_model(synth.ModelShape(n_layer=1, hidden=256, ffn=512, heads=2, kv_heads=1, hdim=128,
+                                              vocab=300, ctx=64), mode="stq", seed=45)
+    fm = lib.FusedModel(backend, model)
+    try:
+        prompt = synth.rand_prompt(synth.rng(46), 10, 300)
+        with pytest.raises(RuntimeError):
+            fm.gen_begin(prompt, 65)      # more positions than ctx
+        fm.gen_begin(prompt, 12)
+        fm.gen_steps(11)
+        with pytest.raises(RuntimeError):
+            fm.gen_steps(1)               # past n_total - 1 steps
+        a = fm.args
+        a.nt, a.pos0, a.want_logits, a.h, a.logits = 17, 0, 1, fm.h.ctypes.data, fm.logits.ctypes.data
+        assert not fm.b.ops.fused_forward(fm.b.impl, ctypes.byref(a))  # nt > 16 (src/cuda.c:341)
+        a.nt, a.pos0 = 2, 63
+        assert not fm.b.ops.fused_forward(fm.b.impl, ctypes.byref(a))  # past ctx
+        # still usable
+        ids, _ = fm.generate_device(prompt, 5)
+        assert np.array_equal(ids, O.OracleModel(model, threads=4).generate(prompt, 5, batch=16))
+    finally:
+        fm.close()
+
+
+@pytest.mark.parametrize("mode", ["stq", "q2"])
+def test_full_size_model_short_run(backend, mode):
+    """Hy-MT2-1.8B shapes (BASELINE configs 3 and 4): 32 layers, hidden 2048, ffn 6144, 16/4 heads,
+    vocab 120818, tied F16 head. 12 prompt ids then 4 greedy ids, logits and ids vs the oracle."""
+    shape = synth.ModelShape(ctx=64)
+    model = synth.make_model(shape, mode=mode, seed=3)
+    prompt = synth.rand_prompt(synth.rng(1234), 12, shape.vocab)
+    om = O.OracleModel(model, threads=16)
+    ref = om.forward(prompt, 0, True)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.forward(list(prompt), 0, True)), bits(ref))
+        want = O.OracleModel(model, threads=16).generate(prompt, 4, batch=16)
+        ids, _ = fm.generate_device(prompt, 4)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
