@@ -44,9 +44,62 @@ def build_model(ctx: int, seed: int = 3):
     return shape, model
 
 
+def _timed_launches(stream, launch, n):
+    """Average seconds per launch of `launch(i)` over i = 0..n-1, from HIP events recorded on
+    the backend stream (the stream the kernels run on)."""
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        launch(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / n / 1000.0
+
+
+def ffn_in_roofline(model, b, copies: int = 64, passes: int = 3):
+    """The decode step's dominant kernel: the fused feed-forward input (RMSNorm + Q8_K prologue,
+    gate and up STQ1_0 panel matvecs, SwiGLU epilogue; 2 x 6144 x 2048 weights), launched
+    standalone through hymt2_hip_ffn_in over `copies` distinct device copies of layer 0's gate/up
+    weights (64 x 6.7 MB = 430 MB, more than the 256 MB Infinity Cache, so every launch streams
+    its weights from HBM as in the decode loop). Algorithmic bytes per launch = panel codes +
+    panel scales of both weights + h + the norm weights + the SwiGLU output."""
+    import torch
+    s = model["shape"]
+    L0 = model["layers"][0]
+    wg, wu = L0["wg"], L0["wu"]
+    handles = [(b.upload(wg), b.upload(wu)) for _ in range(copies)]
+    stream = torch.cuda.ExternalStream(b.stream)
+    h = torch.randn(s.hidden, device="cuda", dtype=torch.float32)
+    nw = torch.from_numpy(L0["ffn_norm"]).to("cuda")
+    out = torch.empty(wg.n, device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    def launch(i):
+        g, u = handles[i % copies]
+        if b.L.hymt2_hip_ffn_in(b.impl, g, u, h.data_ptr(), nw.data_ptr(), C.c_float(s.eps), out.data_ptr()) != 0:
+            raise RuntimeError("hymt2_hip_ffn_in failed: " + b.last_error())
+
+    for i in range(copies):
+        launch(i)
+    avg_s = _timed_launches(stream, launch, copies * passes)
+    for g, u in handles:
+        b.release(g)
+        b.release(u)
+    algo = wg.nbytes_device() + wu.nbytes_device() + 2 * s.hidden * 4 + wg.n * 4
+    return dict(bound="hbm", achieved=round(algo / avg_s / 1e9, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(algo / avg_s / 1e9 / HBM_PEAK_GBS, 4), traffic=_pmc_traffic("ffn_in"),
+                kernel="k_matvec<1024,4,PRO_NORM,PANEL> pair mode (hymt2_hip_ffn_in): fused FFN input of one "
+                       "decode token, gate+up 2x6144x2048 STQ1_0 panel",
+                avg_us=round(avg_s * 1e6, 2), bytes_per_launch=algo,
+                timing=f"HIP events on the backend stream over {copies * passes} launches rotating {copies} "
+                       f"weight copies")
+
+
 def head_roofline(fm, b, reps: int = 20):
-    """Average duration of the LM-head kernel (F16 120818x2048 + argmax) from HIP events on
-    the backend stream; algorithmic bytes = weight rows + input vector + norm + logits."""
+    """LM head (F16 120818 x 2048 + argmax) from HIP events on the backend stream; algorithmic
+    bytes = weight rows + input vector + norm + logits. Its 495 MB of weights exceed the
+    Infinity Cache by themselves."""
     import torch
     s = fm.shape
     stream = torch.cuda.ExternalStream(b.stream)
@@ -56,27 +109,68 @@ def head_roofline(fm, b, reps: int = 20):
     key = torch.zeros(1, device="cuda", dtype=torch.int64)
     torch.cuda.synchronize()
 
-    def launch():
+    def launch(_):
         rc = b.L.hymt2_hip_head(b.impl, fm.outw, h.data_ptr(), nw.data_ptr(), C.c_float(s.eps), logits.data_ptr(),
                                 fm.vocab_out, key.data_ptr())
         if rc != 0:
             raise RuntimeError("hymt2_hip_head failed: " + b.last_error())
 
-    for _ in range(3):
-        launch()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        launch()
-    e1.record(stream)
-    e1.synchronize()
-    avg_s = e0.elapsed_time(e1) / reps / 1000.0
+    for i in range(3):
+        launch(i)
+    avg_s = _timed_launches(stream, launch, reps)
     w = fm.model["outw"]
     algo = w.n * w.k * 2 + 2 * s.hidden * 4 + w.n * 4
-    return dict(bound="hbm", achieved=round(algo / avg_s / 1e9, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(algo / avg_s / 1e9 / HBM_PEAK_GBS, 4), traffic=None,
-                kernel="k_head<true> (F16 LM head 120818x2048 + argmax)", avg_us=round(avg_s * 1e6, 2),
-                bytes_per_launch=algo)
+    return dict(achieved=round(algo / avg_s / 1e9, 1), frac=round(algo / avg_s / 1e9 / HBM_PEAK_GBS, 4),
+                avg_us=round(avg_s * 1e6, 2), bytes_per_launch=algo,
+                kernel="k_head<F16> (LM head 120818x2048 + argmax)")
+
+
+def host_loop_rate(fm, prompt, n_tokens: int):
+    """Decode rate of the reference host's own loop over the drop-in boundary: one
+    fused_forward per token with the host embedding in (8 KB H2D), the 120818 logits out (483 KB
+    D2H) and the argmax on the host (src/model.c:914-958). PCIe-inclusive, for comparison with the
+    device-resident loop that `value` measures."""
+    import numpy as np
+    logits = fm.prefill(list(prompt), batch=16)
+    pos = len(prompt)
+    t0 = time.perf_counter()
+    for _ in range(n_tokens):
+        best = int(np.argmax(logits[:fm.vocab_out]))
+        logits = fm.forward([best], pos, True)
+        pos += 1
+    dt = time.perf_counter() - t0
+    return dict(value=round(n_tokens / dt, 2), unit="tok/s", tokens=n_tokens,
+                note="hy_device_ops.fused_forward per token with logits D2H and host argmax")
+
+
+def _pmc_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (profiles/traffic.json, scaled by the same counters on a copy kernel of known size), or
+    None when not measured."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get(kernel, {}).get("hbm_bytes_per_launch")
+
+
+def kernels_only(args):
+    """Standalone launches for counter collection: the dominant kernel over rotating weight
+    copies, then a plain copy kernel of known size (256 MiB read + 256 MiB written) that
+    calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    from hymt2_amd import lib
+    shape, model = build_model(64, args.seed)
+    b = lib.Backend()
+    roof = ffn_in_roofline(model, b, copies=64, passes=1)
+    log(f"ffn_in: {roof['avg_us']} us, {roof['achieved']} GB/s")
+    src = torch.randn(64 << 20, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)  # the calibration kernel: 256 MiB in, 256 MiB out
+    torch.cuda.synchronize()
+    log("calibration copy: torch.neg over 67108864 fp32 (268435456 B read, 268435456 B written)")
+    b.close()
 
 
 def cpu_baseline(model, shape, n_tokens: int):
@@ -118,6 +212,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the standalone kernel launches used for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the Hy-MT2 token loop at batch 1 runs on a single MI355X "
@@ -126,8 +222,11 @@ def main():
     import torch
     from hymt2_amd import lib, synth
 
+    if args.kernels_only:
+        kernels_only(args)
+        return
     n_total = args.prompt + args.warmup + args.steps + 1  # steps fill positions 1..n_total-1
-    ctx = (n_total + 63) // 64 * 64
+    ctx = (max(n_total, args.prompt + 33) + 63) // 64 * 64  # also room for the host-loop sample
     t = time.time()
     shape, model = build_model(ctx, args.seed)
     log(f"model built in {time.time() - t:.1f} s")
@@ -151,8 +250,12 @@ def main():
     tok_s = args.steps / dt
     wb = synth.model_weight_bytes(model)
     log(f"decode: {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token), {len(set(ids.tolist()))} distinct ids")
-    roof = head_roofline(fm, b)
-    log(f"head kernel: {roof['avg_us']} us, {roof['achieved']} GB/s")
+    host = host_loop_rate(fm, prompt, 32)
+    log(f"host-driven loop (fused_forward + logits D2H + host argmax): {host['value']} tok/s")
+    roof = ffn_in_roofline(model, b)
+    log(f"ffn_in kernel: {roof['avg_us']} us, {roof['achieved']} GB/s")
+    head = head_roofline(fm, b)
+    log(f"head kernel: {head['avg_us']} us, {head['achieved']} GB/s")
     cpu = None
     if not args.no_cpu:
         t = time.time()
@@ -174,6 +277,8 @@ def main():
                    "decode_effective_GBs": round(token_bytes * tok_s / 1e9, 1),
                    "distinct_ids": len(set(ids.tolist()))},
         "roofline": roof,
+        "head_roofline": head,
+        "host_loop": host,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

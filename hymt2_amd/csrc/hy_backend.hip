@@ -958,4 +958,21 @@ int hymt2_hip_head(void* impl, hy_dweight* w, const float* h, const float* norm_
     return launch_head(a, c->s) == hipSuccess ? 0 : -2;
 }
 
+int hymt2_hip_ffn_in(void* impl, hy_dweight* wg, hy_dweight* wu, const float* h, const float* norm_w, float eps,
+                     float* out) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    const DW *g = dw(wg), *u = dw(wu);
+    if (!c || c->broken || !g || !u || g->mw.kind != u->mw.kind || g->mw.n != u->mw.n || g->mw.k != u->mw.k ||
+        !quant_kind(g->mw.kind) || !h || !norm_w || !out)
+        return -1;
+    JobSpec gu[2] = {{g, out, g->mw.n, EPI_STORE}, {u, out, u->mw.n, EPI_STORE}};
+    MvOpts o;
+    o.pro = PRO_NORM;
+    o.threads = 1024;
+    o.x = h;
+    o.norm_w = norm_w;
+    o.eps = eps;
+    return run_matvec(c, gu, 2, true, 1, o) ? 0 : -2;
+}
+
 }  // extern "C"

@@ -59,6 +59,7 @@ def load():
         "hymt2_hip_gen_steps": (i, [vp, i]),
         "hymt2_hip_gen_read": (i, [vp, vp, i, i]),
         "hymt2_hip_head": (i, [vp, vp, vp, vp, C.c_float, vp, i, vp]),
+        "hymt2_hip_ffn_in": (i, [vp, vp, vp, vp, vp, C.c_float, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -70,7 +71,7 @@ def load():
 EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops", "hymt2_hip_last_error",
            "hymt2_hip_abi_layout", "hymt2_hip_stream", "hymt2_hip_quantize_q8k", "hymt2_hip_matvec",
            "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_generate", "hymt2_hip_gen_begin",
-           "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head"]
+           "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in"]
 
 
 def abi_layout() -> dict:

@@ -165,6 +165,14 @@ HYMT2_HIP_API int hymt2_hip_generate(void *impl, const hymt2_fused_args *shape, 
 HYMT2_HIP_API int hymt2_hip_head(void *impl, hy_dweight *w, const float *h_dev, const float *norm_dev, float eps,
                                  float *logits_dev, int n_arg, unsigned long long *key_dev);
 
+/* The decode step's feed-forward input kernel on device pointers (enqueued on the context
+ * stream), for one token: out[r] = SwiGLU(gate_r, up_r) with gate/up = rows of wg/wu . Q8_K(
+ * rmsnorm(h; norm_w, eps)), i.e. src/model.c:870-876 for nt = 1 (RMSNorm :719-739, quantize_q8k
+ * src/kernels.c:128-165, matmul_rows :1241, SiLU-gate :875). wg and wu must be uploaded
+ * quantized weights of one kind and shape. */
+HYMT2_HIP_API int hymt2_hip_ffn_in(void *impl, hy_dweight *wg, hy_dweight *wu, const float *h_dev,
+                                   const float *norm_dev, float eps, float *out_dev);
+
 #ifdef __cplusplus
 }
 #endif

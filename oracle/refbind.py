@@ -3,8 +3,9 @@ TEST INFRASTRUCTURE ONLY.
 
 ``_ref/libhymt2_ref.so`` is the reference's C host + CPU kernels compiled by oracle/Makefile
 straight from the read-only reference tree. Tests use it to pin the oracle bit-for-bit, and
-bench.py's cpu_baseline leg times it. ``_ref/libhymt2_host.so`` is the same host linked against
-the HIP backend instead of the reference's CUDA file (the drop-in, exercised by GPU tests).
+bench.py's cpu_baseline leg times it. ``_ref/libhymt2_host.so`` is the reference's libhymt2 built
+with its own flags (hidden visibility; only the public HYMT2_API symbols exported) and the HIP
+backend's static archive linked in place of src/cuda.c (the drop-in, exercised by GPU tests).
 """
 from __future__ import annotations
 
@@ -54,7 +55,8 @@ def load(path: str = REF_LIB):
         if hasattr(L, name):
             fn = getattr(L, name)
             fn.restype, fn.argtypes = res, args
-    L.kernels_init()
+    if hasattr(L, "kernels_init"):  # internal symbol: exported by _ref/libhymt2_ref.so only
+        L.kernels_init()
     _libs[path] = L
     return L
 

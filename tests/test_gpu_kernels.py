@@ -202,6 +202,32 @@ def test_head_and_argmax(backend, gt, n):
         backend.release(h)
 
 
+# ----------------------------------------------------------------------------- FFN input step
+
+@pytest.mark.parametrize("gt,n,k", [(abi.GT_STQ1_0, 6144, 2048), (abi.GT_Q2_0C, 1536, 1024), (abi.GT_Q4_K, 512, 2048)])
+def test_ffn_in_step(backend, gt, n, k):
+    """hymt2_hip_ffn_in: RMSNorm -> Q8_K -> gate/up matvecs -> g / (1 + expf(-g)) * u, the decode
+    step's fused feed-forward input (src/model.c:870-876), against the oracle's pieces."""
+    g = synth.rng(n + k)
+    wg, wu = synth.make_weight(g, gt, n, k), synth.make_weight(g, gt, n, k)
+    hvec = synth.activations(g, 1, k)[0]
+    nw = g.uniform(0.9, 1.1, k).astype(np.float32)
+    hg, hu = backend.upload(wg), backend.upload(wu)
+    try:
+        out = empty_f32(n)
+        assert backend.L.hymt2_hip_ffn_in(backend.impl, hg, hu, dev(hvec).data_ptr(), dev(nw).data_ptr(),
+                                          C.c_float(1e-5), out.data_ptr()) == 0
+        sync()
+        xn = O.rmsnorm(hvec, nw, 1e-5)[None, :]
+        xq = O.quantize_q8k(xn)
+        gate, up = O.matvec(wg, xn, xq, 1)[0], O.matvec(wu, xn, xq, 1)[0]
+        ref = (gate / (np.float32(1) + O.expf(-gate)) * up).astype(np.float32)
+        assert np.array_equal(bits(out.cpu().numpy()), bits(ref))
+    finally:
+        backend.release(hg)
+        backend.release(hu)
+
+
 # ----------------------------------------------------------------------------- argument checks
 
 def test_entry_points_reject_bad_arguments(backend):
