@@ -296,6 +296,28 @@ static bool run_matvec(Ctx* c, const JobSpec* js, int njobs, bool pair, int nt, 
     return true;
 }
 
+// One token (nt == 1): the decode matvec k_mv1 where its shapes apply (K = 2048 / 6144, one
+// kind class), else the general kernel.
+static bool run_mv1(Ctx* c, const JobSpec* js, int njobs, bool pair, const MvOpts& o) {
+    Mv1Launch L;
+    memset(&L, 0, sizeof L);
+    L.njobs = njobs;
+    L.pair = pair ? 1 : 0;
+    for (int j = 0; j < njobs; j++) {
+        L.job[j].W = js[j].w->mw;
+        L.job[j].out = js[j].out;
+        L.job[j].epi = js[j].epi;
+    }
+    L.act = o.act;
+    L.x = o.x;
+    L.norm_w = o.norm_w;
+    L.eps = o.eps;
+    const hipError_t e = launch_mv1(L, o.pro, c->s);
+    if (e == hipErrorNotSupported) return run_matvec(c, js, njobs, pair, 1, o);
+    HIPCHK(c, e);
+    return true;
+}
+
 static bool ensure_scratch(Ctx* c, size_t act_bytes, size_t out_bytes) {
     if (act_bytes > c->act_cap) {
         if (c->act) (void)hipFree(c->act);
@@ -506,7 +528,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, attn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
             o1.act = f->act_h;
         }
-        if (!run_matvec(c, qkv, 3, false, nt, o1)) return false;
+        if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_matvec(c, qkv, 3, false, nt, o1))) return false;
         const bool fused_attn = nt == 1 && 256 % f->hdim == 0 && (f->heads / f->kv_heads) % (256 / f->hdim) == 0 &&
                                 attn_decode_lds(f->hdim, f->ctx) <= 96 * 1024;
         if (fused_attn) {
@@ -559,7 +581,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
         JobSpec o{wo, f->d_h, H, EPI_ADD};
         MvOpts o2;
         o2.act = f->act_q;
-        if (!run_matvec(c, &o, 1, false, nt, o2)) return false;
+        if (!(nt == 1 ? run_mv1(c, &o, 1, false, o2) : run_matvec(c, &o, 1, false, nt, o2))) return false;
         // ---- feed-forward block
         const bool pair = wg->mw.kind == wu->mw.kind && wg->mw.n == wu->mw.n;
         JobSpec gu[2] = {{wg, f->g, F, EPI_STORE}, {wu, f->u, F, EPI_STORE}};
@@ -574,7 +596,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, ffn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
             o3.act = f->act_h;
         }
-        if (!run_matvec(c, gu, 2, pair, nt, o3)) return false;
+        if (!(nt == 1 ? run_mv1(c, gu, 2, pair, o3) : run_matvec(c, gu, 2, pair, nt, o3))) return false;
         if (!pair) HIPCHK(c, launch_silu_mul(f->g, f->u, nt * F, c->s));
         JobSpec dn{wd, f->d_h, H, EPI_ADD};
         MvOpts o4;
@@ -586,7 +608,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_quantize_q8k(f->g, F, f->act_f, F, nt, c->s));
             o4.act = f->act_f;
         }
-        if (!run_matvec(c, &dn, 1, false, nt, o4)) return false;
+        if (!(nt == 1 ? run_mv1(c, &dn, 1, false, o4) : run_matvec(c, &dn, 1, false, nt, o4))) return false;
     }
     return true;
 }
@@ -804,7 +826,7 @@ int hymt2_hip_matvec(void* impl, hy_dweight* w, const void* act, float* out, int
     JobSpec j{d, out, d->mw.n, EPI_STORE};
     MvOpts o;
     o.act = static_cast<const HyQ8K*>(act);
-    return run_matvec(c, &j, 1, false, nt, o) ? 0 : -2;
+    return (nt == 1 ? run_mv1(c, &j, 1, false, o) : run_matvec(c, &j, 1, false, nt, o)) ? 0 : -2;
 }
 
 int hymt2_hip_selftest_f16(void* impl, const uint16_t* src, float* dst, int n) {
@@ -972,7 +994,7 @@ int hymt2_hip_ffn_in(void* impl, hy_dweight* wg, hy_dweight* wu, const float* h,
     o.x = h;
     o.norm_w = norm_w;
     o.eps = eps;
-    return run_matvec(c, gu, 2, true, 1, o) ? 0 : -2;
+    return run_mv1(c, gu, 2, true, o) ? 0 : -2;
 }
 
 }  // extern "C"

@@ -153,3 +153,35 @@ __device__ inline float hy_wave_seq_sum(const float* p, int n, int lane) {
     }
     return s;
 }
+
+// Sequential fp32 sum of squares x[0]*x[0] + x[1]*x[1] + ... in index order (each square
+// rounded to fp32 first, as `sum += x[i] * x[i]` compiles without contraction), by one whole
+// wavefront, with the lane-serial scheme of hy_wave_seq_sum. x is global or LDS, 16-byte aligned.
+__device__ inline float hy_wave_seq_sq_sum(const float* x, int n, int lane) {
+    float s = 0.f;
+    for (int base = 0; base < n; base += 64 * 32) {
+        float v[32];
+        const int e0 = base + 32 * lane;
+        if (e0 + 32 <= n) {
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const float4 q = *reinterpret_cast<const float4*>(x + e0 + i);
+                v[i] = q.x * q.x;
+                v[i + 1] = q.y * q.y;
+                v[i + 2] = q.z * q.z;
+                v[i + 3] = q.w * q.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? x[e0 + i] * x[e0 + i] : 0.f;
+        }
+        const int nl = min(64, (n - base + 31) / 32);
+        for (int L = 0; L < nl; L++) {
+            float t = s;
+#pragma unroll
+            for (int i = 0; i < 32; i++) t += v[i];
+            s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), L));
+        }
+    }
+    return s;
+}

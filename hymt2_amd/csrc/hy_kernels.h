@@ -62,6 +62,33 @@ hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, 
 hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s);
 size_t matvec_lds_bytes(const MvLaunch& L, int pro);
 
+// Single-token matvec of the fused decode step (k_mv1, hy_decode_mv.hip). Each half-wavefront
+// owns one weight row per iteration; a lane owns the same 16-byte segment positions in every
+// row it visits, so its slice of the Q8_K activation stays in registers.
+struct Mv1Job {
+    MvWeight W;
+    float* out;      // out[r]
+    int epi;         // EPI_STORE / EPI_ADD
+    int wg_begin;    // first workgroup of this job in the grid
+};
+
+struct Mv1Launch {
+    Mv1Job job[kMaxJobs];
+    int njobs;
+    int pair;              // job[0] = gate, job[1] = up of equal shape: job[0].out[r] = silu(g_r) * u_r
+    int rows_per_wg;       // rows (pair: row pairs) per workgroup
+    const HyQ8K* act;      // PRO_NONE: Q8_K activation blocks [K / 256]
+    const float* x;        // PRO_NORM: h [K]; PRO_QUANT: fp32 input [K]
+    const float* norm_w;   // PRO_NORM weights [K]
+    float eps;
+    int K;
+};
+
+// Builds and launches k_mv1 for jobs of one kind class with K = 2048 or 6144; returns
+// hipErrorNotSupported when the shapes fall outside what k_mv1 handles (the caller then uses
+// launch_matvec).
+hipError_t launch_mv1(Mv1Launch& L, int pro, hipStream_t s);
+
 struct AttnArgs {
     float* q;              // [nt][qdim]
     const float* k;        // [nt][kvdim]

@@ -130,6 +130,10 @@ SHAPES = [
     (abi.GT_Q6_K, 65, 512),
     (abi.GT_STQ1_0, 1, 256),       # one row, one block
     (abi.GT_Q2_0C, 129, 512),
+    (abi.GT_Q4_K, 37, 2048),       # ragged row counts at the decode kernel's two input sizes
+    (abi.GT_STQ1_0, 129, 6144),
+    (abi.GT_Q6_K, 65, 2048),
+    (abi.GT_Q4_K, 11, 6144),
 ]
 
 
@@ -204,7 +208,8 @@ def test_head_and_argmax(backend, gt, n):
 
 # ----------------------------------------------------------------------------- FFN input step
 
-@pytest.mark.parametrize("gt,n,k", [(abi.GT_STQ1_0, 6144, 2048), (abi.GT_Q2_0C, 1536, 1024), (abi.GT_Q4_K, 512, 2048)])
+@pytest.mark.parametrize("gt,n,k", [(abi.GT_STQ1_0, 6144, 2048), (abi.GT_Q2_0C, 1536, 1024), (abi.GT_Q4_K, 512, 2048),
+                                    (abi.GT_Q6_K, 101, 2048), (abi.GT_STQ1_0, 7, 2048)])
 def test_ffn_in_step(backend, gt, n, k):
     """hymt2_hip_ffn_in: RMSNorm -> Q8_K -> gate/up matvecs -> g / (1 + expf(-g)) * u, the decode
     step's fused feed-forward input (src/model.c:870-876), against the oracle's pieces."""

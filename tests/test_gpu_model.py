@@ -92,6 +92,28 @@ def test_long_greedy_device_vs_oracle(backend, mode):
         fm.close()
 
 
+@pytest.mark.parametrize("mode", ["stq", "q2", "q4km"])
+def test_hidden2048_models(backend, mode):
+    """Two layers at the 1.8B layer shapes (hidden 2048, ffn 6144, 16/4 heads, hd 128): the
+    single-token steps run the decode matvec kernel (K = 2048 and 6144); logits of a one-token
+    forward after a prefill, and 20 device greedy ids, vs the oracle."""
+    shape = synth.ModelShape(n_layer=2, vocab=1000, ctx=96)
+    model = synth.make_model(shape, mode=mode, seed=47)
+    prompt = synth.rand_prompt(synth.rng(48), 9, shape.vocab)
+    om = O.OracleModel(model, threads=8)
+    om.forward(prompt[:8], 0, False)
+    ref = om.forward(prompt[8:], 8, True)
+    fm = lib.FusedModel(backend, model)
+    try:
+        fm.forward(list(prompt[:8]), 0, False)
+        assert np.array_equal(bits(fm.forward([int(prompt[8])], 8, True)), bits(ref))
+        want = O.OracleModel(model, threads=8).generate(prompt, 20, batch=16)
+        ids, _ = fm.generate_device(prompt, 20)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
 def test_generate_rejects_overlong_runs(backend):
     model = synth.make_model(synth.ModelShape(n_layer=1, hidden=256, ffn=512, heads=2, kv_heads=1, hdim=128,
                                               vocab=300, ctx=64), mode="stq", seed=45)
