@@ -835,6 +835,12 @@ int hymt2_hip_selftest_f16(void* impl, const uint16_t* src, float* dst, int n) {
     return launch_selftest(src, dst, n, 0, c->s) == hipSuccess ? 0 : -2;
 }
 
+int hymt2_hip_selftest_sqsum(void* impl, const float* x, int n, int m, float* out, int method) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || !x || !out) return -1;
+    return launch_selftest_sqsum(x, n, m, out, method, c->s) == hipSuccess ? 0 : -2;
+}
+
 int hymt2_hip_selftest_expf(void* impl, const float* src, float* dst, int n) {
     Ctx* c = static_cast<Ctx*>(impl);
     if (!c || n < 0) return -1;

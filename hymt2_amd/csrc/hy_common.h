@@ -185,3 +185,159 @@ __device__ inline float hy_wave_seq_sq_sum(const float* x, int n, int lane) {
     }
     return s;
 }
+
+// ----------------------------------------------------------------------------------- scans
+
+// Inclusive prefix sums over the 64 lanes (row_shr within 16-lane rows, then row_bcast:15 and
+// row_bcast:31 across rows). The float version is used only for estimates (its rounding
+// depends on the tree); the double version is exact wherever it is used below.
+__device__ inline float hy_wave_incl_scan(float x) {
+#define HY_SCAN_STEP(CTRL, ROWS)                                                                      \
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROWS, \
+                                                               0xF, true))
+    HY_SCAN_STEP(0x111, 0xF);
+    HY_SCAN_STEP(0x112, 0xF);
+    HY_SCAN_STEP(0x114, 0xF);
+    HY_SCAN_STEP(0x118, 0xF);
+    HY_SCAN_STEP(0x142, 0xA);
+    HY_SCAN_STEP(0x143, 0xC);
+#undef HY_SCAN_STEP
+    return x;
+}
+
+__device__ inline double hy_wave_incl_scan_d(double x) {
+#define HY_SCAN_STEP(CTRL, ROWS)                                                                  \
+    do {                                                                                          \
+        const uint64_t u = __builtin_bit_cast(uint64_t, x);                                       \
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROWS, 0xF, true); \
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROWS, 0xF, true); \
+        x += __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);                               \
+    } while (0)
+    HY_SCAN_STEP(0x111, 0xF);
+    HY_SCAN_STEP(0x112, 0xF);
+    HY_SCAN_STEP(0x114, 0xF);
+    HY_SCAN_STEP(0x118, 0xF);
+    HY_SCAN_STEP(0x142, 0xA);
+    HY_SCAN_STEP(0x143, 0xC);
+#undef HY_SCAN_STEP
+    return x;
+}
+
+__device__ inline double hy_readlane_d(double x, int l) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// ----------------------------------------------------------------------------------- exact sums
+
+// The sequential fp32 sum of squares s = (((0 + x0*x0) + x1*x1) + ...) for n <= 2048, bit for
+// bit, computed by one whole wavefront faster than a chain of n dependent adds.
+//
+// Why it is exact: the addends a_i = x_i*x_i are >= 0, so the running sum s never decreases.
+// While s and s + a stay in one binade [M, 2M) (ulp u = M * 2^-23), fl(s + a) = s + RN_u(a),
+// where RN_u(a) rounds a to a multiple of u, unless a lies exactly halfway between two
+// multiples of u (then the result depends on the parity of s). So on a stretch of addends
+// where that holds, the sequential sum is s_start + sum of RN_u(a_i), which needs no chain.
+//
+// Lane L holds addends [32L, 32L+32) as two 16-addend segments. An estimate G of the running
+// sum before each segment (float sums of non-negative values, relative error < 2^-19) places
+// the segment in a binade; the true running sum differs from the exact real prefix sum by at
+// most n * 2^-23 <= 2^-12 relative, so G is within 2^-11 of it, and a segment whose estimated
+// start and end lie inside one binade with a 2^-9 margin is certain to run inside it. Such "clean" segments with no halfway
+// addend contribute K = sum of RN_u(a_i) (exact in fp32: multiples of u below M). All clean
+// K are summed in double prefix sums, exact because they are multiples of the smallest ulp in
+// play and the binades used span at most 27 (checked). Remaining "dirty" segments (the
+// first, those that cross a binade, those with a halfway addend) are added one addend at a
+// time with fp32 adds, in order, with the clean contributions in between added exactly.
+// All-zero segments are clean with K = 0. Non-finite sums make every segment dirty.
+__device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
+    float v[32];
+    const int e0 = 32 * lane;
+    if (e0 + 32 <= n) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(x + e0 + i);
+            v[i] = q.x * q.x;
+            v[i + 1] = q.y * q.y;
+            v[i + 2] = q.z * q.z;
+            v[i + 3] = q.w * q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? x[e0 + i] * x[e0 + i] : 0.f;
+    }
+    // 1. estimates of the running sum before each segment
+    float g[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        float t8[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) t8[i] = v[16 * q + 2 * i] + v[16 * q + 2 * i + 1];
+        g[q] = ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
+    }
+    const float gl = g[0] + g[1];
+    // exclusive prefix as the inclusive scan of the values shifted one lane up (wave_shr:1;
+    // lane 0 reads 0): a sum of non-negative terms only, so its relative error stays tiny
+    const float est0 = hy_wave_incl_scan(
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, gl), 0x138, 0xF, 0xF, true)));
+    const float tail = est0 + gl;
+    const float total = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tail), 63));
+    const int ex_total = (int)((hy_fbits(total) >> 23) & 0xffu);
+    // 2. classify each segment; K = its exact contribution when clean
+    bool clean[2];
+    float K[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const float G = q ? est0 + g[0] : est0;
+        const int ex = (int)((hy_fbits(G) >> 23) & 0xffu);
+        const float M = hy_bitsf((uint32_t)ex << 23);
+        const float hu = hy_bitsf((uint32_t)max(ex - 24, 1) << 23);  // u / 2
+        bool ok = G > 0.f && ex >= 25 && ex <= 253 && ex >= ex_total - 27 && G >= M * 1.001953125f &&
+                  G + g[q] < M * 1.99609375f;
+        float k = 0.f;
+        bool tie = false;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float a = v[16 * q + i];
+            const float r = (M + a) - M;
+            tie |= fabsf(a - r) == hu;
+            k += r;
+        }
+        const bool zero = g[q] == 0.f;  // all addends +0 (g is a sum of non-negative values)
+        clean[q] = zero || (ok && !tie);
+        K[q] = zero ? 0.f : k;
+    }
+    // 3. exact prefix sums of the clean contributions, in addend order
+    const double kd0 = clean[0] ? (double)K[0] : 0.0, kd1 = clean[1] ? (double)K[1] : 0.0;
+    const double kl = kd0 + kd1;
+    const double pin = hy_wave_incl_scan_d(kl);
+    const double pex = pin - kl;
+    // 4. walk the dirty segments in order
+    uint64_t d0 = __builtin_amdgcn_ballot_w64(!clean[0]);
+    uint64_t d1 = __builtin_amdgcn_ballot_w64(!clean[1]);
+    float s = 0.f;
+    double done = 0.0;  // clean contributions already added to s
+    while (d0 | d1) {
+        const int l0 = d0 ? __builtin_ctzll(d0) : 64;
+        const int l1 = d1 ? __builtin_ctzll(d1) : 64;
+        const bool second = l1 < l0;  // segment 2*l1 + 1 comes before 2*l0
+        const int L = second ? l1 : l0;
+        const double before = hy_readlane_d(pex, L) + (second ? hy_readlane_d(kd0, L) : 0.0);
+        s = (float)((double)s + (before - done));
+        float t = s;
+        if (second) {
+#pragma unroll
+            for (int i = 16; i < 32; i++) t += v[i];
+            d1 &= d1 - 1;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) t += v[i];
+            d0 &= d0 - 1;
+        }
+        s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), L));
+        done = before;
+    }
+    return (float)((double)s + (hy_readlane_d(pin, 63) - done));
+}

@@ -296,7 +296,7 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
             }
             // RMSNorm, src/model.c:719-739: sequential sum of squares, then x * scale * w
             if (wave == 0) {
-                const float sum = hy_wave_seq_sq_sum(L.x, K, lane);
+                const float sum = hy_wave_exact_sq_sum(L.x, K, lane);
                 if (lane == 0) scale_slot = 1.0f / sqrtf(sum / (float)K + L.eps);
             }
             __syncthreads();

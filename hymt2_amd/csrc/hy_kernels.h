@@ -156,5 +156,6 @@ hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16,
 hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
 hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s);
+hipError_t launch_selftest_sqsum(const float* x, int n, int m, float* out, int method, hipStream_t s);
 
 }  // namespace hy

@@ -65,15 +65,23 @@ hipError_t launch_quantize_q8k(const float* x, int ldx, HyQ8K* act, int K, int n
 
 // =========================================================================== RMSNorm
 
-// x (LDS, K floats) <- x * (1/sqrtf(sum(x*x)/K + eps)) * w, the scalar RMSNorm of
-// src/model.c:719-739: the squares are formed in parallel (sq: K floats of LDS scratch) and
-// summed sequentially in index order by wavefront 0.
+// x (LDS, K floats, complete before the call) <- x * (1/sqrtf(sum(x*x)/K + eps)) * w, the
+// scalar RMSNorm of src/model.c:719-739. Wavefront 0 forms the sequential sum of squares in
+// index order: the exact segmented form for K <= 2048, else the squares (sq: K floats of LDS
+// scratch) summed by the lane-serial chain.
 __device__ void rmsnorm_lds(float* xs, float* sq, const float* w, int K, float eps, float* scale_slot) {
-    for (int i = threadIdx.x; i < K; i += blockDim.x) sq[i] = xs[i] * xs[i];
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const float sum = hy_wave_seq_sum(sq, K, threadIdx.x);
-        if (threadIdx.x == 0) *scale_slot = 1.0f / sqrtf(sum / (float)K + eps);
+    if (K <= 2048) {
+        if (threadIdx.x < 64) {
+            const float sum = hy_wave_exact_sq_sum(xs, K, threadIdx.x);
+            if (threadIdx.x == 0) *scale_slot = 1.0f / sqrtf(sum / (float)K + eps);
+        }
+    } else {
+        for (int i = threadIdx.x; i < K; i += blockDim.x) sq[i] = xs[i] * xs[i];
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const float sum = hy_wave_seq_sum(sq, K, threadIdx.x);
+            if (threadIdx.x == 0) *scale_slot = 1.0f / sqrtf(sum / (float)K + eps);
+        }
     }
     __syncthreads();
     const float scale = *scale_slot;
@@ -1008,6 +1016,20 @@ __global__ void k_selftest(const void* src, float* dst, int n, int what) {
     if (i >= n) return;
     if (what == 0) dst[i] = hy_f16(reinterpret_cast<const uint16_t*>(src)[i]);
     else dst[i] = hy_expf(reinterpret_cast<const float*>(src)[i]);
+}
+
+// One wavefront per vector: the sequential sum of squares of x[v*n .. v*n + n), by the
+// lane-serial chain (method 0) or the exact segmented form (method 1).
+__global__ __launch_bounds__(64) void k_selftest_sqsum(const float* x, int n, float* out, int method) {
+    const float* p = x + (size_t)blockIdx.x * n;
+    const float s = method ? hy_wave_exact_sq_sum(p, n, threadIdx.x) : hy_wave_seq_sq_sum(p, n, threadIdx.x);
+    if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
+hipError_t launch_selftest_sqsum(const float* x, int n, int m, float* out, int method, hipStream_t s) {
+    if (n < 1 || n > 2048 || (n & 3) || m < 1) return hipErrorInvalidValue;
+    k_selftest_sqsum<<<m, 64, 0, s>>>(x, n, out, method);
+    return hipGetLastError();
 }
 
 hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s) {

@@ -74,6 +74,52 @@ def test_expf_matches_libm(backend):
     assert np.array_equal(bits(out.cpu().numpy()), bits(O.expf(x)))
 
 
+def _sq_inputs(mode, m, n, g):
+    x = g.standard_normal((m, n)).astype(np.float32)
+    if mode == "small":
+        x *= np.float32(0.02)
+    elif mode == "outliers":
+        x[:, ::64] *= np.float32(30)
+    elif mode == "coarse":  # many halfway cases
+        x = (np.trunc(x * 4) * np.float32(0.25)).astype(np.float32)
+    elif mode == "wide":
+        x *= np.exp(3 * g.standard_normal((m, n))).astype(np.float32)
+    elif mode == "spike":
+        x[np.arange(m), g.integers(0, n, m)] *= np.float32(1e6)
+    elif mode == "regimes":
+        x[:, : n // 2] *= np.float32(1e-3)
+    elif mode == "zeros":
+        x[g.random((m, n)) < 0.3] = 0
+        x[: m // 4, :] = 0
+    elif mode == "extreme":
+        x[:, 0] = np.float32(3e19)  # squares overflow to inf
+        x[m // 2:, 1] = np.nan
+    return np.ascontiguousarray(x)
+
+
+@pytest.mark.parametrize("mode", ["normal", "small", "outliers", "coarse", "wide", "spike", "regimes", "zeros",
+                                  "extreme"])
+@pytest.mark.parametrize("n", [2048, 1024, 132, 4])
+def test_rmsnorm_sum_of_squares(backend, mode, n):
+    """The RMSNorm's sequential sum of squares (src/model.c:719-739) by the lane-serial chain and
+    by the exact segmented form, against numpy's sequential float32 accumulation."""
+    g = np.random.default_rng(abs(hash((mode, n))) % 2**32)
+    m = 4096 if n == 2048 else 512
+    x = _sq_inputs(mode, m, n, g)
+    sq = (x * x).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = np.add.accumulate(sq, axis=1, dtype=np.float32)[:, -1]
+    xd = dev(x)
+    for method in (0, 1):
+        out = empty_f32(m)
+        assert backend.L.hymt2_hip_selftest_sqsum(backend.impl, xd.data_ptr(), n, m, out.data_ptr(), method) == 0
+        sync()
+        got = out.cpu().numpy()
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(bits(got)[~nan], bits(want)[~nan]), f"method {method}"
+
+
 # ----------------------------------------------------------------------------- Q8_K
 
 def test_q8k_golden(backend):
