@@ -252,22 +252,30 @@ __device__ inline double hy_readlane_d(double x, int l) {
 // first, those that cross a binade, those with a halfway addend) are added one addend at a
 // time with fp32 adds, in order, with the clean contributions in between added exactly.
 // All-zero segments are clean with K = 0. Non-finite sums make every segment dirty.
-__device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
-    float v[32];
+//
+// hy_wave_load32 fetches lane L's values x[32L .. 32L+32) (zero past n); hy_wave_exact_sq_sum_v
+// takes them, so a caller can issue the loads early.
+__device__ inline void hy_wave_load32(const float* x, int n, int lane, float (&v)[32]) {
     const int e0 = 32 * lane;
     if (e0 + 32 <= n) {
 #pragma unroll
         for (int i = 0; i < 32; i += 4) {
             const float4 q = *reinterpret_cast<const float4*>(x + e0 + i);
-            v[i] = q.x * q.x;
-            v[i + 1] = q.y * q.y;
-            v[i + 2] = q.z * q.z;
-            v[i + 3] = q.w * q.w;
+            v[i] = q.x;
+            v[i + 1] = q.y;
+            v[i + 2] = q.z;
+            v[i + 3] = q.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? x[e0 + i] * x[e0 + i] : 0.f;
+        for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? x[e0 + i] : 0.f;
     }
+}
+
+__device__ inline float hy_wave_exact_sq_sum_v(const float (&xv)[32], int lane) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = xv[i] * xv[i];
     // 1. estimates of the running sum before each segment
     float g[2];
 #pragma unroll
@@ -309,35 +317,79 @@ __device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
         clean[q] = zero || (ok && !tie);
         K[q] = zero ? 0.f : k;
     }
-    // 3. exact prefix sums of the clean contributions, in addend order
+    // 3. exact prefix sums of the clean contributions, in addend order (position 2L + q)
     const double kd0 = clean[0] ? (double)K[0] : 0.0, kd1 = clean[1] ? (double)K[1] : 0.0;
     const double kl = kd0 + kd1;
     const double pin = hy_wave_incl_scan_d(kl);
-    const double pex = pin - kl;
-    // 4. walk the dirty segments in order
-    uint64_t d0 = __builtin_amdgcn_ballot_w64(!clean[0]);
-    uint64_t d1 = __builtin_amdgcn_ballot_w64(!clean[1]);
-    float s = 0.f;
-    double done = 0.0;  // clean contributions already added to s
-    while (d0 | d1) {
-        const int l0 = d0 ? __builtin_ctzll(d0) : 64;
-        const int l1 = d1 ? __builtin_ctzll(d1) : 64;
-        const bool second = l1 < l0;  // segment 2*l1 + 1 comes before 2*l0
-        const int L = second ? l1 : l0;
-        const double before = hy_readlane_d(pex, L) + (second ? hy_readlane_d(kd0, L) : 0.0);
-        s = (float)((double)s + (before - done));
-        float t = s;
-        if (second) {
+    const double pex = pin - kl;  // before segment (L, 0); before (L, 1) is pex + kd0
+    const uint64_t d0 = __builtin_amdgcn_ballot_w64(!clean[0]);
+    const uint64_t d1 = __builtin_amdgcn_ballot_w64(!clean[1]);
+    // 4. for each dirty segment, the clean contribution since the previous dirty one. Between
+    //    two dirty segments every non-zero clean segment lies in one binade [M, 2M) (two clean
+    //    neighbours in different binades would need a gap between their margins), so this sum
+    //    is a multiple of that binade's ulp below M: exact as a float, and s + delta is exact.
+    const uint64_t below = (1ull << lane) - 1;  // lanes < this one
+    const uint64_t cb = (d0 | d1) & below;
+    const int lp = cb ? 63 - __builtin_clzll(cb) : -1;  // last lane below with a dirty segment
+    const bool lp_second = lp >= 0 && ((d1 >> lp) & 1);
+    const int src = lp >= 0 ? lp : 0;
+    const double pex_lp = __builtin_bit_cast(double, ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(__builtin_bit_cast(uint64_t, pex) >> 32), src) << 32) |
+                                                         (uint32_t)__shfl((int)(uint32_t)__builtin_bit_cast(uint64_t, pex), src));
+    const double kd0_lp = __builtin_bit_cast(double, ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(__builtin_bit_cast(uint64_t, kd0) >> 32), src) << 32) |
+                                                         (uint32_t)__shfl((int)(uint32_t)__builtin_bit_cast(uint64_t, kd0), src));
+    const double prev0 = lp < 0 ? 0.0 : (lp_second ? pex_lp + kd0_lp : pex_lp);
+    const float delta0 = (float)(pex - prev0);                       // before (L, 0)
+    const float delta1 = ((d0 >> lane) & 1) ? 0.f : (float)((pex + kd0) - prev0);  // before (L, 1)
+    // 5. compact the dirty segments, in order, into rows of LDS: row k = [delta, 16 addends] of
+    //    the k-th dirty segment; lane k then holds row k (and k + 64)
+    __shared__ float rows[128][20];
+    const int rank0 = __builtin_popcountll(d0 & below) + __builtin_popcountll(d1 & below);
+    const bool dirty0 = (d0 >> lane) & 1, dirty1 = (d1 >> lane) & 1;
+    const int rank1 = rank0 + (dirty0 ? 1 : 0);
+    if (dirty0) {
+        rows[rank0][0] = delta0;
 #pragma unroll
-            for (int i = 16; i < 32; i++) t += v[i];
-            d1 &= d1 - 1;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) t += v[i];
-            d0 &= d0 - 1;
-        }
-        s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), L));
-        done = before;
+        for (int i = 0; i < 16; i++) rows[rank0][1 + i] = v[i];
     }
-    return (float)((double)s + (hy_readlane_d(pin, 63) - done));
+    if (dirty1) {
+        rows[rank1][0] = delta1;
+#pragma unroll
+        for (int i = 0; i < 16; i++) rows[rank1][1 + i] = v[16 + i];
+    }
+    const int nd = __builtin_popcountll(d0) + __builtin_popcountll(d1);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 6. the walk: s + delta is exact; then the segment's addends one fp32 add at a time
+    float s = 0.f;
+    for (int base = 0; base < nd; base += 64) {
+        float r[17];
+        const int k = min(base + lane, 127);
+#pragma unroll
+        for (int i = 0; i < 17; i++) r[i] = rows[k][i];
+        const int cnt = min(64, nd - base);
+        for (int kk = 0; kk < cnt; kk++) {
+            float t = s + r[0];
+#pragma unroll
+            for (int i = 1; i < 17; i++) t += r[i];
+            s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), kk));
+        }
+    }
+    // 7. the clean tail after the last dirty segment
+    const double p_end = hy_readlane_d(pin, 63);
+    double before_last = 0.0;
+    if (d0 | d1) {
+        const int l0 = d0 ? 63 - __builtin_clzll(d0) : -1;
+        const int l1 = d1 ? 63 - __builtin_clzll(d1) : -1;
+        const bool second = l1 >= l0;  // segment 2*l1 + 1 comes after 2*l0
+        const int L = second ? l1 : l0;
+        before_last = hy_readlane_d(pex, L) + (second ? hy_readlane_d(kd0, L) : 0.0);
+    }
+    return s + (float)(p_end - before_last);
+}
+
+__device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
+    float v[32];
+    hy_wave_load32(x, n, lane, v);
+    return hy_wave_exact_sq_sum_v(v, lane);
 }

@@ -217,6 +217,14 @@ __device__ __forceinline__ float mv1_term(const WSeg& S, const ActSeg& A, int su
     }
 }
 
+// Keeps the compiler from moving memory operations or other instructions across this point,
+// so loads are issued in the phase order the kernel is written in (vector loads complete in
+// issue order: what is issued first can be consumed first).
+__device__ __forceinline__ void issue_fence() {
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("" ::: "memory");
+}
+
 }  // namespace
 
 // KIND: PANEL, Q4K, Q6K, or ANY (Q4K and Q6K jobs mixed; the kind is read per workgroup).
@@ -254,28 +262,23 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     const int n = J.W.n;
     const int row0 = (wg - J.wg_begin) * L.rows_per_wg;
 
-    // 1. every weight load of this thread, issued before the prologue
-    WSeg ws[ITERS][SPL];
+    // 1. the prologue's inputs first (vector loads complete in issue order, so anything issued
+    //    before the weights can be consumed without waiting for them); the residual of this
+    //    lane's row as well
+    constexpr int QB = NB / kMv1Waves;  // Q8_K blocks built per wave
+    float e[QB][4], nw[QB][4], hv[32];
+    float resid = 0.f;
+    const int rrow = min(row0 + wave * RPW + lane, n - 1);  // the row this lane sums (lane < RPW)
+    if (!L.pair && J.epi == EPI_ADD) resid = J.out[rrow];
+    ActSeg A[SPL];
+    if (PRO == PRO_NONE) {
 #pragma unroll
-    for (int i = 0; i < ITERS; i++) {
-        const int r = L.pair ? row0 + wave * ITERS + i : row0 + wave * RPW + 2 * i + hh;
-#pragma unroll
-        for (int s = 0; s < SPL; s++) {
-            if (r < n) {
-                ws[i][s] = load_wseg<SPB>(kind, w, w2, wsc, wdh, wps, NB, r, j + 32 * s);
-            } else {
-                ws[i][s].a = ws[i][s].b = make_uint4(0, 0, 0, 0);
-                ws[i][s].c = 0;
-                ws[i][s].sd = 0;
-            }
-        }
+        for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(L.act, kind, j + 32 * s);
     }
-
-    // 2. Q8_K activation: built in LDS by the prologue, or read from global memory
-    const HyQ8K* act = L.act;
     if (PRO != PRO_NONE) {
-        constexpr int QB = NB / kMv1Waves;
-        float e[QB][4];
+        // every wave loads h (only wave 0 sums it): no divergent load, no merge copy that would
+        // wait for it
+        if (PRO == PRO_NORM) hy_wave_load32(L.x, K, lane, hv);
 #pragma unroll
         for (int q = 0; q < QB; q++) {
             const float4 v = *reinterpret_cast<const float4*>(L.x + (wave * QB + q) * HY_QK + 4 * lane);
@@ -283,20 +286,37 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
             e[q][1] = v.y;
             e[q][2] = v.z;
             e[q][3] = v.w;
-        }
-        if (PRO == PRO_NORM) {
-            float nw[QB][4];
-#pragma unroll
-            for (int q = 0; q < QB; q++) {
-                const float4 v = *reinterpret_cast<const float4*>(L.norm_w + (wave * QB + q) * HY_QK + 4 * lane);
-                nw[q][0] = v.x;
-                nw[q][1] = v.y;
-                nw[q][2] = v.z;
-                nw[q][3] = v.w;
+            if (PRO == PRO_NORM) {
+                const float4 u = *reinterpret_cast<const float4*>(L.norm_w + (wave * QB + q) * HY_QK + 4 * lane);
+                nw[q][0] = u.x;
+                nw[q][1] = u.y;
+                nw[q][2] = u.z;
+                nw[q][3] = u.w;
             }
+        }
+    }
+
+    issue_fence();
+
+    // 2. every weight load of this thread, in flight through the prologue. Rows past the end
+    //    load the last row instead (unconditional loads: a conditional load would need a merge
+    //    copy that waits for it); their terms are never used.
+    WSeg ws[ITERS][SPL];
+#pragma unroll
+    for (int i = 0; i < ITERS; i++) {
+        const int r = L.pair ? row0 + wave * ITERS + i : row0 + wave * RPW + 2 * i + hh;
+        const int rl = min(r, n - 1);
+#pragma unroll
+        for (int s = 0; s < SPL; s++) ws[i][s] = load_wseg<SPB>(kind, w, w2, wsc, wdh, wps, NB, rl, j + 32 * s);
+    }
+    issue_fence();
+
+    // 3. Q8_K activation: built in LDS by the prologue, or gathered from global memory above
+    if (PRO != PRO_NONE) {
+        if (PRO == PRO_NORM) {
             // RMSNorm, src/model.c:719-739: sequential sum of squares, then x * scale * w
             if (wave == 0) {
-                const float sum = hy_wave_exact_sq_sum(L.x, K, lane);
+                const float sum = hy_wave_exact_sq_sum_v(hv, lane);
                 if (lane == 0) scale_slot = 1.0f / sqrtf(sum / (float)K + L.eps);
             }
             __syncthreads();
@@ -308,13 +328,11 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
         }
         q8k_quantize_lanes<QB>(e, act_lds + wave * QB, lane);
         __syncthreads();
-        act = act_lds;
-    }
-    ActSeg A[SPL];
 #pragma unroll
-    for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(act, kind, j + 32 * s);
+        for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(act_lds, kind, j + 32 * s);
+    }
 
-    // 3. exact block terms -> LDS
+    // 4. exact block terms -> LDS
 #pragma unroll
     for (int i = 0; i < ITERS; i++) {
         const int rw = 2 * i + hh;  // row slot of this half-wave in the wave
@@ -333,7 +351,7 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     }
     __syncthreads();
 
-    // 4. per-row sums in block order and the epilogue
+    // 5. per-row sums in block order and the epilogue
     if (!L.pair) {
         if (lane < RPW) {
             const int r = row0 + wave * RPW + lane;
@@ -341,7 +359,7 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
                 float acc = 0.f;
 #pragma unroll
                 for (int b = 0; b < NB; b++) acc += terms[wave][lane][b];
-                J.out[r] = J.epi == EPI_ADD ? J.out[r] + acc : acc;  // residual: h += tmp
+                J.out[r] = J.epi == EPI_ADD ? resid + acc : acc;  // residual: h += tmp
             }
         }
     } else if (lane < ITERS) {
