@@ -529,9 +529,33 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             o1.act = f->act_h;
         }
         if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_matvec(c, qkv, 3, false, nt, o1))) return false;
+        // single token: one workgroup per head (k_attn1), fp32 output quantized by the o matvec;
+        // else the 256-output-block attention kernel, else the general path
+        const bool head_attn = nt == 1 && (f->hdim == 64 || f->hdim == 128) && f->ctx <= kA1MaxCtx;
         const bool fused_attn = nt == 1 && 256 % f->hdim == 0 && (f->heads / f->kv_heads) % (256 / f->hdim) == 0 &&
                                 attn_decode_lds(f->hdim, f->ctx) <= 96 * 1024;
-        if (fused_attn) {
+        if (head_attn) {
+            Attn1Args aa{};
+            aa.q = f->q;
+            aa.k = f->k;
+            aa.v = f->v;
+            aa.kc = kc;
+            aa.vc = vc;
+            aa.q_norm = f->norm_ptr(li, 2);
+            aa.k_norm = f->norm_ptr(li, 3);
+            aa.rope_cos = f->rope_c;
+            aa.rope_sin = f->rope_s;
+            aa.pos_dev = pos_dev;
+            aa.pos0 = pos0;
+            aa.ao = f->ao;
+            aa.heads = f->heads;
+            aa.kv_heads = f->kv_heads;
+            aa.hdim = f->hdim;
+            aa.rope_half = f->rope_half;
+            aa.ctx = f->ctx;
+            aa.eps = f->eps;
+            HIPCHK(c, launch_attn1(aa, c->s));
+        } else if (fused_attn) {
             AttnDecodeArgs ad{};
             ad.q = f->q;
             ad.k = f->k;
@@ -581,6 +605,12 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
         JobSpec o{wo, f->d_h, H, EPI_ADD};
         MvOpts o2;
         o2.act = f->act_q;
+        if (head_attn) {  // quantize the fp32 attention output in the matvec prologue
+            o2.pro = PRO_QUANT;
+            o2.threads = 1024;
+            o2.x = f->ao;
+            o2.act = nullptr;
+        }
         if (!(nt == 1 ? run_mv1(c, &o, 1, false, o2) : run_matvec(c, &o, 1, false, nt, o2))) return false;
         // ---- feed-forward block
         const bool pair = wg->mw.kind == wu->mw.kind && wg->mw.n == wu->mw.n;

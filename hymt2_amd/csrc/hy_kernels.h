@@ -127,6 +127,28 @@ hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s);
 size_t attn_decode_lds(int hdim, int ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
+// Single-token attention, one workgroup per query head (k_attn1, hy_attn_decode.hip): RoPE
+// and RMSNorm of q and k, the bf16 KV store at the position, softmax attention over positions
+// 0..pos, fp32 output row per head into ao (quantized by the o-projection).
+constexpr int kA1MaxCtx = 4096;
+struct Attn1Args {
+    const float* q;        // [qdim] fp32, before RoPE
+    const float* k;        // [kvdim]
+    const float* v;        // [kvdim]
+    uint16_t* kc;          // layer base of K cache [kv_heads][ctx][hdim]
+    uint16_t* vc;
+    const float* q_norm;
+    const float* k_norm;
+    const float* rope_cos;
+    const float* rope_sin;
+    const int* pos_dev;    // optional: position read from device memory (graph replay)
+    int pos0;
+    float* ao;             // [qdim] attention output
+    int heads, kv_heads, hdim, rope_half, ctx;
+    float eps;
+};
+hipError_t launch_attn1(const Attn1Args& a, hipStream_t s);
+
 struct HeadArgs {
     MvWeight W;            // F16 or F32 rows
     const float* h;        // last token's hidden state [K]
