@@ -36,18 +36,55 @@ __device__ __forceinline__ void a1_fence() {
 
 }  // namespace
 
+// RoPE (NeoX, src/model.c:754-765) and RMSNorm (src/model.c:840-841) of one head row, by one
+// wavefront: lane l owns elements l, l + 64, ... (RPL per lane). scr is this wavefront's LDS
+// row. Returns the normalized element i of the lane through out[i].
+template <int HD>
+__device__ __forceinline__ void rope_norm_wave(float (&x)[HD / 64], float* scr, const float* cs, const float* sn, int half,
+                                               const float* nw, float eps, int lane, float (&out)[HD / 64]) {
+    constexpr int RPL = HD / 64;
+#pragma unroll
+    for (int i = 0; i < RPL; i++) scr[lane + 64 * i] = x[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float r[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+        const int d = lane + 64 * i;
+        r[i] = x[i];
+        if (d < half) r[i] = x[i] * cs[d] - scr[d + half] * sn[d];
+        else if (d < 2 * half) r[i] = scr[d - half] * sn[d - half] + x[i] * cs[d - half];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < RPL; i++) scr[lane + 64 * i] = r[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float sum = hy_wave_seq_sq_sum(scr, HD, lane);
+    const float scale = 1.0f / sqrtf(sum / (float)HD + eps);
+#pragma unroll
+    for (int i = 0; i < RPL; i++) out[i] = r[i] * scale * nw[lane + 64 * i];
+}
+
 template <int HD>
 __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
-    constexpr int KV4 = HD / 8;                              // 16-byte pieces of one K / V row
-    constexpr int VT_LOADS = kA1Tile * KV4 / kA1Threads;     // 16-byte V loads per thread per tile
-    static_assert(VT_LOADS >= 1 && kA1Tile * KV4 % kA1Threads == 0, "tile split");
-    __shared__ __align__(16) uint16_t vt[kA1Tile * HD];
-    __shared__ __align__(16) float row[3][HD];  // q, k, v of this token
+    constexpr int KV4 = HD / 8;                           // 16-byte pieces of one K / V row
+    constexpr int RPL = HD / 64;                          // row elements per lane
+    constexpr int VT_LOADS = kA1Tile * KV4 / kA1Threads;  // V pieces per thread per tile
+    constexpr int VSTRIDE = kA1Tile + 8;                  // transposed tile row (keys of one dim)
+    static_assert(VT_LOADS >= 1 && kA1Tile * KV4 % kA1Threads == 0 && kA1Threads % kA1Tile == 0, "tile split");
+    __shared__ __align__(16) uint16_t vt[HD * VSTRIDE];   // V tile, transposed: vt[d][j]
+    __shared__ __align__(16) float scr[3][HD];
+    __shared__ __align__(16) float qn[HD];
     __shared__ __align__(16) uint16_t kb[HD];
     __shared__ __align__(16) uint16_t vb[HD];
     __shared__ float red[kA1Threads / 64];
-    __shared__ float stat[2];
-    extern __shared__ __align__(16) float sc[];  // scores, then probabilities [n]
+    __shared__ float stat;
+    extern __shared__ __align__(16) float ex[];           // scores, then exponentials [n]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
@@ -59,60 +96,43 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
 
-    // 0. loads: this token's q, k, v rows, then the first keys' K rows and the first V tile
-    constexpr int TOK = (3 * HD + kA1Threads - 1) / kA1Threads;
-    float tok[TOK];
+    // 0. loads: this token's row for waves 0 (q), 1 (k), 2 (v); the cached K rows of the first
+    //    pass (one key per thread) and the first V tile (lanes over keys, pieces over threads)
+    float x[RPL];
+    {
+        const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
 #pragma unroll
-    for (int i = 0; i < TOK; i++) {
-        const int f = min(tid + kA1Threads * i, 3 * HD - 1), r = f / HD, d = f % HD;
-        tok[i] = r == 0 ? a.q[(size_t)h * HD + d] : (r == 1 ? a.k[(size_t)g * HD + d] : a.v[(size_t)g * HD + d]);
+        for (int i = 0; i < RPL; i++) x[i] = src[lane + 64 * i];
     }
     uint4 kr[KV4];
-    {
-        const int j = min(tid, max(pos - 1, 0));  // keys < pos come from the cache
+    if (tid < pos) {
 #pragma unroll
-        for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)j * HD + 8 * i);
+        for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)tid * HD + 8 * i);
     }
     uint4 vr[VT_LOADS];
+    const int vkey = tid % kA1Tile, vpiece0 = tid / kA1Tile;  // piece p = vpiece0 + (256 / T) * i
 #pragma unroll
     for (int i = 0; i < VT_LOADS; i++) {
-        const int f = tid + kA1Threads * i, j = min(f / KV4, max(pos - 1, 0));
-        vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (f % KV4));
+        const int pc = vpiece0 + (kA1Threads / kA1Tile) * i;
+        if (vkey < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)vkey * HD + 8 * pc);
     }
     a1_fence();
 
-    // 1. RoPE (NeoX, src/model.c:754-765) of q and k, then their RMSNorm (src/model.c:840-841)
-#pragma unroll
-    for (int i = 0; i < TOK; i++) {
-        const int f = tid + kA1Threads * i;
-        if (f < 3 * HD) row[f / HD][f % HD] = tok[i];
-    }
-    __syncthreads();
+    // 1. RoPE + RMSNorm of q (wave 0) and k (wave 1), bf16 of k and v
     const float* cs = a.rope_cos + (size_t)pos * half;
     const float* sn = a.rope_sin + (size_t)pos * half;
-    static_assert(2 * HD <= kA1Threads, "one thread per q / k element");
-    float rot = 0.f;
-    if (tid < 2 * HD) {
-        const int r = tid / HD, d = tid % HD;
-        rot = row[r][d];
-        if (d < half) rot = row[r][d] * cs[d] - row[r][d + half] * sn[d];
-        else if (d < 2 * half) rot = row[r][d - half] * sn[d - half] + row[r][d] * cs[d - half];
-    }
-    __syncthreads();
-    if (tid < 2 * HD) row[tid / HD][tid % HD] = rot;
-    __syncthreads();
     if (wave < 2) {
-        const float sum = hy_wave_seq_sq_sum(row[wave], HD, lane);
-        if (lane == 0) stat[wave] = 1.0f / sqrtf(sum / (float)HD + a.eps);
+        float y[RPL];
+        rope_norm_wave<HD>(x, scr[wave], cs, sn, half, wave == 0 ? a.q_norm : a.k_norm, a.eps, lane, y);
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            if (wave == 0) qn[lane + 64 * i] = y[i];
+            else kb[lane + 64 * i] = hy_to_bf16(y[i]);
+        }
+    } else if (wave == 2) {
+#pragma unroll
+        for (int i = 0; i < RPL; i++) vb[lane + 64 * i] = hy_to_bf16(x[i]);
     }
-    __syncthreads();
-    if (tid < 2 * HD) {
-        const int r = tid / HD, d = tid % HD;
-        const float y = row[r][d] * stat[r] * (r == 0 ? a.q_norm[d] : a.k_norm[d]);
-        if (r == 0) row[0][d] = y;
-        else kb[d] = hy_to_bf16(y);
-    }
-    for (int d = tid; d < HD; d += kA1Threads) vb[d] = hy_to_bf16(row[2][d]);
     __syncthreads();
     // the bf16 k, v of this position (src/model.c:842-847), stored once per KV head
     if (h % group == 0 && tid < HD) {
@@ -123,14 +143,12 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
 
     // 2. scores s_j = dot_bf16(q, K_j) * (1/sqrtf(hd)); key `pos` is this token's kb
     const float scale = 1.0f / sqrtf((float)HD);
-    const float* qn = row[0];
     float lmax = -__builtin_inff();
     for (int p0 = 0; p0 < n; p0 += kA1Keys) {
         const int j = p0 + tid;
-        if (p0 > 0) {
-            const int jl = min(j, max(pos - 1, 0));
+        if (p0 > 0 && j < pos) {
 #pragma unroll
-            for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)jl * HD + 8 * i);
+            for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)j * HD + 8 * i);
         }
         if (j < n) {
             float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -149,65 +167,78 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
                 a2 += qb.z * kf[6];
                 a3 += qb.w * kf[7];
             }
-            const float s = ((a0 + a1) + (a2 + a3)) * scale;
-            sc[j] = s;
-            lmax = fmaxf(lmax, s);
+            const float sj = ((a0 + a1) + (a2 + a3)) * scale;
+            ex[j] = sj;
+            lmax = fmaxf(lmax, sj);
         }
     }
-    // 3. softmax over positions: max (order-free), exp, sum in order, normalise
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
-    __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int j = tid; j < n; j += kA1Threads) sc[j] = hy_expf(sc[j] - mx);
-    __syncthreads();
-    if (wave == 0) {
-        const float sum = hy_wave_seq_sum(sc, n, lane);
-        if (lane == 0) stat[0] = 1.0f / sum;
-    }
-    __syncthreads();
-    const float inv = stat[0];
-    for (int j = tid; j < n; j += kA1Threads) sc[j] = sc[j] * inv;
 
-    // 4. o[d] = sum_j p_j * V_j[d] in position order, from LDS tiles of V
-    float o = 0.f;
-    for (int t0 = 0; t0 < n; t0 += kA1Tile) {
-        __syncthreads();  // previous tile consumed; probabilities visible
+    // 3. the first V tile into LDS (transposed) while the maximum settles
+    auto store_tile = [&](int t0) {
 #pragma unroll
         for (int i = 0; i < VT_LOADS; i++) {
-            const int f = tid + kA1Threads * i, jj = f / KV4, j = t0 + jj;
-            const uint4 val = j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * (f % KV4)) : vr[i];
-            *reinterpret_cast<uint4*>(vt + (size_t)jj * HD + 8 * (f % KV4)) = val;
+            const int pc = vpiece0 + (kA1Threads / kA1Tile) * i, j = t0 + vkey;
+            const uint4 val = j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : vr[i];
+            const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                vt[(8 * pc + 2 * e) * VSTRIDE + vkey] = (uint16_t)(w[e] & 0xffffu);
+                vt[(8 * pc + 2 * e + 1) * VSTRIDE + vkey] = (uint16_t)(w[e] >> 16);
+            }
         }
-        __syncthreads();
-        if (t0 + kA1Tile < n) {  // next tile in flight while this one is summed
+    };
+    store_tile(0);
+    __syncthreads();
+    // softmax over positions (src/model.c:781-789): max (order-free), exp, sum in order
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int j = tid; j < n; j += kA1Threads) ex[j] = hy_expf(ex[j] - mx);
+    __syncthreads();
+    if (wave == 0) {
+        const float sum = hy_wave_seq_sum(ex, n, lane);
+        if (lane == 0) stat = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = stat;
+
+    // 4. o[d] = sum_j (e_j * inv) * V_j[d] in position order (axpy_bf16 with p = sc[j] * inv)
+    float o = 0.f;
+    for (int t0 = 0; t0 < n; t0 += kA1Tile) {
+        if (t0 > 0) {
+            __syncthreads();  // previous tile consumed
+            store_tile(t0);
+            __syncthreads();
+        }
+        if (t0 + kA1Tile < n) {  // the next tile's loads, in flight while this one is summed
 #pragma unroll
             for (int i = 0; i < VT_LOADS; i++) {
-                const int f = tid + kA1Threads * i, j = min(t0 + kA1Tile + f / KV4, max(pos - 1, 0));
-                vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (f % KV4));
+                const int pc = vpiece0 + (kA1Threads / kA1Tile) * i, j = t0 + kA1Tile + vkey;
+                if (j < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * pc);
             }
         }
         if (tid < HD) {
             const int cnt = min(kA1Tile, n - t0);
-            const float* pj = sc + t0;
+            const float* ej = ex + t0;
+            const uint16_t* vd = vt + (size_t)tid * VSTRIDE;
             int jj = 0;
             for (; jj + 8 <= cnt; jj += 8) {
-                float pv[8], vv[8];
+                const uint4 v8 = *reinterpret_cast<const uint4*>(vd + jj);
+                const float4 e0 = *reinterpret_cast<const float4*>(ej + jj);
+                const float4 e1 = *reinterpret_cast<const float4*>(ej + jj + 4);
+                float vf[8];
+                bf16x8f(v8, vf);
+                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    pv[k] = pj[jj + k];
-                    vv[k] = hy_bf16(vt[(size_t)(jj + k) * HD + tid]);
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) o += pv[k] * vv[k];
+                for (int k = 0; k < 8; k++) o += (ev[k] * inv) * vf[k];
             }
-            for (; jj < cnt; jj++) o += pj[jj] * hy_bf16(vt[(size_t)jj * HD + tid]);
+            for (; jj < cnt; jj++) o += (ej[jj] * inv) * hy_bf16(vd[jj]);
         }
     }
     if (tid < HD) a.ao[(size_t)h * HD + tid] = o;
 }
 
-size_t attn1_lds(int ctx) { return (size_t)ctx * sizeof(float); }
+size_t attn1_lds(int ctx) { return ((size_t)ctx + 8) * sizeof(float); }
 
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {
     if (a.heads % a.kv_heads || 2 * a.rope_half > a.hdim || a.ctx > kA1MaxCtx) return hipErrorNotSupported;

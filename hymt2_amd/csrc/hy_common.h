@@ -393,3 +393,130 @@ __device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
     hy_wave_load32(x, n, lane, v);
     return hy_wave_exact_sq_sum_v(v, lane);
 }
+
+// ----------------------------------------------------------------------------------- block forms
+
+// LDS of hy_block_exact_sq_sum8 (a workgroup of up to 4 wavefronts).
+struct HyExactLds {
+    float wtot[4];          // estimate of each wavefront's total
+    double ktot[4];         // each wavefront's clean contributions
+    uint64_t dmask[4];      // dirty segments of each wavefront
+    double lpex[256];       // wavefront-local exclusive prefix of clean contributions per segment
+    float rows[256][12];    // dirty segments in order: [delta, 8 addends]
+    float result;
+};
+
+// The sequential sum of squares of n = 512 * NW values, the workgroup's NW wavefronts holding 8
+// consecutive values per lane (lane l of wavefront w: values 512w + 8l .. +8), bit for bit the
+// one-lane loop. The same method as hy_wave_exact_sq_sum_v with 8-addend segments, the
+// estimates and the exact prefix sums carried across wavefronts through LDS (the proof there
+// holds unchanged: n <= 2048 keeps the sequential sum within 2^-12 of the exact one). Every
+// thread of the workgroup must call it; all receive the sum.
+template <int NW>
+__device__ inline float hy_block_exact_sq_sum8(const float (&xv)[8], HyExactLds& S, int wave, int lane) {
+    static_assert(NW >= 1 && NW <= 4, "up to 4 wavefronts");
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = xv[i] * xv[i];
+    const float g = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    // 1. estimate of the running sum before this segment (float sums of non-negative values)
+    const float estw = hy_wave_incl_scan(
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, g), 0x138, 0xF, 0xF, true)));
+    if (lane == 63) S.wtot[wave] = estw + g;
+    __syncthreads();
+    float off = 0.f, total = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        if (w < wave) off += S.wtot[w];
+        total += S.wtot[w];
+    }
+    const float G = off + estw;
+    const int ex_total = (int)((hy_fbits(total) >> 23) & 0xffu);
+    // 2. classify the segment
+    const int ex = (int)((hy_fbits(G) >> 23) & 0xffu);
+    const float M = hy_bitsf((uint32_t)ex << 23);
+    const float hu = hy_bitsf((uint32_t)max(ex - 24, 1) << 23);
+    const bool ok = G > 0.f && ex >= 25 && ex <= 253 && ex >= ex_total - 27 && G >= M * 1.001953125f &&
+                    G + g < M * 1.99609375f;
+    float k = 0.f;
+    bool tie = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float r = (M + v[i]) - M;
+        tie |= fabsf(v[i] - r) == hu;
+        k += r;
+    }
+    const bool zero = g == 0.f;
+    const bool clean = zero || (ok && !tie);
+    // 3. exact prefix sums of the clean contributions
+    const double kd = clean && !zero ? (double)k : 0.0;
+    const double pin = hy_wave_incl_scan_d(kd);
+    const double pex = pin - kd;
+    S.lpex[64 * wave + lane] = pex;
+    if (lane == 63) S.ktot[wave] = pin;
+    const uint64_t dm = __builtin_amdgcn_ballot_w64(!clean);
+    if (lane == 0) S.dmask[wave] = dm;
+    __syncthreads();
+    double koff = 0.0;
+    int rank = 0, nd = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        const int c = __builtin_popcountll(S.dmask[w]);
+        if (w < wave) {
+            koff += S.ktot[w];
+            rank += c;
+        }
+        nd += c;
+    }
+    // 4. dirty segments: the clean contribution since the previous dirty one, then a row of LDS
+    if (!clean) {
+        const uint64_t below = dm & ((1ull << lane) - 1);
+        double prev = 0.0;
+        if (below) {
+            prev = S.lpex[64 * wave + (63 - __builtin_clzll(below))] + koff;
+        } else {
+            double kw = koff;
+            for (int w = wave - 1; w >= 0; w--) {
+                kw -= S.ktot[w];  // exact: the same sums taken apart
+                const uint64_t m = S.dmask[w];
+                if (m) {
+                    prev = S.lpex[64 * w + (63 - __builtin_clzll(m))] + kw;
+                    break;
+                }
+            }
+        }
+        const int r = rank + __builtin_popcountll(below);
+        S.rows[r][0] = (float)((pex + koff) - prev);
+#pragma unroll
+        for (int i = 0; i < 8; i++) S.rows[r][1 + i] = v[i];
+    }
+    __syncthreads();
+    // 5. wavefront 0 walks the dirty rows, then adds the clean tail
+    if (wave == 0) {
+        float s = 0.f;
+        for (int base = 0; base < nd; base += 64) {
+            float r[9];
+            const int kk0 = min(base + lane, 255);
+#pragma unroll
+            for (int i = 0; i < 9; i++) r[i] = S.rows[kk0][i];
+            const int cnt = min(64, nd - base);
+            for (int kk = 0; kk < cnt; kk++) {
+                float t = s + r[0];
+#pragma unroll
+                for (int i = 1; i < 9; i++) t += r[i];
+                s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), kk));
+            }
+        }
+        double ptot = 0.0, plast = 0.0, kw = 0.0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const uint64_t m = S.dmask[w];
+            if (m) plast = S.lpex[64 * w + (63 - __builtin_clzll(m))] + kw;
+            kw += S.ktot[w];
+        }
+        ptot = kw;
+        if (lane == 0) S.result = s + (float)(ptot - plast);
+    }
+    __syncthreads();
+    return S.result;
+}

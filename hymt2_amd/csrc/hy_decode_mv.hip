@@ -11,6 +11,8 @@
 // order by one lane, which also applies the epilogue (store, residual add, or SwiGLU of a
 // gate/up pair). The arithmetic is the reference's scalar path (src/kernels.c:565-581 panel,
 // :808-877 Q6_K / Q4_K, src/model.c:719-739 RMSNorm, :865-876 residuals and SwiGLU).
+#include <type_traits>
+
 #include "hy_kernels.h"
 
 namespace hy {
@@ -73,6 +75,94 @@ __device__ inline void q8k_quantize_lanes(const float (&e)[QB][4], HyQ8K* dst, i
             dst[q].d = zero ? 0.f : 1.f / iscale;
             dst[q].sum = total;
         }
+    }
+}
+
+// Row (16-lane) reductions: every lane of the row receives the result.
+__device__ __forceinline__ uint32_t row_max_u(uint32_t v) {
+    int x = (int)v;
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP1>(x));
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP2>(x));
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_HMIRROR>(x));
+    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
+    return (uint32_t)x;
+}
+__device__ __forceinline__ int row_min_i(int x) {
+    x = min(x, hy_dpp<HY_DPP_QSWAP1>(x));
+    x = min(x, hy_dpp<HY_DPP_QSWAP2>(x));
+    x = min(x, hy_dpp<HY_DPP_HMIRROR>(x));
+    x = min(x, hy_dpp<HY_DPP_MIRROR>(x));
+    return x;
+}
+// the value of half-wavefront `hl` (rows 2hl and 2hl + 1) combined from the row results
+__device__ __forceinline__ uint32_t half_max_u(uint32_t rowv, int hl) {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 48);
+    return hl ? max(c, d) : max(a, b);
+}
+__device__ __forceinline__ int half_min_i(int rowv, int hl) {
+    const int a = __builtin_amdgcn_readlane(rowv, 0), b = __builtin_amdgcn_readlane(rowv, 16);
+    const int c = __builtin_amdgcn_readlane(rowv, 32), d = __builtin_amdgcn_readlane(rowv, 48);
+    return hl ? min(c, d) : min(a, b);
+}
+__device__ __forceinline__ int half_sum_i(int rowv, int hl) {
+    const int a = __builtin_amdgcn_readlane(rowv, 0), b = __builtin_amdgcn_readlane(rowv, 16);
+    const int c = __builtin_amdgcn_readlane(rowv, 32), d = __builtin_amdgcn_readlane(rowv, 48);
+    return hl ? c + d : a + b;
+}
+
+// Q8_K of two 256-element blocks (quantize_q8k, src/kernels.c:128-165) held 8 consecutive
+// elements per lane: lanes 0..31 hold dst[0]'s elements 8l..8l+7, lanes 32..63 dst[1]'s.
+__device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int lane) {
+    const int hl = lane >> 5, jl = lane & 31;
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) m = max(m, hy_fbits(e[i]) & 0x7fffffffu);
+    const uint32_t am = half_max_u(row_max_u(m), hl);
+    int f = 256;
+#pragma unroll
+    for (int i = 7; i >= 0; i--)
+        if ((hy_fbits(e[i]) & 0x7fffffffu) == am) f = 8 * jl + i;
+    const int frow = row_min_i(f);
+    const int first0 = half_min_i(frow, 0), first1 = half_min_i(frow, 1);
+    const int fi = (hl ? first1 : first0) & 7;
+    float cand = e[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) cand = fi == i ? e[i] : cand;
+    const float vm0 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), first0 >> 3));
+    const float vm1 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), 32 + (first1 >> 3)));
+    const float vmax = hl ? vm1 : vm0;
+    const bool zero = am == 0;
+    const float iscale = zero ? 0.f : -127.f / vmax;
+    int q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = (int)__builtin_rintf(iscale * e[i]);
+        q[i] = r > 127 ? 127 : (r < -127 ? -127 : r);
+    }
+    const int s8 = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+    const int s16 = s8 + hy_dpp<HY_DPP_QSWAP1>(s8);  // lanes 2k, 2k+1 hold one 16-element group
+    const int total = half_sum_i(hy_group_sum<16>(s8), hl);
+    uint32_t p[2];
+#pragma unroll
+    for (int w = 0; w < 2; w++)
+        p[w] = (uint32_t)(q[4 * w] & 0xff) | ((uint32_t)(q[4 * w + 1] & 0xff) << 8) |
+               ((uint32_t)(q[4 * w + 2] & 0xff) << 16) | ((uint32_t)(q[4 * w + 3] & 0xff) << 24);
+    HyQ8K* y = dst + hl;
+    uint32_t* dw = reinterpret_cast<uint32_t*>(y);
+    const int idx = 8 * jl;  // first element of this lane in the block
+    dw[(320 + idx) / 4] = p[0];
+    dw[(320 + idx) / 4 + 1] = p[1];
+    // qp: element c*64 + l*16 + i at qp[l*64 + {0,2,1,3}[c]*16 + i] (src/internal.h:31-36)
+    const int c = idx >> 6, l = (idx >> 4) & 3, i0 = idx & 15;
+    const int seg = (c == 1) ? 2 : (c == 2 ? 1 : c);
+    dw[(l * 64 + seg * 16 + i0) / 4] = p[0];
+    dw[(l * 64 + seg * 16 + i0) / 4 + 1] = p[1];
+    if ((jl & 1) == 0) y->bsums[jl >> 1] = (int16_t)s16;
+    if (jl < 6) dw[296 / 4 + jl] = 0;
+    if (jl == 0) {
+        y->d = zero ? 0.f : 1.f / iscale;
+        y->sum = total;
     }
 }
 
@@ -235,10 +325,11 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     constexpr int NB = SPL * 32 / SPB;              // blocks per row
     constexpr int K = NB * HY_QK;
     constexpr int RPW = 2 * ITERS;                  // rows per wave
-    static_assert(NB % kMv1Waves == 0, "blocks per row must split over the waves");
+    static_assert(NB % (2 * kMv1Waves) == 0, "blocks per row must split in pairs over the waves");
     __shared__ __align__(64) HyQ8K act_lds[PRO == PRO_NONE ? 1 : NB];
     __shared__ float terms[kMv1Waves][RPW][NB];
-    __shared__ float scale_slot;
+    using ExLds = typename std::conditional<PRO == PRO_NORM, HyExactLds, int>::type;  // LDS of the norm only
+    __shared__ ExLds ex_lds;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hh = lane >> 5, j = lane & 31;
@@ -264,9 +355,10 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
 
     // 1. the prologue's inputs first (vector loads complete in issue order, so anything issued
     //    before the weights can be consumed without waiting for them); the residual of this
-    //    lane's row as well
-    constexpr int QB = NB / kMv1Waves;  // Q8_K blocks built per wave
-    float e[QB][4], nw[QB][4], hv[32];
+    //    lane's row as well. Wavefront w quantizes the blocks 2w*R .. 2w*R + 2R (R rounds of
+    //    two blocks); a lane holds 8 consecutive elements of a block per round.
+    constexpr int R = NB / (2 * kMv1Waves);
+    float e[R][8], nw[R][8];
     float resid = 0.f;
     const int rrow = min(row0 + wave * RPW + lane, n - 1);  // the row this lane sums (lane < RPW)
     if (!L.pair && J.epi == EPI_ADD) resid = J.out[rrow];
@@ -276,26 +368,21 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
         for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(L.act, kind, j + 32 * s);
     }
     if (PRO != PRO_NONE) {
-        // every wave loads h (only wave 0 sums it): no divergent load, no merge copy that would
-        // wait for it
-        if (PRO == PRO_NORM) hy_wave_load32(L.x, K, lane, hv);
 #pragma unroll
-        for (int q = 0; q < QB; q++) {
-            const float4 v = *reinterpret_cast<const float4*>(L.x + (wave * QB + q) * HY_QK + 4 * lane);
-            e[q][0] = v.x;
-            e[q][1] = v.y;
-            e[q][2] = v.z;
-            e[q][3] = v.w;
+        for (int k = 0; k < R; k++) {
+            const int off = (2 * (wave * R + k)) * HY_QK + 8 * lane;
+            const float4 v0 = *reinterpret_cast<const float4*>(L.x + off);
+            const float4 v1 = *reinterpret_cast<const float4*>(L.x + off + 4);
+            e[k][0] = v0.x, e[k][1] = v0.y, e[k][2] = v0.z, e[k][3] = v0.w;
+            e[k][4] = v1.x, e[k][5] = v1.y, e[k][6] = v1.z, e[k][7] = v1.w;
             if (PRO == PRO_NORM) {
-                const float4 u = *reinterpret_cast<const float4*>(L.norm_w + (wave * QB + q) * HY_QK + 4 * lane);
-                nw[q][0] = u.x;
-                nw[q][1] = u.y;
-                nw[q][2] = u.z;
-                nw[q][3] = u.w;
+                const float4 u0 = *reinterpret_cast<const float4*>(L.norm_w + off);
+                const float4 u1 = *reinterpret_cast<const float4*>(L.norm_w + off + 4);
+                nw[k][0] = u0.x, nw[k][1] = u0.y, nw[k][2] = u0.z, nw[k][3] = u0.w;
+                nw[k][4] = u1.x, nw[k][5] = u1.y, nw[k][6] = u1.z, nw[k][7] = u1.w;
             }
         }
     }
-
     issue_fence();
 
     // 2. every weight load of this thread, in flight through the prologue. Rows past the end
@@ -313,20 +400,16 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
 
     // 3. Q8_K activation: built in LDS by the prologue, or gathered from global memory above
     if (PRO != PRO_NONE) {
-        if (PRO == PRO_NORM) {
+        if constexpr (PRO == PRO_NORM) {
             // RMSNorm, src/model.c:719-739: sequential sum of squares, then x * scale * w
-            if (wave == 0) {
-                const float sum = hy_wave_exact_sq_sum_v(hv, lane);
-                if (lane == 0) scale_slot = 1.0f / sqrtf(sum / (float)K + L.eps);
-            }
-            __syncthreads();
-            const float scale = scale_slot;
+            static_assert(R == 1, "RMSNorm prologue over 2048 values");
+            const float sum = hy_block_exact_sq_sum8<kMv1Waves>(e[0], ex_lds, wave, lane);
+            const float scale = 1.0f / sqrtf(sum / (float)K + L.eps);
 #pragma unroll
-            for (int q = 0; q < QB; q++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) e[q][i] = e[q][i] * scale * nw[q][i];
+            for (int i = 0; i < 8; i++) e[0][i] = e[0][i] * scale * nw[0][i];
         }
-        q8k_quantize_lanes<QB>(e, act_lds + wave * QB, lane);
+#pragma unroll
+        for (int k = 0; k < R; k++) q8k_quantize_halves(e[k], act_lds + 2 * (wave * R + k), lane);
         __syncthreads();
 #pragma unroll
         for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(act_lds, kind, j + 32 * s);

@@ -1026,9 +1026,23 @@ __global__ __launch_bounds__(64) void k_selftest_sqsum(const float* x, int n, fl
     if (threadIdx.x == 0) out[blockIdx.x] = s;
 }
 
+// One 256-thread workgroup per vector: the workgroup-wide exact form (method 2) the decode
+// matvec's RMSNorm uses, values past n read as zero.
+__global__ __launch_bounds__(256) void k_selftest_sqsum_block(const float* x, int n, float* out) {
+    __shared__ HyExactLds lds;
+    const float* p = x + (size_t)blockIdx.x * n;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, e0 = 512 * wave + 8 * lane;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = e0 + i < n ? p[e0 + i] : 0.f;
+    const float s = hy_block_exact_sq_sum8<4>(v, lds, wave, lane);
+    if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
 hipError_t launch_selftest_sqsum(const float* x, int n, int m, float* out, int method, hipStream_t s) {
-    if (n < 1 || n > 2048 || (n & 3) || m < 1) return hipErrorInvalidValue;
-    k_selftest_sqsum<<<m, 64, 0, s>>>(x, n, out, method);
+    if (n < 1 || n > 2048 || (n & 3) || m < 1 || method < 0 || method > 2) return hipErrorInvalidValue;
+    if (method == 2) k_selftest_sqsum_block<<<m, 256, 0, s>>>(x, n, out);
+    else k_selftest_sqsum<<<m, 64, 0, s>>>(x, n, out, method);
     return hipGetLastError();
 }
 

@@ -131,7 +131,8 @@ HYMT2_HIP_API int hymt2_hip_selftest_f16(void *impl, const uint16_t *src_dev, fl
 HYMT2_HIP_API int hymt2_hip_selftest_expf(void *impl, const float *src_dev, float *dst_dev, int n);
 /* The RMSNorm sum of squares of m vectors x[m][n] (n <= 2048, n % 4 == 0): out[v] = the
  * sequential fp32 sum x0*x0 + x1*x1 + ... (src/model.c:719-739), by the lane-serial chain
- * (method 0) or the exact segmented form the decode kernels use (method 1). */
+ * (method 0), the one-wavefront exact segmented form (method 1) or the workgroup-wide exact
+ * form of the decode matvec's RMSNorm (method 2). */
 HYMT2_HIP_API int hymt2_hip_selftest_sqsum(void *impl, const float *x_dev, int n, int m, float *out_dev, int method);
 
 /* Device-resident greedy generation (no host round trip per token). Each step runs one

@@ -110,7 +110,7 @@ def test_rmsnorm_sum_of_squares(backend, mode, n):
     with np.errstate(invalid="ignore", over="ignore"):
         want = np.add.accumulate(sq, axis=1, dtype=np.float32)[:, -1]
     xd = dev(x)
-    for method in (0, 1):
+    for method in (0, 1, 2):
         out = empty_f32(m)
         assert backend.L.hymt2_hip_selftest_sqsum(backend.impl, xd.data_ptr(), n, m, out.data_ptr(), method) == 0
         sync()
