@@ -37,11 +37,12 @@ __device__ __forceinline__ void a1_fence() {
 }  // namespace
 
 // RoPE (NeoX, src/model.c:754-765) and RMSNorm (src/model.c:840-841) of one head row, by one
-// wavefront: lane l owns elements l, l + 64, ... (RPL per lane). scr is this wavefront's LDS
-// row. Returns the normalized element i of the lane through out[i].
+// wavefront: lane l owns elements l, l + 64, ... (RPL per lane), with its cos / sin table
+// entries (c, sn) and norm weights (nw) already in registers. scr is this wavefront's LDS row.
 template <int HD>
-__device__ __forceinline__ void rope_norm_wave(float (&x)[HD / 64], float* scr, const float* cs, const float* sn, int half,
-                                               const float* nw, float eps, int lane, float (&out)[HD / 64]) {
+__device__ __forceinline__ void rope_norm_wave(const float (&x)[HD / 64], float* scr, const float (&c)[HD / 64],
+                                               const float (&sn)[HD / 64], int half, const float (&nw)[HD / 64],
+                                               float eps, int lane, float (&out)[HD / 64]) {
     constexpr int RPL = HD / 64;
 #pragma unroll
     for (int i = 0; i < RPL; i++) scr[lane + 64 * i] = x[i];
@@ -53,8 +54,8 @@ __device__ __forceinline__ void rope_norm_wave(float (&x)[HD / 64], float* scr, 
     for (int i = 0; i < RPL; i++) {
         const int d = lane + 64 * i;
         r[i] = x[i];
-        if (d < half) r[i] = x[i] * cs[d] - scr[d + half] * sn[d];
-        else if (d < 2 * half) r[i] = scr[d - half] * sn[d - half] + x[i] * cs[d - half];
+        if (d < half) r[i] = x[i] * c[i] - scr[d + half] * sn[i];
+        else if (d < 2 * half) r[i] = scr[d - half] * sn[i] + x[i] * c[i];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -67,7 +68,7 @@ __device__ __forceinline__ void rope_norm_wave(float (&x)[HD / 64], float* scr, 
     const float sum = hy_wave_seq_sq_sum(scr, HD, lane);
     const float scale = 1.0f / sqrtf(sum / (float)HD + eps);
 #pragma unroll
-    for (int i = 0; i < RPL; i++) out[i] = r[i] * scale * nw[lane + 64 * i];
+    for (int i = 0; i < RPL; i++) out[i] = r[i] * scale * nw[i];
 }
 
 template <int HD>
@@ -75,16 +76,15 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     constexpr int KV4 = HD / 8;                           // 16-byte pieces of one K / V row
     constexpr int RPL = HD / 64;                          // row elements per lane
     constexpr int VT_LOADS = kA1Tile * KV4 / kA1Threads;  // V pieces per thread per tile
-    constexpr int VSTRIDE = kA1Tile + 8;                  // transposed tile row (keys of one dim)
-    static_assert(VT_LOADS >= 1 && kA1Tile * KV4 % kA1Threads == 0 && kA1Threads % kA1Tile == 0, "tile split");
-    __shared__ __align__(16) uint16_t vt[HD * VSTRIDE];   // V tile, transposed: vt[d][j]
-    __shared__ __align__(16) float scr[3][HD];
+    static_assert(VT_LOADS >= 1 && kA1Tile * KV4 % kA1Threads == 0, "tile split");
+    __shared__ __align__(16) uint16_t vt[kA1Tile * HD];   // V tile, natural layout vt[j][d]
+    __shared__ __align__(16) float scr[2][HD];
     __shared__ __align__(16) float qn[HD];
     __shared__ __align__(16) uint16_t kb[HD];
     __shared__ __align__(16) uint16_t vb[HD];
     __shared__ float red[kA1Threads / 64];
     __shared__ float stat;
-    extern __shared__ __align__(16) float ex[];           // scores, then exponentials [n]
+    extern __shared__ __align__(16) float ex[];           // scores, exponentials, probabilities [n]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
@@ -96,34 +96,34 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
 
-    // 0. loads: this token's row for waves 0 (q), 1 (k), 2 (v); the cached K rows of the first
-    //    pass (one key per thread) and the first V tile (lanes over keys, pieces over threads)
-    float x[RPL];
+    // 0. loads: this token's row (wavefronts 0: q, 1: k, 2: v) with its RoPE table entries and
+    //    norm weights, then the cached K rows of the first pass (one key per thread)
+    float x[RPL], rc[RPL], rs[RPL], nw[RPL];
     {
         const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
+        const float* nsrc = wave == 0 ? a.q_norm : a.k_norm;
+        const float* cs = a.rope_cos + (size_t)pos * half;
+        const float* sn = a.rope_sin + (size_t)pos * half;
 #pragma unroll
-        for (int i = 0; i < RPL; i++) x[i] = src[lane + 64 * i];
+        for (int i = 0; i < RPL; i++) {
+            const int d = lane + 64 * i, t = d < half ? d : (d < 2 * half ? d - half : 0);
+            x[i] = src[d];
+            rc[i] = cs[t];
+            rs[i] = sn[t];
+            nw[i] = nsrc[d];
+        }
     }
     uint4 kr[KV4];
     if (tid < pos) {
 #pragma unroll
         for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)tid * HD + 8 * i);
     }
-    uint4 vr[VT_LOADS];
-    const int vkey = tid % kA1Tile, vpiece0 = tid / kA1Tile;  // piece p = vpiece0 + (256 / T) * i
-#pragma unroll
-    for (int i = 0; i < VT_LOADS; i++) {
-        const int pc = vpiece0 + (kA1Threads / kA1Tile) * i;
-        if (vkey < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)vkey * HD + 8 * pc);
-    }
     a1_fence();
 
-    // 1. RoPE + RMSNorm of q (wave 0) and k (wave 1), bf16 of k and v
-    const float* cs = a.rope_cos + (size_t)pos * half;
-    const float* sn = a.rope_sin + (size_t)pos * half;
+    // 1. RoPE + RMSNorm of q (wavefront 0) and k (1), bf16 of k and v
     if (wave < 2) {
         float y[RPL];
-        rope_norm_wave<HD>(x, scr[wave], cs, sn, half, wave == 0 ? a.q_norm : a.k_norm, a.eps, lane, y);
+        rope_norm_wave<HD>(x, scr[wave], rc, rs, half, nw, a.eps, lane, y);
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
             if (wave == 0) qn[lane + 64 * i] = y[i];
@@ -132,6 +132,13 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     } else if (wave == 2) {
 #pragma unroll
         for (int i = 0; i < RPL; i++) vb[lane + 64 * i] = hy_to_bf16(x[i]);
+    }
+    // the first V tile's loads (natural layout: consecutive threads, consecutive pieces of a row)
+    uint4 vr[VT_LOADS];
+#pragma unroll
+    for (int i = 0; i < VT_LOADS; i++) {
+        const int f = tid + kA1Threads * i, j = f / KV4;
+        if (j < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (f % KV4));
     }
     __syncthreads();
     // the bf16 k, v of this position (src/model.c:842-847), stored once per KV head
@@ -175,25 +182,20 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
 
-    // 3. the first V tile into LDS (transposed) while the maximum settles
+    // 3. softmax over positions (src/model.c:781-789): max (order-free), exp, sum in order,
+    //    p_j = e_j * (1 / sum); the first V tile goes into LDS meanwhile
     auto store_tile = [&](int t0) {
 #pragma unroll
         for (int i = 0; i < VT_LOADS; i++) {
-            const int pc = vpiece0 + (kA1Threads / kA1Tile) * i, j = t0 + vkey;
-            const uint4 val = j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : vr[i];
-            const uint32_t w[4] = {val.x, val.y, val.z, val.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                vt[(8 * pc + 2 * e) * VSTRIDE + vkey] = (uint16_t)(w[e] & 0xffffu);
-                vt[(8 * pc + 2 * e + 1) * VSTRIDE + vkey] = (uint16_t)(w[e] >> 16);
-            }
+            const int f = tid + kA1Threads * i, jj = f / KV4, pc = f % KV4;
+            const uint4 val = t0 + jj == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : vr[i];
+            *reinterpret_cast<uint4*>(vt + (size_t)jj * HD + 8 * pc) = val;
         }
     };
-    store_tile(0);
     __syncthreads();
-    // softmax over positions (src/model.c:781-789): max (order-free), exp, sum in order
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int j = tid; j < n; j += kA1Threads) ex[j] = hy_expf(ex[j] - mx);
+    store_tile(0);
     __syncthreads();
     if (wave == 0) {
         const float sum = hy_wave_seq_sum(ex, n, lane);
@@ -201,8 +203,10 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     }
     __syncthreads();
     const float inv = stat;
+    for (int j = tid; j < n; j += kA1Threads) ex[j] = ex[j] * inv;  // sc[j] * inv, once per position
+    __syncthreads();
 
-    // 4. o[d] = sum_j (e_j * inv) * V_j[d] in position order (axpy_bf16 with p = sc[j] * inv)
+    // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16), one lane per dimension
     float o = 0.f;
     for (int t0 = 0; t0 < n; t0 += kA1Tile) {
         if (t0 > 0) {
@@ -213,26 +217,26 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
         if (t0 + kA1Tile < n) {  // the next tile's loads, in flight while this one is summed
 #pragma unroll
             for (int i = 0; i < VT_LOADS; i++) {
-                const int pc = vpiece0 + (kA1Threads / kA1Tile) * i, j = t0 + kA1Tile + vkey;
-                if (j < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * pc);
+                const int f = tid + kA1Threads * i, j = t0 + kA1Tile + f / KV4;
+                if (j < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (f % KV4));
             }
         }
         if (tid < HD) {
             const int cnt = min(kA1Tile, n - t0);
-            const float* ej = ex + t0;
-            const uint16_t* vd = vt + (size_t)tid * VSTRIDE;
+            const float* pj = ex + t0;
+            const uint16_t* vd = vt + tid;
             int jj = 0;
             for (; jj + 8 <= cnt; jj += 8) {
-                const uint4 v8 = *reinterpret_cast<const uint4*>(vd + jj);
-                const float4 e0 = *reinterpret_cast<const float4*>(ej + jj);
-                const float4 e1 = *reinterpret_cast<const float4*>(ej + jj + 4);
-                float vf[8];
-                bf16x8f(v8, vf);
-                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                const float4 p0 = *reinterpret_cast<const float4*>(pj + jj);
+                const float4 p1 = *reinterpret_cast<const float4*>(pj + jj + 4);
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                float vv[8];
 #pragma unroll
-                for (int k = 0; k < 8; k++) o += (ev[k] * inv) * vf[k];
+                for (int k = 0; k < 8; k++) vv[k] = hy_bf16(vd[(size_t)(jj + k) * HD]);
+#pragma unroll
+                for (int k = 0; k < 8; k++) o += pv[k] * vv[k];
             }
-            for (; jj < cnt; jj++) o += (ej[jj] * inv) * hy_bf16(vd[jj]);
+            for (; jj < cnt; jj++) o += pj[jj] * hy_bf16(vd[(size_t)jj * HD]);
         }
     }
     if (tid < HD) a.ao[(size_t)h * HD + tid] = o;
