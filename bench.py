@@ -125,6 +125,88 @@ def head_roofline(fm, b, reps: int = 20):
                 kernel="k_head<F16> (LM head 120818x2048 + argmax)")
 
 
+def layer_sets(b, copies: int = 64, passes: int = 2):
+    """BASELINE configs 0-2 on the single-token matvec entry point (hymt2_hip_matvec, Q8_K
+    activation already on the device, the reference's matmul_rows contract), each timed with
+    HIP events over `copies` rotating device copies of its weights (beyond the 256 MB Infinity
+    Cache):
+      config0: the fused gate/up 12288x2048 STQ1_0 panel (codes uniform 0..2, fp32 scales
+               U(0.005, 0.05)), one call; also timed repeating one copy (cache-resident)
+      config1: one Q2_0C layer: q, k, v, o, gate, up, down
+      config2: one Q4_K_M layer: Q4_K q, k, o, gate, up; Q6_K v, down
+    Algorithmic bytes: weights as stored + Q8_K activations + fp32 outputs."""
+    import torch
+    from hymt2_amd import abi, synth
+    s = synth.HYMT2_1_8B
+    g = synth.rng(0xC0DE0)
+    stream = torch.cuda.ExternalStream(b.stream)
+    shapes = [("wq", s.qdim, s.hidden), ("wk", s.kvdim, s.hidden), ("wv", s.kvdim, s.hidden), ("wo", s.hidden, s.qdim),
+              ("wg", s.ffn, s.hidden), ("wu", s.ffn, s.hidden), ("wd", s.hidden, s.ffn)]
+    act = {k: torch.zeros(k // 256 * abi.Q8K_BYTES, dtype=torch.uint8, device="cuda") for k in (s.hidden, s.ffn)}
+    for k, a in act.items():
+        x = torch.randn(k, device="cuda", dtype=torch.float32)
+        b.quantize_q8k(x.data_ptr(), a.data_ptr(), k, 1)
+    out = torch.empty(max(s.ffn * 2, s.hidden), device="cuda", dtype=torch.float32)
+    res = {}
+
+    def timed(weights, reps):
+        """weights: list of (Weight, [device copies]); one unit = one pass over the list."""
+        def launch(i):
+            for w, hs in weights:
+                b.matvec(hs[i % len(hs)], act[w.k].data_ptr(), out.data_ptr(), 1)
+        n = max(len(hs) for _, hs in weights)
+        for i in range(n):
+            launch(i)
+        return _timed_launches(stream, launch, reps)
+
+    # config 0: per call (launch included), and streaming: one launch over `copies` stacked
+    # copies of the panel (copies * 12288 rows, 430 MB), the kernel's sustained bandwidth
+    pk, ps = synth.panel_uniform_codes(g, 2 * s.ffn, s.hidden)
+    w0 = synth.Weight(abi.GT_STQ1_0, s.hidden, 2 * s.ffn,
+                      np.zeros((2 * s.ffn, abi.row_bytes(abi.GT_STQ1_0, s.hidden)), np.uint8), pk, ps, 0, 1)
+    hs = [b.upload(w0) for _ in range(copies)]
+    algo0 = w0.nbytes_device() + (s.hidden // 256) * abi.Q8K_BYTES + 2 * s.ffn * 4
+    t_call = timed([(w0, hs)], copies * passes)
+    for h in hs:
+        b.release(h)
+    nrow = copies * 2 * s.ffn
+    ws = synth.Weight(abi.GT_STQ1_0, s.hidden, nrow, np.zeros((nrow, abi.row_bytes(abi.GT_STQ1_0, s.hidden)), np.uint8),
+                      np.tile(pk, (copies, 1, 1)), np.tile(ps, (copies, 1)), 0, 1)
+    big = torch.empty(nrow, device="cuda", dtype=torch.float32)
+    hb = b.upload(ws)
+
+    def launch_big(_):
+        b.matvec(hb, act[s.hidden].data_ptr(), big.data_ptr(), 1)
+
+    launch_big(0)
+    t_big = _timed_launches(stream, launch_big, 5)
+    b.release(hb)
+    algo_big = ws.nbytes_device() + (s.hidden // 256) * abi.Q8K_BYTES + nrow * 4
+    res["config0"] = dict(unit="call", bytes=algo0, call_us=round(t_call * 1e6, 2),
+                          call_GBs=round(algo0 / t_call / 1e9, 1), call_frac=round(algo0 / t_call / 1e9 / HBM_PEAK_GBS, 4),
+                          stream_rows=nrow, stream_bytes=algo_big, stream_us=round(t_big * 1e6, 2),
+                          stream_GBs=round(algo_big / t_big / 1e9, 1),
+                          stream_frac=round(algo_big / t_big / 1e9 / HBM_PEAK_GBS, 4),
+                          timing="call: HIP events over back-to-back launches rotating 64 copies (launch cost "
+                                 "included); stream: one launch over 64 stacked copies")
+    # configs 1 and 2: one layer's matvec set
+    for name, mode in (("config1", "q2"), ("config2", "q4km")):
+        types = synth.LAYER_TYPES[mode]
+        ws = []
+        for nm, n, k in shapes:
+            w = synth.make_weight(g, types[nm], n, k)
+            ws.append((w, [b.upload(w) for _ in range(copies)]))
+        algo = sum(w.nbytes_device() if w.pk is not None else w.n * w.row_bytes for w, _ in ws)
+        algo += sum((w.k // 256) * abi.Q8K_BYTES + w.n * 4 for w, _ in ws)
+        t = timed(ws, copies * passes)
+        for _, hh in ws:
+            for h in hh:
+                b.release(h)
+        res[name] = dict(unit="layer (7 matvecs)", bytes=algo, us=round(t * 1e6, 2), GBs=round(algo / t / 1e9, 1),
+                         frac=round(algo / t / 1e9 / HBM_PEAK_GBS, 4))
+    return res
+
+
 def host_loop_rate(fm, prompt, n_tokens: int):
     """Decode rate of the reference host's own loop over the drop-in boundary: one
     fused_forward per token with the host embedding in (8 KB H2D), the 120818 logits out (483 KB
@@ -212,6 +294,7 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--no-layer-sets", action="store_true", help="skip the configs 0-2 matvec timings")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the standalone kernel launches used for rocprofv3 counter passes")
     args = ap.parse_args()
@@ -256,6 +339,10 @@ def main():
     log(f"ffn_in kernel: {roof['avg_us']} us, {roof['achieved']} GB/s")
     head = head_roofline(fm, b)
     log(f"head kernel: {head['avg_us']} us, {head['achieved']} GB/s")
+    sets = None
+    if not args.no_layer_sets:
+        sets = layer_sets(b)
+        log(f"layer sets: {sets}")
     cpu = None
     if not args.no_cpu:
         t = time.time()
@@ -279,6 +366,7 @@ def main():
         "roofline": roof,
         "head_roofline": head,
         "host_loop": host,
+        "layer_sets": sets,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
