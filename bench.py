@@ -26,6 +26,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 
 def log(*a):
@@ -207,6 +208,75 @@ def layer_sets(b, copies: int = 64, passes: int = 2):
     return res
 
 
+def gemm_roofline(b, nt: int = 128, copies: int = 8, reps: int = 64):
+    """The prefill GEMM (k_gemm_panel, int8 MFMA) at config 4's widest contraction: 2 x 6144 rows
+    of Q2_0C panel (gate and up stacked), K 2048, one 128-token chunk of Q8_K activations, through
+    hymt2_hip_matvec; HIP events on the backend stream over launches rotating `copies` weight
+    copies. int8 ops per launch = 2 * rows * K * tokens."""
+    import torch
+    from hymt2_amd import abi, synth
+    s = synth.HYMT2_1_8B
+    g = synth.rng(0x6E77)
+    n, k = 2 * s.ffn, s.hidden
+    w = synth.make_weight(g, abi.GT_Q2_0C, n, k)
+    hs = [b.upload(w) for _ in range(copies)]
+    stream = torch.cuda.ExternalStream(b.stream)
+    act = torch.zeros(nt * (k // 256) * abi.Q8K_BYTES, dtype=torch.uint8, device="cuda")
+    x = torch.randn(nt, k, device="cuda", dtype=torch.float32)
+    out = torch.empty(nt * n, device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    b.quantize_q8k(x.data_ptr(), act.data_ptr(), k, nt)
+
+    def launch(i):
+        b.matvec(hs[i % copies], act.data_ptr(), out.data_ptr(), nt)
+
+    for i in range(copies):
+        launch(i)
+    avg_s = _timed_launches(stream, launch, reps)
+    for h in hs:
+        b.release(h)
+    ops = 2.0 * n * k * nt
+    return dict(bound="mfma", achieved=round(ops / avg_s / 1e12, 1), peak=INT8_PEAK_TOPS, unit="TOP/s",
+                frac=round(ops / avg_s / 1e12 / INT8_PEAK_TOPS, 4), avg_us=round(avg_s * 1e6, 2),
+                ops_per_launch=int(ops), kernel="k_gemm_panel (int8 MFMA 16x16x64): 12288x2048 Q2_0C panel x "
+                f"{nt} tokens", timing=f"HIP events on the backend stream over {reps} launches rotating {copies} "
+                                       f"weight copies")
+
+
+def config4(b, seed: int = 4, n_prompt: int = 1024, n_gen: int = 256, chunk: int = 128):
+    """the 1.8B-shaped model with Q2_0C weights, a 1024-token prompt of random
+    ids in 128-token chunks on the device (hymt2_hip_generate_chunked: int8-MFMA GEMMs, causal GQA
+    attention over the growing KV cache, LM head + argmax on the last position), then 256 greedy
+    decode tokens. Prefill and decode are timed separately with HIP events on the backend stream.
+    MFMA utilisation of the prefill = int8 ops of all layer contractions / (time x peak)."""
+    from hymt2_amd import lib, synth
+    shape = synth.ModelShape(ctx=n_prompt + n_gen + 64)
+    t = time.time()
+    model = synth.make_model(shape, mode="q2", seed=seed)
+    log(f"config 4 model built in {time.time() - t:.1f} s")
+    fm = lib.FusedModel(b, model)
+    prompt = synth.rand_prompt(synth.rng(4096), n_prompt, shape.vocab)
+    fm.generate_device(prompt[:chunk + 5], 4, chunk=chunk)  # warm: kernels loaded, graphs captured
+    ids, st = fm.generate_device(prompt, n_gen, chunk=chunk)
+    _, st1 = fm.generate_device(prompt, 2, chunk=1)          # the same prompt one position per step
+    weights = sum(L[nm].n * L[nm].k for L in model["layers"] for nm in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"))
+    ops = 2.0 * weights * n_prompt
+    pre_s = st.prefill_ms / 1e3
+    wb = synth.model_weight_bytes(model)
+    avg_pos = n_prompt + (n_gen - 1) / 2.0
+    tok_bytes = wb["layers"] + wb["head"] + 2 * shape.n_layer * shape.kvdim * 2 * (avg_pos + 1)
+    dec_tok_s = st.decode_steps / (st.decode_ms / 1e3)
+    fm.close()
+    return dict(workload=f"config4: Hy-MT2-1.8B-shaped Q2_0C, {n_prompt}-token random prompt in {chunk}-token "
+                         f"chunks, then {n_gen} greedy tokens (device loop)",
+                prefill_tok_s=round(n_prompt / pre_s, 1), prefill_ms=round(st.prefill_ms, 3),
+                prefill_int8_ops=int(ops), prefill_mfma_util=round(ops / pre_s / 1e12 / INT8_PEAK_TOPS, 4),
+                prefill_stepwise_tok_s=round(st1.prefill_steps / (st1.prefill_ms / 1e3), 1),
+                decode_tok_s=round(dec_tok_s, 2), decode_bytes_per_token=int(tok_bytes),
+                decode_effective_GBs=round(tok_bytes * dec_tok_s / 1e9, 1),
+                distinct_ids=len(set(ids.tolist())))
+
+
 def host_loop_rate(fm, prompt, n_tokens: int):
     """Decode rate of the reference host's own loop over the drop-in boundary: one
     fused_forward per token with the host embedding in (8 KB H2D), the 120818 logits out (483 KB
@@ -295,6 +365,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--no-layer-sets", action="store_true", help="skip the configs 0-2 matvec timings")
+    ap.add_argument("--no-config4", action="store_true", help="skip the config 4 chunked-prefill run")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the standalone kernel launches used for rocprofv3 counter passes")
     args = ap.parse_args()
@@ -343,6 +414,11 @@ def main():
     if not args.no_layer_sets:
         sets = layer_sets(b)
         log(f"layer sets: {sets}")
+    c4 = None
+    if not args.no_config4:
+        c4 = config4(b)
+        c4["gemm_roofline"] = gemm_roofline(b)
+        log(f"config 4: {c4}")
     cpu = None
     if not args.no_cpu:
         t = time.time()
@@ -367,6 +443,7 @@ def main():
         "head_roofline": head,
         "host_loop": host,
         "layer_sets": sets,
+        "config4_prefill": c4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

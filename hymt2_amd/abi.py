@@ -16,6 +16,7 @@ import ctypes as C
 
 QK_K = 256
 MAX_BATCH = 16  # src/internal.h:12
+MAX_CHUNK = 128  # tokens per call the backend accepts (HYMT2_HIP_MAX_CHUNK)
 Q8K_BYTES = 576
 
 # GGUF tensor type codes (src/internal.h:46)

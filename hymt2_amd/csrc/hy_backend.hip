@@ -4,6 +4,7 @@
 // host synchronisation per fused_forward, and a device-resident greedy loop.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -54,7 +55,7 @@ struct Fused {
     int n_layer = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, hdim = 0, qdim = 0, kvdim = 0, ctx = 0,
         rope_half = 0;
     float eps = 0.f;
-    char* in_dev = nullptr;   // [MAX_BATCH * hidden floats][pos int]
+    char* in_dev = nullptr;   // [pos int, padded to 64 B][HY_MAX_CHUNK * hidden floats]
     char* in_host = nullptr;  // pinned staging of the same layout
     float* d_h = nullptr;
     int* d_pos = nullptr;
@@ -69,6 +70,9 @@ struct Fused {
     int ids_cap = 0;
     int gen_total = 0;   // positions of the current device loop (0: no loop begun)
     int gen_steps = 0;   // steps enqueued so far
+    int gen_prompt = 0, gen_vocab = 0;
+    const uint16_t* gen_e16 = nullptr;
+    const float* gen_e32 = nullptr;
     hipGraphExec_t g_fwd = nullptr, g_step = nullptr;
     std::vector<const void*> sig_fwd, sig_step;
     float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
@@ -318,6 +322,44 @@ static bool run_mv1(Ctx* c, const JobSpec* js, int njobs, bool pair, const MvOpt
     return true;
 }
 
+// Several tokens: panel weights go to the int8-MFMA GEMM once a chunk is larger than the
+// reference's batch; otherwise (and for Q4_K / Q6_K) the general matvec kernel runs over groups of
+// at most HY_MAX_BATCH tokens. Both give every token the single-token result.
+static bool run_multi(Ctx* c, const JobSpec* js, int njobs, bool pair, int nt, const MvOpts& o) {
+    if (nt > HY_MAX_BATCH && o.pro == PRO_NONE) {
+        GemmLaunch G;
+        memset(&G, 0, sizeof G);
+        G.njobs = njobs;
+        G.pair = pair ? 1 : 0;
+        G.nt = nt;
+        G.act = o.act;
+        for (int j = 0; j < njobs; j++) {
+            G.job[j].W = js[j].w->mw;
+            G.job[j].out = js[j].out;
+            G.job[j].ldo = js[j].ldo;
+            G.job[j].epi = js[j].epi;
+        }
+        const hipError_t e = launch_gemm_panel(G, c->s);
+        if (e != hipErrorNotSupported) {
+            HIPCHK(c, e);
+            return true;
+        }
+    }
+    if (nt <= HY_MAX_BATCH || o.pro != PRO_NONE) return run_matvec(c, js, njobs, pair, nt, o);
+    const int nb = js[0].w->mw.nb;
+    for (int t0 = 0; t0 < nt; t0 += HY_MAX_BATCH) {
+        JobSpec g[kMaxJobs];
+        for (int j = 0; j < njobs; j++) {
+            g[j] = js[j];
+            g[j].out = js[j].out + (size_t)t0 * js[j].ldo;
+        }
+        MvOpts og = o;
+        og.act = o.act + (size_t)t0 * nb;
+        if (!run_matvec(c, g, njobs, pair, std::min(HY_MAX_BATCH, nt - t0), og)) return false;
+    }
+    return true;
+}
+
 static bool ensure_scratch(Ctx* c, size_t act_bytes, size_t out_bytes) {
     if (act_bytes > c->act_cap) {
         if (c->act) (void)hipFree(c->act);
@@ -343,7 +385,7 @@ static bool ensure_scratch(Ctx* c, size_t act_bytes, size_t out_bytes) {
 static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, int cnt, const hymt2_q8k_block* xq,
                        int nt) {
     Ctx* c = static_cast<Ctx*>(impl);
-    if (!c || c->broken || cnt < 1 || nt < 1 || nt > HY_MAX_BATCH || !xq) return false;
+    if (!c || c->broken || cnt < 1 || nt < 1 || nt > HY_MAX_CHUNK || !xq) return false;
     const DW* w0 = reinterpret_cast<const DW*>(ws[0]);
     const int nb = w0->mw.nb;
     size_t out_total = 0;
@@ -364,7 +406,7 @@ static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, in
         JobSpec j{w, c->out + off, w->mw.n, EPI_STORE};
         MvOpts o;
         o.act = static_cast<const HyQ8K*>(c->act);
-        if (!run_matvec(c, &j, 1, false, nt, o)) {
+        if (!run_multi(c, &j, 1, false, nt, o)) {
             c->broken = true;
             return false;
         }
@@ -454,8 +496,8 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
     f->ctx = a->ctx;
     f->rope_half = a->rope_half;
     f->eps = a->eps;
-    const size_t B = HY_MAX_BATCH, H = a->hidden, F = a->ffn, Q = a->qdim, KV = a->kvdim;
-    f->in_bytes = B * H * 4 + 64;
+    const size_t B = HY_MAX_CHUNK, H = a->hidden, F = a->ffn, Q = a->qdim, KV = a->kvdim;
+    f->in_bytes = 64 + B * H * 4;
     bool ok = dalloc(c, &f->in_dev, f->in_bytes) && hipHostMalloc(&f->in_host, f->in_bytes, 0) == hipSuccess;
     ok = ok && dalloc(c, &f->q, B * Q * 4) && dalloc(c, &f->k, B * KV * 4) && dalloc(c, &f->v, B * KV * 4) &&
          dalloc(c, &f->ao, B * Q * 4) && dalloc(c, &f->g, B * F * 4) && dalloc(c, &f->u, B * F * 4) &&
@@ -470,8 +512,8 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
         free_fused(f);
         return false;
     }
-    f->d_h = reinterpret_cast<float*>(f->in_dev);
-    f->d_pos = reinterpret_cast<int*>(f->in_dev + B * H * 4);
+    f->d_pos = reinterpret_cast<int*>(f->in_dev);
+    f->d_h = reinterpret_cast<float*>(f->in_dev + 64);
     c->f = f;
     if (!copy_params(c, a)) return false;
     HIPCHK(c, hipMemset(f->kc, 0, (size_t)a->n_layer * a->ctx * KV * 2));
@@ -528,7 +570,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, attn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
             o1.act = f->act_h;
         }
-        if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_matvec(c, qkv, 3, false, nt, o1))) return false;
+        if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_multi(c, qkv, 3, false, nt, o1))) return false;
         // single token: one workgroup per head (k_attn1), fp32 output quantized by the o matvec;
         // else the 256-output-block attention kernel, else the general path
         const bool head_attn = nt == 1 && (f->hdim == 64 || f->hdim == 128) && f->ctx <= kA1MaxCtx;
@@ -611,7 +653,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             o2.x = f->ao;
             o2.act = nullptr;
         }
-        if (!(nt == 1 ? run_mv1(c, &o, 1, false, o2) : run_matvec(c, &o, 1, false, nt, o2))) return false;
+        if (!(nt == 1 ? run_mv1(c, &o, 1, false, o2) : run_multi(c, &o, 1, false, nt, o2))) return false;
         // ---- feed-forward block
         const bool pair = wg->mw.kind == wu->mw.kind && wg->mw.n == wu->mw.n;
         JobSpec gu[2] = {{wg, f->g, F, EPI_STORE}, {wu, f->u, F, EPI_STORE}};
@@ -626,7 +668,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, ffn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
             o3.act = f->act_h;
         }
-        if (!(nt == 1 ? run_mv1(c, gu, 2, pair, o3) : run_matvec(c, gu, 2, pair, nt, o3))) return false;
+        if (!(nt == 1 ? run_mv1(c, gu, 2, pair, o3) : run_multi(c, gu, 2, pair, nt, o3))) return false;
         if (!pair) HIPCHK(c, launch_silu_mul(f->g, f->u, nt * F, c->s));
         JobSpec dn{wd, f->d_h, H, EPI_ADD};
         MvOpts o4;
@@ -638,7 +680,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_quantize_q8k(f->g, F, f->act_f, F, nt, c->s));
             o4.act = f->act_f;
         }
-        if (!(nt == 1 ? run_mv1(c, &dn, 1, false, o4) : run_matvec(c, &dn, 1, false, nt, o4))) return false;
+        if (!(nt == 1 ? run_mv1(c, &dn, 1, false, o4) : run_multi(c, &dn, 1, false, nt, o4))) return false;
     }
     return true;
 }
@@ -713,17 +755,17 @@ static bool capture(Ctx* c, hipGraphExec_t* exec, Fn&& body) {
 // memory, uploaded together with h in one copy.
 static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
     Ctx* c = static_cast<Ctx*>(impl);
-    if (!c || c->broken || !a || !c->f || !same_shape(c->f, a) || a->nt < 1 || a->nt > HY_MAX_BATCH || !a->h ||
+    if (!c || c->broken || !a || !c->f || !same_shape(c->f, a) || a->nt < 1 || a->nt > HY_MAX_CHUNK || !a->h ||
         a->pos0 < 0 || a->pos0 + a->nt > c->f->ctx)
         return false;
     Fused* f = c->f;
     const int nt = a->nt;
     const size_t hbytes = (size_t)nt * f->hidden * 4;
     const bool logits = a->want_logits && a->outw && a->logits;
-    memcpy(f->in_host, a->h, hbytes);
+    memcpy(f->in_host + 64, a->h, hbytes);
     if (nt == 1) {
-        memcpy(f->in_host + (size_t)HY_MAX_BATCH * f->hidden * 4, &a->pos0, 4);
-        HIPCHK(c, hipMemcpyAsync(f->in_dev, f->in_host, f->in_bytes, hipMemcpyHostToDevice, c->s));
+        memcpy(f->in_host, &a->pos0, 4);
+        HIPCHK(c, hipMemcpyAsync(f->in_dev, f->in_host, 64 + hbytes, hipMemcpyHostToDevice, c->s));
         if (logits && !ensure_logits(c, f, dw(a->outw)->mw.n)) return false;
         std::vector<const void*> sig = weight_sig(a);
         sig.push_back(reinterpret_cast<const void*>((uintptr_t)logits));
@@ -740,7 +782,7 @@ static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
         }
         HIPCHK(c, hipGraphLaunch(f->g_fwd, c->s));
     } else {
-        HIPCHK(c, hipMemcpyAsync(f->d_h, f->in_host, hbytes, hipMemcpyHostToDevice, c->s));
+        HIPCHK(c, hipMemcpyAsync(f->d_h, f->in_host + 64, hbytes, hipMemcpyHostToDevice, c->s));
         if (!enqueue_layers(c, a, nt, a->pos0, nullptr) || (logits && !enqueue_head(c, a, nt, false, 0))) {
             c->broken = true;
             return false;
@@ -852,11 +894,11 @@ int hymt2_hip_quantize_q8k(void* impl, const float* x, void* act, int k, int nt)
 int hymt2_hip_matvec(void* impl, hy_dweight* w, const void* act, float* out, int nt) {
     Ctx* c = static_cast<Ctx*>(impl);
     const DW* d = dw(w);
-    if (!c || c->broken || !d || nt < 1 || nt > HY_MAX_BATCH || !quant_kind(d->mw.kind)) return -1;
+    if (!c || c->broken || !d || nt < 1 || nt > HY_MAX_CHUNK || !quant_kind(d->mw.kind)) return -1;
     JobSpec j{d, out, d->mw.n, EPI_STORE};
     MvOpts o;
     o.act = static_cast<const HyQ8K*>(act);
-    return (nt == 1 ? run_mv1(c, &j, 1, false, o) : run_matvec(c, &j, 1, false, nt, o)) ? 0 : -2;
+    return (nt == 1 ? run_mv1(c, &j, 1, false, o) : run_multi(c, &j, 1, false, nt, o)) ? 0 : -2;
 }
 
 int hymt2_hip_selftest_f16(void* impl, const uint16_t* src, float* dst, int n) {
@@ -929,7 +971,7 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     }
     // start state: ids[0..n_prompt) = prompt, pos = 0, key = 0, h = embedding of ids[0]
     memset(f->in_host, 0, f->in_bytes);
-    const size_t pos_off = (size_t)HY_MAX_BATCH * f->hidden * 4;
+    const size_t pos_off = 0;
     if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->in_dev + pos_off, f->in_host + pos_off, 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->key, f->in_host, 8, hipMemcpyHostToDevice, c->s) != hipSuccess ||
@@ -941,6 +983,45 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     }
     f->gen_total = n_total;
     f->gen_steps = 0;
+    f->gen_prompt = n_prompt;
+    f->gen_vocab = vocab_out;
+    f->gen_e16 = e16;
+    f->gen_e32 = e32;
+    return 0;
+}
+
+int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !c->f || !c->f->gen_total || !shape || !shape->layers) return -1;
+    Fused* f = c->f;
+    if (f->gen_steps != 0 || chunk < 1 || chunk > HY_MAX_CHUNK || !same_shape(f, shape)) {
+        set_err(c, "gen_prefill: needs a fresh loop of the same shape and 1 <= chunk <= %d", HY_MAX_CHUNK);
+        return -2;
+    }
+    const std::vector<const void*> sig = weight_sig(shape);
+    if (f->sig_step.size() < sig.size() || !std::equal(sig.begin(), sig.end(), f->sig_step.begin())) {
+        set_err(c, "gen_prefill: weights differ from the ones gen_begin captured");
+        return -2;
+    }
+    const int np = f->gen_prompt;
+    for (int i = 0; i < np; i += chunk) {
+        const int nt = std::min(chunk, np - i);
+        if (launch_embed_rows(f->ids, i, nt, f->gen_e16, f->gen_e32, f->d_h, f->hidden, c->s) != hipSuccess ||
+            !enqueue_layers(c, shape, nt, i, nullptr) ||
+            (i + nt == np && !enqueue_head(c, shape, nt, true, f->gen_vocab))) {
+            c->broken = true;
+            return -3;
+        }
+    }
+    // position np - 1 has been processed: the finishing kernel records the first generated id,
+    // embeds it and advances the step counter to np, where the step graph continues
+    FinishArgs fa{f->key, f->ids, f->d_pos, np, f->gen_e16, f->gen_e32, f->d_h, f->hidden, f->gen_total};
+    if (launch_set_int(f->d_pos, np - 1, c->s) != hipSuccess || launch_finish(fa, c->s) != hipSuccess) {
+        set_err(c, "gen_prefill: launch failed");
+        c->broken = true;
+        return -3;
+    }
+    f->gen_steps = np;
     return 0;
 }
 
@@ -976,14 +1057,15 @@ int hymt2_hip_gen_read(void* impl, int* ids, int first, int count) {
     return count;
 }
 
-int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
-                       int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
+int hymt2_hip_generate_chunked(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out,
+                               const int* prompt, int n_prompt, int n_gen, int chunk, int* out_ids,
+                               hymt2_gen_stats* stats) {
     Ctx* c = static_cast<Ctx*>(impl);
-    if (!c || !out_ids || n_gen < 1) return -1;
+    if (!c || !out_ids || n_gen < 1 || chunk < 1) return -1;
     int rc = hymt2_hip_gen_begin(impl, shape, embd, vocab_out, prompt, n_prompt, n_prompt + n_gen);
     if (rc) return rc;
     (void)hipEventRecord(c->ev[0], c->s);
-    if ((rc = hymt2_hip_gen_steps(impl, n_prompt))) return rc;
+    if ((rc = chunk > 1 ? hymt2_hip_gen_prefill(impl, shape, chunk) : hymt2_hip_gen_steps(impl, n_prompt))) return rc;
     (void)hipEventRecord(c->ev[1], c->s);
     if ((rc = hymt2_hip_gen_steps(impl, n_gen - 1))) return rc;
     (void)hipEventRecord(c->ev[2], c->s);
@@ -998,6 +1080,11 @@ int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* em
         stats->decode_steps = n_gen - 1;
     }
     return n_gen;
+}
+
+int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
+                       int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
+    return hymt2_hip_generate_chunked(impl, shape, embd, vocab_out, prompt, n_prompt, n_gen, 1, out_ids, stats);
 }
 
 int hymt2_hip_head(void* impl, hy_dweight* w, const float* h, const float* norm_w, float eps, float* logits,

@@ -13,6 +13,10 @@
 
 #define HY_QK 256
 #define HY_MAX_BATCH 16  // src/internal.h:12
+// Tokens per forward this backend accepts (fused_forward, matmul, the device prefill): the
+// reference host sends at most HY_MAX_BATCH; a host built with a larger MAX_BATCH (128-token
+// prefill chunks) may send up to this many.
+#define HY_MAX_CHUNK 128
 
 // Q8_K activation block, byte-identical to the reference's q8k_block (src/internal.h:29-41).
 struct alignas(64) HyQ8K {

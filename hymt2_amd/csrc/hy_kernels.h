@@ -89,6 +89,28 @@ struct Mv1Launch {
 // launch_matvec).
 hipError_t launch_mv1(Mv1Launch& L, int pro, hipStream_t s);
 
+// Multi-token GEMM of panel weights on int8 MFMA (k_gemm_panel, hy_prefill.hip): out[t * ldo + r]
+// for nt tokens of Q8_K activations [nt][K / 256], bit-identical to nt single-token matvecs.
+struct GemmJob {
+    MvWeight W;
+    float* out;
+    int ldo;
+    int epi;         // EPI_STORE / EPI_ADD
+    int tile_begin;  // first row tile of this job in the grid (set by the launcher)
+};
+
+struct GemmLaunch {
+    GemmJob job[kMaxJobs];
+    int njobs;
+    int pair;              // job[0] = gate, job[1] = up of equal shape: job[0].out = silu(g) * u
+    int nt;
+    const HyQ8K* act;      // [nt][nb]
+    int nb;                // set by the launcher
+};
+// hipErrorNotSupported for weights that are not panels of one K (the caller then uses
+// launch_matvec).
+hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s);
+
 struct AttnArgs {
     float* q;              // [nt][qdim]
     const float* k;        // [nt][kvdim]
@@ -174,6 +196,10 @@ struct FinishArgs {
 hipError_t launch_finish(const FinishArgs& a, hipStream_t s);
 hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16, const float* embd32, float* h,
                         int H, hipStream_t s);
+
+hipError_t launch_embed_rows(const int* ids, int first, int nt, const uint16_t* embd16, const float* embd32,
+                             float* h, int H, hipStream_t s);
+hipError_t launch_set_int(int* p, int v, hipStream_t s);
 
 hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
 hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s);

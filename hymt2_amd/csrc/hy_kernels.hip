@@ -982,6 +982,25 @@ hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16,
     return hipGetLastError();
 }
 
+// Embedding rows of nt consecutive ids (ids[first + t] -> h[t]), for a prefill chunk.
+__global__ __launch_bounds__(256) void k_embed_rows(const int* ids, int first, const uint16_t* e16, const float* e32,
+                                                    float* h, int H) {
+    embed_row(e16, e32, ids[first + blockIdx.x], h + (size_t)blockIdx.x * H, H);
+}
+
+hipError_t launch_embed_rows(const int* ids, int first, int nt, const uint16_t* embd16, const float* embd32,
+                             float* h, int H, hipStream_t s) {
+    k_embed_rows<<<nt, 256, 0, s>>>(ids, first, embd16, embd32, h, H);
+    return hipGetLastError();
+}
+
+__global__ void k_set_int(int* p, int v) { *p = v; }
+
+hipError_t launch_set_int(int* p, int v, hipStream_t s) {
+    k_set_int<<<1, 1, 0, s>>>(p, v);
+    return hipGetLastError();
+}
+
 // =========================================================================== small kernels
 
 // Greedy argmax over rows [0, n) of fp32 logits into a 64-bit key (first index on ties).

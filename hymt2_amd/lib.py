@@ -58,6 +58,9 @@ def load():
         "hymt2_hip_generate": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i, vp, C.POINTER(GenStats)]),
         "hymt2_hip_gen_begin": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i]),
         "hymt2_hip_gen_steps": (i, [vp, i]),
+        "hymt2_hip_gen_prefill": (i, [vp, C.POINTER(abi.FusedArgs), i]),
+        "hymt2_hip_generate_chunked": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i, i, vp,
+                                           C.POINTER(GenStats)]),
         "hymt2_hip_gen_read": (i, [vp, vp, i, i]),
         "hymt2_hip_head": (i, [vp, vp, vp, vp, C.c_float, vp, i, vp]),
         "hymt2_hip_ffn_in": (i, [vp, vp, vp, vp, vp, C.c_float, vp]),
@@ -72,7 +75,8 @@ def load():
 EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops", "hymt2_hip_last_error",
            "hymt2_hip_abi_layout", "hymt2_hip_stream", "hymt2_hip_quantize_q8k", "hymt2_hip_matvec",
            "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_selftest_sqsum", "hymt2_hip_generate", "hymt2_hip_gen_begin",
-           "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in"]
+           "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in",
+           "hymt2_hip_gen_prefill", "hymt2_hip_generate_chunked"]
 
 
 def abi_layout() -> dict:
@@ -178,7 +182,7 @@ class FusedModel:
                                   h=None, logits=None)
         if not backend.ops.fused_prepare(backend.impl, C.byref(self.args)):
             raise RuntimeError(f"fused_prepare failed: {backend.last_error()}")
-        self.h = np.zeros((abi.MAX_BATCH, s.hidden), dtype=np.float32)
+        self.h = np.zeros((abi.MAX_CHUNK, s.hidden), dtype=np.float32)
         self.logits = np.zeros(model["outw"].n, dtype=np.float32)
         self.vocab_out = model["vocab_out"]
 
@@ -192,7 +196,7 @@ class FusedModel:
         raise ValueError("host embedding supports F16/F32 tables")
 
     def forward(self, toks, pos0: int, want_logits: bool = True):
-        """One fused_forward of len(toks) <= MAX_BATCH tokens; returns logits or None."""
+        """One fused_forward of len(toks) <= MAX_CHUNK tokens; returns logits or None."""
         nt = len(toks)
         self.h[:nt] = self.embed(toks)
         a = self.args
@@ -223,15 +227,17 @@ class FusedModel:
             pos += 1
         return np.array(out, dtype=np.int32)
 
-    def generate_device(self, prompt, n_gen: int):
-        """Greedy loop entirely on the device; returns (ids, GenStats)."""
+    def generate_device(self, prompt, n_gen: int, chunk: int = 1):
+        """Greedy loop entirely on the device; the prompt runs as single-token steps (chunk 1)
+        or as chunks of up to `chunk` positions. Returns (ids, GenStats)."""
         if self.embd_dev is None:
             raise ValueError("device generation needs an F16/F32 embedding table")
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
         st = GenStats()
-        rc = self.b.L.hymt2_hip_generate(self.b.impl, C.byref(self.args), self.embd_dev, self.vocab_out,
-                                         prompt.ctypes.data, len(prompt), n_gen, out.ctypes.data, C.byref(st))
+        rc = self.b.L.hymt2_hip_generate_chunked(self.b.impl, C.byref(self.args), self.embd_dev, self.vocab_out,
+                                                 prompt.ctypes.data, len(prompt), n_gen, chunk, out.ctypes.data,
+                                                 C.byref(st))
         if rc != n_gen:
             raise RuntimeError(f"hymt2_hip_generate failed ({rc}): {self.b.last_error()}")
         return out, st
@@ -244,6 +250,11 @@ class FusedModel:
                                           self._prompt.ctypes.data, len(self._prompt), n_total)
         if rc != 0:
             raise RuntimeError(f"gen_begin failed ({rc}): {self.b.last_error()}")
+
+    def gen_prefill(self, chunk: int):
+        rc = self.b.L.hymt2_hip_gen_prefill(self.b.impl, C.byref(self.args), chunk)
+        if rc != 0:
+            raise RuntimeError(f"gen_prefill failed ({rc}): {self.b.last_error()}")
 
     def gen_steps(self, n: int):
         rc = self.b.L.hymt2_hip_gen_steps(self.b.impl, n)

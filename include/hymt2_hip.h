@@ -27,6 +27,11 @@ extern "C" {
 
 #define HYMT2_HIP_API __attribute__((visibility("default")))
 
+/* Tokens per call that matmul and fused_forward accept. The reference host sends at most
+ * MAX_BATCH = 16 (src/internal.h:12); a host built with MAX_BATCH up to 128 can send 128-token
+ * prefill chunks, which run on the int8-MFMA GEMM. */
+#define HYMT2_HIP_MAX_CHUNK 128
+
 /* ---------------------------------------------------------------- reference ABI mirrors */
 
 typedef struct hy_device hy_device;   /* opaque, owned by the host (src/device.c:18-24) */
@@ -121,7 +126,8 @@ HYMT2_HIP_API void *hymt2_hip_stream(void *impl);
  * 0 on success, negative on error):
  *   quantize_q8k: x[nt][k] fp32 -> act[nt][k/256] q8k_block (quantize_q8k, src/kernels.c:128)
  *   matvec:       out[t*n + r] = row r of an uploaded weight . act[t] (matmul_rows,
- *                 src/kernels.c:1241), panel / Q4_K / Q6_K weights, 1 <= nt <= 16 */
+ *                 src/kernels.c:1241), panel / Q4_K / Q6_K weights, 1 <= nt <= 128; above 16
+ *                 tokens panel weights run on the int8-MFMA GEMM */
 HYMT2_HIP_API int hymt2_hip_quantize_q8k(void *impl, const float *x_dev, void *act_dev, int k, int nt);
 HYMT2_HIP_API int hymt2_hip_matvec(void *impl, hy_dweight *w, const void *act_dev, float *out_dev, int nt);
 
@@ -147,8 +153,15 @@ HYMT2_HIP_API int hymt2_hip_selftest_sqsum(void *impl, const float *x_dev, int n
  *   gen_steps: enqueues n steps (asynchronous; replays of one captured graph); at most
  *              n_total - 1 steps in all.
  *   gen_read:  waits for the stream and copies ids[first .. first + count).
+ *   gen_prefill: instead of the first n_prompt steps, runs the whole prompt as chunks of up to
+ *              `chunk` (<= 128) positions through the multi-token forward (int8-MFMA GEMMs
+ *              for panel weights, causal attention over the growing KV cache), then the LM
+ *              head on the last prompt position; the loop continues with gen_steps exactly as
+ *              after n_prompt steps (bit-identical ids, logits and KV cache). The prompt pass
+ *              of the reference's gen_ids (src/model.c:928-937, forward_tokens :904-909).
  *   generate:  begin + n_prompt steps + (n_gen - 1) steps + read of the n_gen generated ids,
- *              with HIP-event timings of the two phases. Returns n_gen. */
+ *              with HIP-event timings of the two phases. Returns n_gen.
+ *   generate_chunked: the same with the prompt through gen_prefill(chunk) (chunk 1: steps). */
 typedef struct hymt2_gen_stats {
     double prefill_ms;  /* steps that consume prompt ids */
     double decode_ms;   /* steps that consume generated ids */
@@ -157,10 +170,14 @@ typedef struct hymt2_gen_stats {
 HYMT2_HIP_API int hymt2_hip_gen_begin(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
                                       const int *prompt, int n_prompt, int n_total);
 HYMT2_HIP_API int hymt2_hip_gen_steps(void *impl, int n);
+HYMT2_HIP_API int hymt2_hip_gen_prefill(void *impl, const hymt2_fused_args *shape, int chunk);
 HYMT2_HIP_API int hymt2_hip_gen_read(void *impl, int *ids, int first, int count);
 HYMT2_HIP_API int hymt2_hip_generate(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
                                      const int *prompt, int n_prompt, int n_gen, int *out_ids,
                                      hymt2_gen_stats *stats);
+HYMT2_HIP_API int hymt2_hip_generate_chunked(void *impl, const hymt2_fused_args *shape, hy_dweight *embd,
+                                             int vocab_out, const int *prompt, int n_prompt, int n_gen, int chunk,
+                                             int *out_ids, hymt2_gen_stats *stats);
 
 /* LM head on device pointers (enqueued on the context stream): logits[r] = row r of an
  * uploaded F16/F32 weight . rmsnorm(h; norm_w, eps), each row summed sequentially in the

@@ -19,14 +19,20 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
+# torch fills and copies on its own stream, the backend on the context stream: each helper
+# waits for its torch work before the tensor is handed to the backend.
 def dev(a):
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+    t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+    torch.cuda.synchronize()
+    return t
 
 
 def empty_f32(n):
     import torch
-    return torch.zeros(n, dtype=torch.float32, device="cuda:0")
+    t = torch.zeros(n, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    return t
 
 
 def sync():
@@ -223,6 +229,87 @@ def test_per_op_matmul_groups(backend):
             backend.release(h)
 
 
+# ----------------------------------------------------------------------------- prefill GEMM
+
+GEMM_SHAPES = [
+    (abi.GT_STQ1_0, 3072, 2048),  # qkv of the 1.8B layer
+    (abi.GT_Q2_0C, 2048, 6144),   # config 4: down
+    (abi.GT_STQ1_0, 129, 512),    # ragged rows (row tiles of 32 / 64)
+    (abi.GT_Q2_0C, 1, 256),       # one row, one block
+    (abi.GT_STQ1_0, 100, 1536),
+]
+
+
+@pytest.mark.parametrize("gt,n,k", GEMM_SHAPES)
+def test_gemm_vs_oracle(backend, gt, n, k):
+    """Chunks above 16 tokens run panel weights on the int8-MFMA GEMM (k_gemm_panel): every
+    token's row equals panel_rows_scalar (src/kernels.c:565-581) bit for bit, for token counts
+    that fill, straddle and undershoot the 64-token tiles."""
+    g = synth.rng(gt * 11 + n + k)
+    w = synth.make_weight(g, gt, n, k)
+    for nt in (17, 64, 77, 128):
+        x = synth.activations(g, nt, k)
+        out, xq = run_matvec(backend, w, x)
+        assert np.array_equal(bits(out), bits(O.matvec(w, x, xq, nt))), f"nt={nt}"
+
+
+def test_gemm_full_gate_up_vs_single_token(backend):
+    """Config 4's widest contraction (2 x 6144 rows, K 2048, 128 tokens): the GEMM equals 128
+    single-token decode-matvec calls on the same activations (each pinned to the oracle by
+    test_matvec_vs_oracle), and the oracle on a sample of tokens."""
+    g = synth.rng(0x6E77)
+    n, k, nt = 12288, 2048, 128
+    w = synth.make_weight(g, abi.GT_Q2_0C, n, k)
+    x = synth.activations(g, nt, k)
+    x[5] *= 1e-3   # small and large activation scales
+    x[77] *= 50.0
+    h = backend.upload(w)
+    try:
+        act, xq = q8k_dev(backend, x)
+        out = empty_f32(nt * n)
+        one = empty_f32(nt * n)
+        backend.matvec(h, act.data_ptr(), out.data_ptr(), nt)
+        for t in range(nt):
+            backend.matvec(h, act.data_ptr() + t * (k // 256) * abi.Q8K_BYTES, one.data_ptr() + t * n * 4, 1)
+        sync()
+        got = out.cpu().numpy().reshape(nt, n)
+        assert np.array_equal(bits(got), bits(one.cpu().numpy().reshape(nt, n)))
+        nb = k // 256
+        for t in (0, 5, 77, 127):
+            xt = np.ascontiguousarray(xq[t * nb:(t + 1) * nb])
+            assert np.array_equal(bits(got[t]), bits(O.matvec(w, x[t:t + 1], xt, 1)[0])), f"t={t}"
+    finally:
+        backend.release(h)
+
+
+@pytest.mark.parametrize("gt", [abi.GT_Q4_K, abi.GT_Q6_K])
+def test_multi_token_non_panel_groups(backend, gt):
+    """Q4_K / Q6_K chunks above 16 tokens run the general matvec over groups of 16."""
+    g = synth.rng(gt + 500)
+    w = synth.make_weight(g, gt, 300, 2048)
+    x = synth.activations(g, 45, 2048)
+    out, xq = run_matvec(backend, w, x)
+    assert np.array_equal(bits(out), bits(O.matvec(w, x, xq, 45)))
+
+
+def test_per_op_matmul_128_tokens(backend):
+    """matmul() with a 128-token chunk (a host built with MAX_BATCH = 128): panel weights on the
+    GEMM, a Q6_K weight of the same group on the general kernel."""
+    g = synth.rng(78)
+    ws = [synth.make_weight(g, abi.GT_STQ1_0, 512, 1024), synth.make_weight(g, abi.GT_Q2_0C, 256, 1024),
+          synth.make_weight(g, abi.GT_Q6_K, 128, 1024)]
+    hs = [backend.upload(w) for w in ws]
+    try:
+        x = synth.activations(g, 128, 1024)
+        xq = O.quantize_q8k(x)
+        outs = backend.matmul(hs, [w.n for w in ws], xq, 128)
+        for w, o in zip(ws, outs):
+            assert np.array_equal(bits(o), bits(O.matvec(w, x, xq, 128)))
+    finally:
+        for h in hs:
+            backend.release(h)
+
+
 # ----------------------------------------------------------------------------- LM head
 
 @pytest.mark.parametrize("gt,n", [(abi.GT_F16, 120818), (abi.GT_F16, 1000), (abi.GT_F32, 777)])
@@ -288,14 +375,14 @@ def test_entry_points_reject_bad_arguments(backend):
     h = backend.upload(w)
     try:
         act, _ = q8k_dev(backend, synth.activations(g, 1, 512))
-        out = empty_f32(64 * 17)
+        out = empty_f32(64 * 129)
         assert L.hymt2_hip_matvec(backend.impl, h, act.data_ptr(), out.data_ptr(), 0) < 0
-        assert L.hymt2_hip_matvec(backend.impl, h, act.data_ptr(), out.data_ptr(), 17) < 0
+        assert L.hymt2_hip_matvec(backend.impl, h, act.data_ptr(), out.data_ptr(), 129) < 0  # > MAX_CHUNK
         assert L.hymt2_hip_quantize_q8k(backend.impl, out.data_ptr(), act.data_ptr(), 300, 1) < 0
         xq = O.quantize_q8k(synth.activations(g, 1, 512))
         ws = (C.c_void_p * 1)(h)
         outs = (C.c_void_p * 1)(np.zeros(64, np.float32).ctypes.data)
-        assert not backend.ops.matmul(backend.impl, ws, outs, 1, xq.ctypes.data, 17)
+        assert not backend.ops.matmul(backend.impl, ws, outs, 1, xq.ctypes.data, 129)
         # an unsupported tensor type is refused at upload (NULL), as the reference backend does
         bad = abi.WeightT(w.data.ctypes.data, abi.GT_Q8_0, 512, 64, abi.row_bytes(abi.GT_Q8_0, 512), None, None, 0, 0,
                           None)

@@ -72,6 +72,40 @@ def test_chunking_and_prefix_reuse(backend, mode):
         fm.close()
 
 
+@pytest.mark.parametrize("mode", ["stq", "q2", "q4km"])
+def test_chunked_prefill_vs_oracle(backend, mode):
+    """Prompt chunks above the reference's 16-token batch (128, and ragged 100 / 33): panel
+    weights on the int8-MFMA GEMM (Q4_K / Q6_K on the general kernel in groups of 16), causal
+    attention over the growing KV cache. The last prompt position's logits through
+    fused_forward, and the device loop's greedy ids after gen_prefill, vs the oracle."""
+    model = synth.make_model(SHAPE, mode=mode, seed=51)
+    prompt = synth.rand_prompt(synth.rng(52), 290, SHAPE.vocab)
+    om = O.OracleModel(model, threads=8)
+    ref = None
+    for i in range(0, len(prompt), 16):
+        c = prompt[i:i + 16]
+        ref = om.forward(c, i, want_logits=(i + len(c) == len(prompt)))
+    want = O.OracleModel(model, threads=8).generate(prompt, 24, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        for batch in (128, 100):
+            assert np.array_equal(bits(fm.prefill(list(prompt), batch=batch)), bits(ref)), f"batch={batch}"
+        for chunk in (128, 33):
+            ids, st = fm.generate_device(prompt, 24, chunk=chunk)
+            assert np.array_equal(ids, want), f"chunk={chunk}"
+            assert st.prefill_steps == len(prompt) and st.decode_steps == 23
+        # the step API: prefill, then steps in pieces
+        fm.gen_begin(prompt, len(prompt) + 10)
+        fm.gen_prefill(128)
+        fm.gen_steps(4)
+        fm.gen_steps(5)
+        assert np.array_equal(fm.gen_read(len(prompt), 10), want[:10])
+        with pytest.raises(RuntimeError):
+            fm.gen_prefill(128)  # only on a fresh loop
+    finally:
+        fm.close()
+
+
 @pytest.mark.parametrize("mode", ["stq", "q4km"])
 def test_long_greedy_device_vs_oracle(backend, mode):
     """A 300-position greedy run (attention past several 64-key tiles; softmax over > 256 keys)."""
@@ -114,6 +148,28 @@ def test_hidden2048_models(backend, mode):
         fm.close()
 
 
+@pytest.mark.parametrize("mode", ["stq", "q2"])
+def test_hidden2048_chunked_prefill(backend, mode):
+    """Chunked prefill at the 1.8B layer shapes: a 150-token prompt as chunks of 128 + 22, both
+    above the 16-token batch, so every qkv / o / gate-up / down contraction runs on the GEMM."""
+    shape = synth.ModelShape(n_layer=2, vocab=1000, ctx=192)
+    model = synth.make_model(shape, mode=mode, seed=53)
+    prompt = synth.rand_prompt(synth.rng(54), 150, shape.vocab)
+    om = O.OracleModel(model, threads=8)
+    ref = None
+    for i in range(0, len(prompt), 16):
+        c = prompt[i:i + 16]
+        ref = om.forward(c, i, want_logits=(i + len(c) == len(prompt)))
+    want = O.OracleModel(model, threads=8).generate(prompt, 12, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt), batch=128)), bits(ref))
+        ids, _ = fm.generate_device(prompt, 12, chunk=128)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
 def test_generate_rejects_overlong_runs(backend):
     model = synth.make_model(synth.ModelShape(n_layer=1, hidden=256, ffn=512, heads=2, kv_heads=1, hdim=128,
                                               vocab=300, ctx=64), mode="stq", seed=45)
@@ -127,8 +183,8 @@ def test_generate_rejects_overlong_runs(backend):
         with pytest.raises(RuntimeError):
             fm.gen_steps(1)               # past n_total - 1 steps
         a = fm.args
-        a.nt, a.pos0, a.want_logits, a.h, a.logits = 17, 0, 1, fm.h.ctypes.data, fm.logits.ctypes.data
-        assert not fm.b.ops.fused_forward(fm.b.impl, ctypes.byref(a))  # nt > 16 (src/cuda.c:341)
+        a.nt, a.pos0, a.want_logits, a.h, a.logits = 129, 0, 1, fm.h.ctypes.data, fm.logits.ctypes.data
+        assert not fm.b.ops.fused_forward(fm.b.impl, ctypes.byref(a))  # nt > HYMT2_HIP_MAX_CHUNK
         a.nt, a.pos0 = 2, 63
         assert not fm.b.ops.fused_forward(fm.b.impl, ctypes.byref(a))  # past ctx
         # still usable
@@ -153,5 +209,27 @@ def test_full_size_model_short_run(backend, mode):
         want = O.OracleModel(model, threads=16).generate(prompt, 4, batch=16)
         ids, _ = fm.generate_device(prompt, 4)
         assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
+def test_full_size_chunked_prefill_config4(backend):
+    """BASELINE config 4 at full size: the 1.8B Q2_0C model, a 1024-token prompt in 128-token
+    chunks. The last position's logits equal those of a token-by-token prefill (single-token
+    decode kernels, pinned to the oracle at this size by test_full_size_model_short_run), bit for
+    bit, and the device loop's greedy ids after the chunked prefill equal those after 1024
+    single-token steps (batched == stepwise, tests/test_model.py:369-374)."""
+    shape = synth.ModelShape(ctx=1040)
+    model = synth.make_model(shape, mode="q2", seed=4)
+    prompt = synth.rand_prompt(synth.rng(4096), 1024, shape.vocab)
+    fm = lib.FusedModel(backend, model)
+    try:
+        chunked = fm.prefill(list(prompt), batch=128)
+        stepwise = fm.prefill(list(prompt), batch=1)
+        assert np.array_equal(bits(chunked), bits(stepwise))
+        a, _ = fm.generate_device(prompt, 8, chunk=128)
+        b, _ = fm.generate_device(prompt, 8, chunk=1)
+        assert np.array_equal(a, b)
+        assert a[0] == int(np.argmax(stepwise[:fm.vocab_out]))
     finally:
         fm.close()
