@@ -366,6 +366,8 @@ def main():
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--no-layer-sets", action="store_true", help="skip the configs 0-2 matvec timings")
     ap.add_argument("--no-config4", action="store_true", help="skip the config 4 chunked-prefill run")
+    ap.add_argument("--config4-only", action="store_true",
+                    help="only the config 4 chunked-prefill run and the prefill GEMM timing (for profiling)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the standalone kernel launches used for rocprofv3 counter passes")
     args = ap.parse_args()
@@ -378,6 +380,13 @@ def main():
 
     if args.kernels_only:
         kernels_only(args)
+        return
+    if args.config4_only:
+        b = lib.Backend()
+        c4 = config4(b)
+        c4["gemm_roofline"] = gemm_roofline(b)
+        print(json.dumps(c4), flush=True)
+        b.close()
         return
     n_total = args.prompt + args.warmup + args.steps + 1  # steps fill positions 1..n_total-1
     ctx = (max(n_total, args.prompt + 33) + 63) // 64 * 64  # also room for the host-loop sample

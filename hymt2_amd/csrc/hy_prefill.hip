@@ -33,13 +33,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kGemmThreads = 256;
 constexpr int kGemmMaxNb = 64;  // K <= 16384 (LDS for the row scales)
 
-struct GemmFrag {
-    uint4 a[2];      // panel bytes of this lane's row in each row tile
-    uint4 q[2][4];   // qp chunks of this lane's token in each token tile
-    float d[2];
-    int sum[2];
-};
-
 __device__ __forceinline__ v4i chunk_codes(const uint4& p, int l) {
     const int sh = 2 * l;
     v4i r;
@@ -59,73 +52,127 @@ __device__ __forceinline__ v4i as_v4i(const uint4& u) {
     return r;
 }
 
+// Workgroup barrier for LDS only: waits for this wave's LDS operations, not for its global
+// loads, so prefetches stay in flight across it (a __syncthreads fence would drain them).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+constexpr int kTokRow = 272;  // LDS bytes per token row of qp: 256 + 16, so the 16 rows a
+                              // B-fragment read touches start in 16 different bank groups
+
 template <int MT, int NT, int WR, int WT, bool PAIR>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
     static_assert(WR * WT == kGemmThreads / 64, "4 wavefronts per workgroup");
     static_assert(!PAIR || MT == 2, "pair mode: one gate and one up tile per wavefront");
-    static_assert(MT <= 2 && NT <= 2, "fragment arrays");
     constexpr int SLOTS = WR * MT * 16;  // row slots of the workgroup
+    constexpr int TOK = WT * NT * 16;    // tokens of the workgroup
+    constexpr int BCH = TOK * 16 / kGemmThreads;  // 16-byte qp pieces per thread per block
+    static_assert(BCH >= 1 && TOK <= kGemmThreads, "token tile");
     __shared__ __align__(16) float ps_lds[kGemmMaxNb * SLOTS];
+    __shared__ __align__(16) uint8_t q_lds[2][TOK * kTokRow];
+    __shared__ __align__(16) int2 ds_lds[2][TOK];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave % WR, wt = wave / WR;
     const int nb = L.nb, nt = L.nt;
+    const HyQ8K* const act = L.act;
 
-    // job of this row tile
+    // job of this row tile (uniform)
     int j = 0;
 #pragma unroll
     for (int q = 1; q < kMaxJobs; q++)
         if (q < L.njobs && (int)blockIdx.x >= L.job[q].tile_begin) j = q;
     const int rows_wg = PAIR ? WR * 16 : SLOTS;
     const int row0 = ((int)blockIdx.x - L.job[j].tile_begin) * rows_wg;
-    const int tok0 = (int)blockIdx.y * (WT * NT * 16) + wt * NT * 16;
+    const int tokw = (int)blockIdx.y * TOK;  // first token of the workgroup
 
-    // which weight and row a slot s (= wr * MT * 16 + mt * 16 + rr) refers to
     auto slot_job = [&](int mt) { return PAIR ? mt : j; };
     auto slot_row = [&](int w_r, int mt, int rr) {
         return PAIR ? row0 + w_r * 16 + rr : row0 + w_r * MT * 16 + mt * 16 + rr;
     };
 
-    // stage the block scales of the workgroup's rows: ps_lds[b * SLOTS + s]
-    for (int idx = tid; idx < nb * SLOTS; idx += kGemmThreads) {
-        const int b = idx / SLOTS, s = idx % SLOTS;
-        const int w_r = s / (MT * 16), mt = (s / 16) % MT, rr = s % 16;
+    // Per row tile: its weight (uniform; read from the kernel arguments with scalar loads: a
+    // per-lane index into the job table would turn every field into a dependent vector load).
+    const uint8_t* wbase[MT];
+    const float* psbase[MT];
+    int nrow[MT], psh[MT], pof[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
         const MvWeight& W = L.job[slot_job(mt)].W;
-        const int r = min(slot_row(w_r, mt, rr), W.n - 1);
-        ps_lds[idx] = W.ps[(size_t)r * nb + b];
+        wbase[mt] = W.w;
+        psbase[mt] = W.ps;
+        nrow[mt] = W.n;
+        psh[mt] = W.pshift;
+        pof[mt] = W.poff;
     }
 
-    // this lane's operand rows and token (clamped to valid memory; results outside are dropped)
+    // Activations of one block for the workgroup's tokens: thread t loads 16-byte pieces
+    // t, t + 256, ... of the TOK x 256 qp bytes (16 threads per token, coalesced), the first TOK
+    // threads also (d, sum) of one token. Token indices are clamped to valid memory.
+    v4i qreg[BCH];
+    int2 dreg = make_int2(0, 0);
+    const int8_t* qsrc[BCH];
+#pragma unroll
+    for (int i = 0; i < BCH; i++) {
+        const int q = tid + i * kGemmThreads;
+        qsrc[i] = act[(size_t)min(tokw + (q >> 4), nt - 1) * nb].qp + 16 * (q & 15);
+    }
+    const int2* dsrc = reinterpret_cast<const int2*>(&act[(size_t)min(tokw + (tid % TOK), nt - 1) * nb].d);
+    auto qload = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < BCH; i++)
+            qreg[i] = *reinterpret_cast<const v4i*>(qsrc[i] + (size_t)b * sizeof(HyQ8K));
+        if (tid < TOK) dreg = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(dsrc) + (size_t)b * sizeof(HyQ8K));
+    };
+    auto qstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < BCH; i++) {
+            const int q = tid + i * kGemmThreads;
+            *reinterpret_cast<v4i*>(&q_lds[buf][(q >> 4) * kTokRow + 16 * (q & 15)]) = qreg[i];
+        }
+        if (tid < TOK) ds_lds[buf][tid] = dreg;
+    };
+
+    // this lane's weight rows (clamped; results outside are dropped)
     const uint8_t* arow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        const MvWeight& W = L.job[slot_job(mt)].W;
-        const int r = min(slot_row(wr, mt, lane & 15), W.n - 1);
-        arow[mt] = W.w + (size_t)r * nb * 64 + 16 * (lane >> 4);
+        const int r = min(slot_row(wr, mt, lane & 15), nrow[mt] - 1);
+        arow[mt] = wbase[mt] + (size_t)r * nb * 64 + 16 * (lane >> 4);
     }
-    const HyQ8K* brow[NT];
+    uint4 a0[MT], a1[MT];
+    auto aload = [&](uint4 (&a)[MT], int b) __attribute__((always_inline)) {
 #pragma unroll
-    for (int n = 0; n < NT; n++) brow[n] = L.act + (size_t)min(tok0 + n * 16 + (lane & 15), nt - 1) * nb;
-    int psh[MT], pof[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        psh[mt] = L.job[slot_job(mt)].W.pshift;
-        pof[mt] = L.job[slot_job(mt)].W.poff;
-    }
-
-    auto load = [&](GemmFrag& f, int b) {
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) f.a[mt] = *reinterpret_cast<const uint4*>(arow[mt] + (size_t)b * 64);
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const HyQ8K* y = brow[n] + b;
-#pragma unroll
-            for (int l = 0; l < 4; l++) f.q[n][l] = *reinterpret_cast<const uint4*>(y->qp + 64 * l + 16 * (lane >> 4));
-            const int2 ds = *reinterpret_cast<const int2*>(&y->d);
-            f.d[n] = __builtin_bit_cast(float, ds.x);
-            f.sum[n] = ds.y;
-        }
+        for (int mt = 0; mt < MT; mt++) a[mt] = *reinterpret_cast<const uint4*>(arow[mt] + (size_t)b * 64);
     };
+
+    // first block's operands, then the block scales of the workgroup's rows: ps_lds[b][slot]
+    qload(0);
+    aload(a0, 0);
+    {
+        constexpr int ROWS = WR * 16;                          // rows of one row-tile slice
+        constexpr int CNT = kGemmMaxNb * ROWS / kGemmThreads;  // entries per thread per slice
+        float v[MT][CNT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < CNT; i++) {
+                const int idx = tid + i * kGemmThreads;
+                const int b = min(idx / ROWS, nb - 1), q = idx % ROWS;
+                const int r = min(slot_row(q / 16, mt, q % 16), nrow[mt] - 1);
+                v[mt][i] = psbase[mt][(size_t)r * nb + b];
+            }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < CNT; i++) {
+                const int idx = tid + i * kGemmThreads;
+                const int b = idx / ROWS, q = idx % ROWS;
+                if (b < nb) ps_lds[b * SLOTS + (q / 16) * MT * 16 + mt * 16 + q % 16] = v[mt][i];
+            }
+    }
+    qstore(0);
 
     float accf[MT][NT][4];
 #pragma unroll
@@ -135,11 +182,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
 #pragma unroll
             for (int r = 0; r < 4; r++) accf[mt][n][r] = 0.f;
 
-    GemmFrag cur, nxt;
-    load(cur, 0);
-    __syncthreads();  // ps_lds ready
-    for (int b = 0; b < nb; b++) {
-        load(nxt, min(b + 1, nb - 1));
+    const int tl = lane & 15, g = lane >> 4;
+    // one block: MFMAs over its four K = 64 chunks, then the fp32 terms added in block order
+    // (src/kernels.c:576: ps * d * (float)((enc << pshift) - poff * sum))
+    auto compute = [&](const uint4 (&a)[MT], int b, int buf) __attribute__((always_inline)) {
         v4i acc[MT][NT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
@@ -147,60 +193,104 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
             for (int n = 0; n < NT; n++) acc[mt][n] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const v4i a = chunk_codes(cur.a[mt], l);
-#pragma unroll
-                for (int n = 0; n < NT; n++)
-                    acc[mt][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, as_v4i(cur.q[n][l]), acc[mt][n], 0, 0, 0);
-            }
-        }
-        // fp32 block terms, added in block order (src/kernels.c:576)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const float4 ps4 =
-                *reinterpret_cast<const float4*>(&ps_lds[b * SLOTS + wr * MT * 16 + mt * 16 + 4 * (lane >> 4)]);
-            const float psr[4] = {ps4.x, ps4.y, ps4.z, ps4.w};
+            uint4 qv[NT];
 #pragma unroll
             for (int n = 0; n < NT; n++)
+                qv[n] = *reinterpret_cast<const uint4*>(
+                    &q_lds[buf][(wt * NT * 16 + n * 16 + tl) * kTokRow + 64 * l + 16 * g]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const v4i av = chunk_codes(a[mt], l);
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+                    acc[mt][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, as_v4i(qv[n]), acc[mt][n], 0, 0, 0);
+            }
+        }
+        float dn[NT];
+        int off[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int2 ds = ds_lds[buf][wt * NT * 16 + n * 16 + tl];
+            dn[n] = __builtin_bit_cast(float, ds.x);
+            off[n] = ds.y;
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const float4 ps4 = *reinterpret_cast<const float4*>(&ps_lds[b * SLOTS + wr * MT * 16 + mt * 16 + 4 * g]);
+            const float psr[4] = {ps4.x, ps4.y, ps4.z, ps4.w};
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const int sub = pof[mt] * off[n];
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float term =
-                        psr[r] * cur.d[n] * (float)((acc[mt][n][r] << psh[mt]) - pof[mt] * cur.sum[n]);
+                    const float term = psr[r] * dn[n] * (float)((acc[mt][n][r] << psh[mt]) - sub);
                     accf[mt][n][r] = accf[mt][n][r] + term;
                 }
+            }
         }
-        cur = nxt;
+    };
+
+    lds_barrier();  // ps_lds and block 0 in LDS
+    for (int b = 0; b < nb; b += 2) {
+        // block b from buffer 0 with a0; block b + 1 loaded meanwhile (clamped, unused past the end)
+        const int b1 = min(b + 1, nb - 1);
+        qload(b1);
+        aload(a1, b1);
+        compute(a0, b, 0);
+        __builtin_amdgcn_sched_barrier(0);  // the LDS stores wait for the loads: after the terms
+        qstore(1);
+        lds_barrier();
+        if (b + 1 >= nb) break;
+        const int b2 = min(b + 2, nb - 1);
+        qload(b2);
+        aload(a0, b2);
+        compute(a1, b + 1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        qstore(0);
+        lds_barrier();
     }
 
-    // epilogue
-    const int tl = lane & 15, rq = 4 * (lane >> 4);
+    // epilogue: lane holds rows 4 g .. 4 g + 3 of each row tile for token tl of each token tile
+    float* const out = L.job[j].out;
+    const int ldo = L.job[j].ldo, nout = L.job[j].W.n, epi = L.job[j].epi;
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-        const int t = tok0 + n * 16 + tl;
+        const int t = tokw + wt * NT * 16 + n * 16 + tl;
         if (t >= nt) continue;
         if (PAIR) {
-            const GemmJob& J = L.job[0];
+            const int row = slot_row(wr, 0, 4 * g);
+            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int row = slot_row(wr, 0, rq + r);
-                if (row < J.W.n) {
-                    const float g = accf[0][n][r], u = accf[1][n][r];
-                    J.out[(size_t)t * J.ldo + row] = g / (1.0f + hy_expf(-g)) * u;
-                }
+                const float gt = accf[0][n][r], up = accf[1][n][r];
+                v[r] = gt / (1.0f + hy_expf(-gt)) * up;
+            }
+            float* o = out + (size_t)t * ldo + row;
+            if (row + 3 < nout && ((ldo | row) & 3) == 0) {
+                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (row + r < nout) o[r] = v[r];
             }
         } else {
-            const GemmJob& J = L.job[j];
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = slot_row(wr, mt, rq + r);
-                    if (row < J.W.n) {
-                        float* o = J.out + (size_t)t * J.ldo + row;
-                        *o = J.epi == EPI_ADD ? *o + accf[mt][n][r] : accf[mt][n][r];
+            for (int mt = 0; mt < MT; mt++) {
+                const int row = slot_row(wr, mt, 4 * g);
+                float* o = out + (size_t)t * ldo + row;
+                if (row + 3 < nout && ((ldo | row) & 3) == 0) {
+                    float4 v = make_float4(accf[mt][n][0], accf[mt][n][1], accf[mt][n][2], accf[mt][n][3]);
+                    if (epi == EPI_ADD) {
+                        const float4 h = *reinterpret_cast<const float4*>(o);
+                        v = make_float4(h.x + v.x, h.y + v.y, h.z + v.z, h.w + v.w);
                     }
+                    *reinterpret_cast<float4*>(o) = v;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (row + r < nout) o[r] = epi == EPI_ADD ? o[r] + accf[mt][n][r] : accf[mt][n][r];
                 }
+            }
         }
     }
 }
