@@ -1,24 +1,26 @@
-// Single-token attention of the fused decode step (nt = 1), gfx950: one 256-thread workgroup
+// Single-token attention of the fused decode step (nt = 1), gfx950: one 512-thread workgroup
 // per query head, the reference's attn_task for one position (src/model.c:767-795) after the
 // per-token RoPE, q/k RMSNorm and bf16 KV store (src/model.c:836-847).
 //
-// Latency plan: the key rows of the first 256 positions and the value tile of the first 128
-// positions are loaded at kernel entry, so their HBM latency overlaps the RoPE + RMSNorm of
-// this token. Scores: one key per thread, dot_bf16's four interleaved partial sums in order
-// (src/kernels.c:1111-1121). Softmax: max (order-free), expf, the sum in position order, the
-// probabilities p_j = e_j * (1 / sum). Output: one lane per head dimension accumulates
-// o += p_j * V_j[d] in position order (axpy_bf16, src/kernels.c:1122-1124) from LDS tiles of
-// 128 positions; the next tile is loaded while the current one is summed. The fp32 output row
-// goes to `ao`; the o-projection quantizes it.
+// Scores: one key per thread per pass of 512 positions, dot_bf16's four interleaved partial
+// sums in order (src/kernels.c:1111-1121); the first pass's key rows load at kernel entry. Softmax (src/model.c:781-789): max (order-free), expf, the sum in
+// position order by the 8-wavefront exact segmented sum (hy_block_exact_sum8), p_j =
+// e_j * (1 / sum). Output (axpy_bf16, src/kernels.c:1122-1124): o[d] += p_j * V_j[d] in
+// position order. Per tile of 128 positions all threads form the products p_j * V_j[d] (each
+// rounded to fp32, as the reference rounds them) into a [d][j] LDS tile; then one lane per
+// dimension adds its row in position order, four products per LDS read, while the next tile's
+// V rows load. The fp32 output row goes to `ao`; the o-projection quantizes it.
 #include "hy_kernels.h"
 
 namespace hy {
 
 namespace {
 
-constexpr int kA1Threads = 256;
-constexpr int kA1Keys = 256;  // keys per score pass (one per thread)
-constexpr int kA1Tile = 128;  // positions per V tile in LDS
+constexpr int kA1Threads = 512;
+constexpr int kA1Waves = kA1Threads / 64;
+constexpr int kA1Tile = 128;           // positions per product tile
+constexpr int kA1Row = kA1Tile + 4;    // floats per [d] row of the product tile (16-byte rows)
+constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
 
 __device__ __forceinline__ void bf16x8f(const uint4& v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -71,53 +73,162 @@ __device__ __forceinline__ void rope_norm_wave(const float (&x)[HD / 64], float*
     for (int i = 0; i < RPL; i++) out[i] = r[i] * scale * nw[i];
 }
 
+// dot_bf16(q, K_j) * scale with the reference's four partial sums (src/kernels.c:1111-1121).
+// q is read from LDS on every call (the offset is opaque to the compiler): held in registers
+// across a loop of passes it would take HD registers of its own.
+template <int HD>
+__device__ __forceinline__ float a1_score(const uint4 (&k)[HD / 8], const float* qn, float scale) {
+    int qo = 0;
+    asm volatile("" : "+v"(qo));
+    qn += qo;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) {
+        float kf[8];
+        bf16x8f(k[i], kf);
+        const float4 qa = *reinterpret_cast<const float4*>(qn + 8 * i);
+        const float4 qb = *reinterpret_cast<const float4*>(qn + 8 * i + 4);
+        a0 += qa.x * kf[0];
+        a1 += qa.y * kf[1];
+        a2 += qa.z * kf[2];
+        a3 += qa.w * kf[3];
+        a0 += qb.x * kf[4];
+        a1 += qb.y * kf[5];
+        a2 += qb.z * kf[6];
+        a3 += qb.w * kf[7];
+    }
+    return ((a0 + a1) + (a2 + a3)) * scale;
+}
+
+template <int HD>
+__device__ __forceinline__ void a1_load_key(uint4 (&k)[HD / 8], const uint16_t* K, int row) {
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) k[i] = *reinterpret_cast<const uint4*>(K + (size_t)row * HD + 8 * i);
+}
+
+// V pieces of one tile for this thread: row t0 + jj (clamped to `last`), piece columns
+// pc0 + 4 i
+template <int HD>
+__device__ __forceinline__ void a1_load_v(uint4 (&v)[HD / 32], const uint16_t* V, int t0, int jj, int pc0, int last) {
+    const int j = min(t0 + jj, last);
+#pragma unroll
+    for (int i = 0; i < HD / 32; i++) v[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (pc0 + 4 * i));
+}
+
+// o += row[0] + row[1] + ... + row[cnt - 1] in order, the LDS reads running 32 positions ahead
+// of the adds (FULL: cnt = kA1Tile, no per-position test)
+template <bool FULL>
+__device__ __forceinline__ void a1_chain(const float4* pr, int cnt, float& o) {
+    float4 w0[8], w1[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) w0[i] = pr[i];
+#pragma unroll
+    for (int q = 0; q < kA1Tile / 4; q += 16) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) w1[i] = pr[min(q + 8 + i, kA1Tile / 4 - 1)];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int b = 4 * (q + i);
+            if (FULL || b < cnt) o += w0[i].x;
+            if (FULL || b + 1 < cnt) o += w0[i].y;
+            if (FULL || b + 2 < cnt) o += w0[i].z;
+            if (FULL || b + 3 < cnt) o += w0[i].w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) w0[i] = pr[min(q + 16 + i, kA1Tile / 4 - 1)];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int b = 4 * (q + 8 + i);
+            if (FULL || b < cnt) o += w1[i].x;
+            if (FULL || b + 1 < cnt) o += w1[i].y;
+            if (FULL || b + 2 < cnt) o += w1[i].z;
+            if (FULL || b + 3 < cnt) o += w1[i].w;
+        }
+    }
+}
+
+// One tile of the output: the products p_j * V_j[d] (p_j = e_j * inv, formed once per position
+// as the reference forms it) into prod[d][j], then one lane per dimension adds its row in
+// position order.
+template <int HD>
+__device__ __forceinline__ void a1_tile(const uint4 (&v)[HD / 32], float* prod, const float* ex, const uint16_t* vb,
+                                        float inv, int t0, int jj, int pc0, int pos, int n, int tid, float& o) {
+    {
+        const int j = t0 + jj;
+        const float pj = ex[min(j, n - 1)] * inv;
+#pragma unroll
+        for (int i = 0; i < HD / 32; i++) {
+            const int pc = pc0 + 4 * i;
+            float vf[8];
+            bf16x8f(j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : v[i], vf);
+#pragma unroll
+            for (int e = 0; e < 8; e++) prod[(8 * pc + e) * kA1Row + jj] = pj * vf[e];
+        }
+    }
+    __syncthreads();
+    if (tid < HD) {
+        const float4* pr = reinterpret_cast<const float4*>(prod + tid * kA1Row);
+        const int cnt = min(kA1Tile, n - t0);
+        if (cnt == kA1Tile) a1_chain<true>(pr, cnt, o);
+        else a1_chain<false>(pr, cnt, o);
+    }
+    __syncthreads();
+}
+
 template <int HD>
 __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
-    constexpr int KV4 = HD / 8;                           // 16-byte pieces of one K / V row
-    constexpr int RPL = HD / 64;                          // row elements per lane
-    constexpr int VT_LOADS = kA1Tile * KV4 / kA1Threads;  // V pieces per thread per tile
-    static_assert(VT_LOADS >= 1 && kA1Tile * KV4 % kA1Threads == 0, "tile split");
-    __shared__ __align__(16) uint16_t vt[kA1Tile * HD];   // V tile, natural layout vt[j][d]
+    constexpr int KV4 = HD / 8;                 // 16-byte pieces of one K / V row
+    constexpr int RPL = HD / 64;                // row elements per lane
+    constexpr int PPT = KV4 / 4;                // V pieces per thread per tile
+    constexpr int PASSES = kA1MaxCtx / kA1Threads;
+    static_assert(kA1Waves == 8 && KV4 % 4 == 0, "8 wavefronts: 2 x 64 positions x 4 piece columns");
+    __shared__ __align__(16) float ex[kA1MaxCtx];       // e_j = expf(s_j - max)
+    __shared__ __align__(16) float prod[HD * kA1Row];   // products of one tile, [d][j]
+    __shared__ HyExactLdsT<kA1Waves> exs;
     __shared__ __align__(16) float scr[2][HD];
     __shared__ __align__(16) float qn[HD];
     __shared__ __align__(16) uint16_t kb[HD];
     __shared__ __align__(16) uint16_t vb[HD];
-    __shared__ float red[kA1Threads / 64];
+    __shared__ float red[kA1Waves];
     __shared__ float stat;
-    extern __shared__ __align__(16) float ex[];           // scores, exponentials, probabilities [n]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
     const int group = a.heads / a.kv_heads;
     const int g = h / group;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
-    const int n = pos + 1;
     const int half = a.rope_half;
+    const int cap = a.ctx - 1;  // loads issued before the position is known stay within the cache
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
+    // product-tile role of this thread: position jj of the tile, piece columns pc0 + 4 i
+    const int jj = lane + 64 * (wave & 1), pc0 = wave >> 1;
 
-    // 0. loads: this token's row (wavefronts 0: q, 1: k, 2: v) with its RoPE table entries and
-    //    norm weights, then the cached K rows of the first pass (one key per thread)
+    // 0. loads: the position (scalar), this token's q / k / v row for wavefronts 0 / 1 / 2
+    //    with the norm weights and the position's RoPE row (rope_cur when the position lives in
+    //    device memory), then the key rows of the first pass and the first V tile, only those
+    //    below the position
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
     float x[RPL], rc[RPL], rs[RPL], nw[RPL];
     {
         const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
         const float* nsrc = wave == 0 ? a.q_norm : a.k_norm;
-        const float* cs = a.rope_cos + (size_t)pos * half;
-        const float* sn = a.rope_sin + (size_t)pos * half;
+        const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
+        const float* sn = a.rope_cur ? a.rope_cur + half : a.rope_sin + (size_t)pos * half;
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
             const int d = lane + 64 * i, t = d < half ? d : (d < 2 * half ? d - half : 0);
             x[i] = src[d];
+            nw[i] = nsrc[d];
             rc[i] = cs[t];
             rs[i] = sn[t];
-            nw[i] = nsrc[d];
         }
     }
-    uint4 kr[KV4];
-    if (tid < pos) {
-#pragma unroll
-        for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)tid * HD + 8 * i);
-    }
+    const int n = pos + 1;
+    a1_fence();  // the row loads go out first: loads return in issue order
+    uint4 kA[KV4], kB[KV4];
+    if (tid < pos) a1_load_key<HD>(kA, K, tid);
+    uint4 v0[PPT], v1[PPT], v2[PPT];
+    if (jj < pos) a1_load_v<HD>(v0, V, 0, jj, pc0, cap);
     a1_fence();
 
     // 1. RoPE + RMSNorm of q (wavefront 0) and k (1), bf16 of k and v
@@ -133,13 +244,6 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
 #pragma unroll
         for (int i = 0; i < RPL; i++) vb[lane + 64 * i] = hy_to_bf16(x[i]);
     }
-    // the first V tile's loads (natural layout: consecutive threads, consecutive pieces of a row)
-    uint4 vr[VT_LOADS];
-#pragma unroll
-    for (int i = 0; i < VT_LOADS; i++) {
-        const int f = tid + kA1Threads * i, j = f / KV4;
-        if (j < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (f % KV4));
-    }
     __syncthreads();
     // the bf16 k, v of this position (src/model.c:842-847), stored once per KV head
     if (h % group == 0 && tid < HD) {
@@ -148,108 +252,97 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
         a.vc[off] = vb[tid];
     }
 
-    // 2. scores s_j = dot_bf16(q, K_j) * (1/sqrtf(hd)); key `pos` is this token's kb
+    // 2. scores s_j = dot_bf16(q, K_j) * (1/sqrtf(hd)) for j = tid + 512 p, kept in registers;
+    //    key `pos` is this token's kb; the next pass's rows load while this one is scored
     const float scale = 1.0f / sqrtf((float)HD);
+    float sv[PASSES];
     float lmax = -__builtin_inff();
-    for (int p0 = 0; p0 < n; p0 += kA1Keys) {
-        const int j = p0 + tid;
-        if (p0 > 0 && j < pos) {
 #pragma unroll
-            for (int i = 0; i < KV4; i++) kr[i] = *reinterpret_cast<const uint4*>(K + (size_t)j * HD + 8 * i);
+    for (int p = 0; p < PASSES; p += 2) {
+        const int j0 = p * kA1Threads + tid, j1 = j0 + kA1Threads;
+        if (j0 - tid >= n) break;
+        if (j1 - tid < n) a1_load_key<HD>(kB, K, min(j1, cap));
+        if (j0 < n) {
+            if (j0 == pos) a1_load_key<HD>(kA, kb, 0);
+            sv[p] = a1_score<HD>(kA, qn, scale);
+            lmax = fmaxf(lmax, sv[p]);
         }
-        if (j < n) {
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-            for (int i = 0; i < KV4; i++) {
-                float kf[8];
-                bf16x8f(j == pos ? *reinterpret_cast<const uint4*>(kb + 8 * i) : kr[i], kf);
-                const float4 qa = *reinterpret_cast<const float4*>(qn + 8 * i);
-                const float4 qb = *reinterpret_cast<const float4*>(qn + 8 * i + 4);
-                a0 += qa.x * kf[0];
-                a1 += qa.y * kf[1];
-                a2 += qa.z * kf[2];
-                a3 += qa.w * kf[3];
-                a0 += qb.x * kf[4];
-                a1 += qb.y * kf[5];
-                a2 += qb.z * kf[6];
-                a3 += qb.w * kf[7];
-            }
-            const float sj = ((a0 + a1) + (a2 + a3)) * scale;
-            ex[j] = sj;
-            lmax = fmaxf(lmax, sj);
+        if (j1 - tid >= n) break;
+        if (j1 + kA1Threads - tid < n) a1_load_key<HD>(kA, K, min(j1 + kA1Threads, cap));
+        if (j1 < n) {
+            if (j1 == pos) a1_load_key<HD>(kB, kb, 0);
+            sv[p + 1] = a1_score<HD>(kB, qn, scale);
+            lmax = fmaxf(lmax, sv[p + 1]);
         }
     }
+    if (kA1Tile + jj < pos) a1_load_v<HD>(v1, V, kA1Tile, jj, pc0, cap);
+    if (2 * kA1Tile + jj < pos) a1_load_v<HD>(v2, V, 2 * kA1Tile, jj, pc0, cap);
+    a1_fence();  // issued here, not next to their first use
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
+    __syncthreads();
 
-    // 3. softmax over positions (src/model.c:781-789): max (order-free), exp, sum in order,
-    //    p_j = e_j * (1 / sum); the first V tile goes into LDS meanwhile
-    auto store_tile = [&](int t0) {
+    // 3. softmax (src/model.c:781-789): max (order-free), e_j = expf(s_j - max), their sum in
+    //    position order, inv = 1 / sum. Short rows: the lane-serial chain of wavefront 0; long
+    //    ones: the exact segmented form over 8 consecutive positions per thread.
+    float inv;
+    {
+        float mx = red[0];
 #pragma unroll
-        for (int i = 0; i < VT_LOADS; i++) {
-            const int f = tid + kA1Threads * i, jj = f / KV4, pc = f % KV4;
-            const uint4 val = t0 + jj == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : vr[i];
-            *reinterpret_cast<uint4*>(vt + (size_t)jj * HD + 8 * pc) = val;
+        for (int w = 1; w < kA1Waves; w++) mx = fmaxf(mx, red[w]);
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            const int j = p * kA1Threads + tid;
+            if (j - tid >= n) break;
+            if (j < n) ex[j] = hy_expf(sv[p] - mx);
         }
-    };
-    __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int j = tid; j < n; j += kA1Threads) ex[j] = hy_expf(ex[j] - mx);
-    store_tile(0);
-    __syncthreads();
-    if (wave == 0) {
-        const float sum = hy_wave_seq_sum(ex, n, lane);
-        if (lane == 0) stat = 1.0f / sum;
-    }
-    __syncthreads();
-    const float inv = stat;
-    for (int j = tid; j < n; j += kA1Threads) ex[j] = ex[j] * inv;  // sc[j] * inv, once per position
-    __syncthreads();
-
-    // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16), one lane per dimension
-    float o = 0.f;
-    for (int t0 = 0; t0 < n; t0 += kA1Tile) {
-        if (t0 > 0) {
-            __syncthreads();  // previous tile consumed
-            store_tile(t0);
+        __syncthreads();
+        if (n <= kA1SerialSum) {
+            if (wave == 0) {
+                const float sum = hy_wave_seq_sum(ex, n, lane);
+                if (lane == 0) stat = 1.0f / sum;
+            }
             __syncthreads();
-        }
-        if (t0 + kA1Tile < n) {  // the next tile's loads, in flight while this one is summed
+            inv = stat;
+        } else {
+            const int e0 = 8 * tid;
+            float e[8];
 #pragma unroll
-            for (int i = 0; i < VT_LOADS; i++) {
-                const int f = tid + kA1Threads * i, j = t0 + kA1Tile + f / KV4;
-                if (j < pos) vr[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (f % KV4));
+            for (int i = 0; i < 8; i++) e[i] = 0.f;
+            if (e0 < n) {
+                const float4 s0 = *reinterpret_cast<const float4*>(ex + e0);
+                const float4 s1 = *reinterpret_cast<const float4*>(ex + e0 + 4);
+                const float ev[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? ev[i] : 0.f;
             }
+            inv = 1.0f / hy_block_exact_sum8<kA1Waves, false>(e, exs, wave, lane);
         }
-        if (tid < HD) {
-            const int cnt = min(kA1Tile, n - t0);
-            const float* pj = ex + t0;
-            const uint16_t* vd = vt + tid;
-            int jj = 0;
-            for (; jj + 8 <= cnt; jj += 8) {
-                const float4 p0 = *reinterpret_cast<const float4*>(pj + jj);
-                const float4 p1 = *reinterpret_cast<const float4*>(pj + jj + 4);
-                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                float vv[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) vv[k] = hy_bf16(vd[(size_t)(jj + k) * HD]);
-#pragma unroll
-                for (int k = 0; k < 8; k++) o += pv[k] * vv[k];
-            }
-            for (; jj < cnt; jj++) o += pj[jj] * hy_bf16(vd[(size_t)jj * HD]);
+    }
+
+    // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16); three V tiles in flight
+    float o = 0.f;
+    const int last = max(pos - 1, 0);
+    for (int t0 = 0; t0 < n; t0 += 3 * kA1Tile) {
+        a1_tile<HD>(v0, prod, ex, vb, inv, t0, jj, pc0, pos, n, tid, o);
+        a1_load_v<HD>(v0, V, t0 + 3 * kA1Tile, jj, pc0, last);
+        if (t0 + kA1Tile < n) {
+            a1_tile<HD>(v1, prod, ex, vb, inv, t0 + kA1Tile, jj, pc0, pos, n, tid, o);
+            a1_load_v<HD>(v1, V, t0 + 4 * kA1Tile, jj, pc0, last);
+        }
+        if (t0 + 2 * kA1Tile < n) {
+            a1_tile<HD>(v2, prod, ex, vb, inv, t0 + 2 * kA1Tile, jj, pc0, pos, n, tid, o);
+            a1_load_v<HD>(v2, V, t0 + 5 * kA1Tile, jj, pc0, last);
         }
     }
     if (tid < HD) a.ao[(size_t)h * HD + tid] = o;
 }
 
-size_t attn1_lds(int ctx) { return ((size_t)ctx + 8) * sizeof(float); }
-
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {
     if (a.heads % a.kv_heads || 2 * a.rope_half > a.hdim || a.ctx > kA1MaxCtx) return hipErrorNotSupported;
-    const size_t lds = attn1_lds(a.ctx);
     switch (a.hdim) {
-    case 64: k_attn1<64><<<a.heads, kA1Threads, lds, s>>>(a); break;
-    case 128: k_attn1<128><<<a.heads, kA1Threads, lds, s>>>(a); break;
+    case 64: k_attn1<64><<<a.heads, kA1Threads, 0, s>>>(a); break;
+    case 128: k_attn1<128><<<a.heads, kA1Threads, 0, s>>>(a); break;
     default: return hipErrorNotSupported;
     }
     return hipGetLastError();

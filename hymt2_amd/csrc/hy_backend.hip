@@ -51,14 +51,20 @@ struct DW {  // hy_dweight
     size_t bytes = 0;
 };
 
+// Input staging layout (device in_dev and pinned in_host): the position, its RoPE row, then the
+// hidden rows of the chunk at kInH.
+constexpr size_t kInH = 2048;
+
 struct Fused {
     int n_layer = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, hdim = 0, qdim = 0, kvdim = 0, ctx = 0,
         rope_half = 0;
     float eps = 0.f;
-    char* in_dev = nullptr;   // [pos int, padded to 64 B][HY_MAX_CHUNK * hidden floats]
+    char* in_dev = nullptr;   // [pos int | pad to 64 B][RoPE row of pos: cos, sin | pad to kInH]
+                              // [HY_MAX_CHUNK * hidden floats]
     char* in_host = nullptr;  // pinned staging of the same layout
     float* d_h = nullptr;
     int* d_pos = nullptr;
+    float* d_rope = nullptr;  // RoPE row of d_pos (single-token graphs)
     size_t in_bytes = 0;
     float *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr, *g = nullptr, *u = nullptr, *logits = nullptr;
     HyQ8K *act_h = nullptr, *act_q = nullptr, *act_f = nullptr;
@@ -497,7 +503,7 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
     f->rope_half = a->rope_half;
     f->eps = a->eps;
     const size_t B = HY_MAX_CHUNK, H = a->hidden, F = a->ffn, Q = a->qdim, KV = a->kvdim;
-    f->in_bytes = 64 + B * H * 4;
+    f->in_bytes = kInH + B * H * 4;
     bool ok = dalloc(c, &f->in_dev, f->in_bytes) && hipHostMalloc(&f->in_host, f->in_bytes, 0) == hipSuccess;
     ok = ok && dalloc(c, &f->q, B * Q * 4) && dalloc(c, &f->k, B * KV * 4) && dalloc(c, &f->v, B * KV * 4) &&
          dalloc(c, &f->ao, B * Q * 4) && dalloc(c, &f->g, B * F * 4) && dalloc(c, &f->u, B * F * 4) &&
@@ -513,7 +519,8 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
         return false;
     }
     f->d_pos = reinterpret_cast<int*>(f->in_dev);
-    f->d_h = reinterpret_cast<float*>(f->in_dev + 64);
+    f->d_rope = reinterpret_cast<float*>(f->in_dev + 64);
+    f->d_h = reinterpret_cast<float*>(f->in_dev + kInH);
     c->f = f;
     if (!copy_params(c, a)) return false;
     HIPCHK(c, hipMemset(f->kc, 0, (size_t)a->n_layer * a->ctx * KV * 2));
@@ -521,6 +528,14 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
     HIPCHK(c, hipMemset(f->key, 0, 64));
     HIPCHK(c, hipMemset(f->in_dev, 0, f->in_bytes));
     return true;
+}
+
+// Stages pos and its RoPE row (cos[half], then sin[half]) at the front of in_host.
+static void stage_pos(Fused* f, const hymt2_fused_args* a, int pos) {
+    memcpy(f->in_host, &pos, 4);
+    memcpy(f->in_host + 64, a->rope_cos + (size_t)pos * f->rope_half, (size_t)f->rope_half * 4);
+    memcpy(f->in_host + 64 + (size_t)f->rope_half * 4, a->rope_sin + (size_t)pos * f->rope_half,
+           (size_t)f->rope_half * 4);
 }
 
 static bool ensure_logits(Ctx* c, Fused* f, int n) {
@@ -588,6 +603,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             aa.rope_cos = f->rope_c;
             aa.rope_sin = f->rope_s;
             aa.pos_dev = pos_dev;
+            aa.rope_cur = pos_dev ? f->d_rope : nullptr;
             aa.pos0 = pos0;
             aa.ao = f->ao;
             aa.heads = f->heads;
@@ -762,10 +778,10 @@ static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
     const int nt = a->nt;
     const size_t hbytes = (size_t)nt * f->hidden * 4;
     const bool logits = a->want_logits && a->outw && a->logits;
-    memcpy(f->in_host + 64, a->h, hbytes);
+    memcpy(f->in_host + kInH, a->h, hbytes);
     if (nt == 1) {
-        memcpy(f->in_host, &a->pos0, 4);
-        HIPCHK(c, hipMemcpyAsync(f->in_dev, f->in_host, 64 + hbytes, hipMemcpyHostToDevice, c->s));
+        stage_pos(f, a, a->pos0);
+        HIPCHK(c, hipMemcpyAsync(f->in_dev, f->in_host, kInH + hbytes, hipMemcpyHostToDevice, c->s));
         if (logits && !ensure_logits(c, f, dw(a->outw)->mw.n)) return false;
         std::vector<const void*> sig = weight_sig(a);
         sig.push_back(reinterpret_cast<const void*>((uintptr_t)logits));
@@ -782,7 +798,7 @@ static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
         }
         HIPCHK(c, hipGraphLaunch(f->g_fwd, c->s));
     } else {
-        HIPCHK(c, hipMemcpyAsync(f->d_h, f->in_host + 64, hbytes, hipMemcpyHostToDevice, c->s));
+        HIPCHK(c, hipMemcpyAsync(f->d_h, f->in_host + kInH, hbytes, hipMemcpyHostToDevice, c->s));
         if (!enqueue_layers(c, a, nt, a->pos0, nullptr) || (logits && !enqueue_head(c, a, nt, false, 0))) {
             c->broken = true;
             return false;
@@ -960,7 +976,8 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     if (!f->g_step || f->sig_step != sig) {
         if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
         f->g_step = nullptr;
-        FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e16, e32, f->d_h, f->hidden, n_total};
+        FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e16, e32, f->d_h, f->hidden, n_total,
+                      f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
         if (!capture(c, &f->g_step, [&] {
                 if (!enqueue_layers(c, shape, 1, 0, f->d_pos) || !enqueue_head(c, shape, 1, true, vocab_out))
                     return false;
@@ -971,9 +988,9 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     }
     // start state: ids[0..n_prompt) = prompt, pos = 0, key = 0, h = embedding of ids[0]
     memset(f->in_host, 0, f->in_bytes);
-    const size_t pos_off = 0;
+    stage_pos(f, shape, 0);
     if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
-        hipMemcpyAsync(f->in_dev + pos_off, f->in_host + pos_off, 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
+        hipMemcpyAsync(f->in_dev, f->in_host, kInH, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->key, f->in_host, 8, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         launch_embed(f->ids, f->d_pos, e16, e32, f->d_h, f->hidden, c->s) != hipSuccess ||
         hipStreamSynchronize(c->s) != hipSuccess) {
@@ -1015,7 +1032,8 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     }
     // position np - 1 has been processed: the finishing kernel records the first generated id,
     // embeds it and advances the step counter to np, where the step graph continues
-    FinishArgs fa{f->key, f->ids, f->d_pos, np, f->gen_e16, f->gen_e32, f->d_h, f->hidden, f->gen_total};
+    FinishArgs fa{f->key, f->ids, f->d_pos, np, f->gen_e16, f->gen_e32, f->d_h, f->hidden, f->gen_total,
+                  f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
     if (launch_set_int(f->d_pos, np - 1, c->s) != hipSuccess || launch_finish(fa, c->s) != hipSuccess) {
         set_err(c, "gen_prefill: launch failed");
         c->broken = true;

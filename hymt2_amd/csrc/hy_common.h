@@ -400,28 +400,32 @@ __device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
 
 // ----------------------------------------------------------------------------------- block forms
 
-// LDS of hy_block_exact_sq_sum8 (a workgroup of up to 4 wavefronts).
-struct HyExactLds {
-    float wtot[4];          // estimate of each wavefront's total
-    double ktot[4];         // each wavefront's clean contributions
-    uint64_t dmask[4];      // dirty segments of each wavefront
-    double lpex[256];       // wavefront-local exclusive prefix of clean contributions per segment
-    float rows[256][12];    // dirty segments in order: [delta, 8 addends]
+// LDS of hy_block_exact_sum8 for a workgroup of NW wavefronts.
+template <int NW>
+struct HyExactLdsT {
+    float wtot[NW];          // estimate of each wavefront's total
+    double ktot[NW];         // each wavefront's clean contributions
+    uint64_t dmask[NW];      // dirty segments of each wavefront
+    double lpex[64 * NW];    // wavefront-local exclusive prefix of clean contributions per segment
+    float rows[64 * NW][12]; // dirty segments in order: [delta, 8 addends]
     float result;
 };
+using HyExactLds = HyExactLdsT<4>;
 
-// The sequential sum of squares of n = 512 * NW values, the workgroup's NW wavefronts holding 8
-// consecutive values per lane (lane l of wavefront w: values 512w + 8l .. +8), bit for bit the
-// one-lane loop. The same method as hy_wave_exact_sq_sum_v with 8-addend segments, the
-// estimates and the exact prefix sums carried across wavefronts through LDS (the proof there
-// holds unchanged: n <= 2048 keeps the sequential sum within 2^-12 of the exact one). Every
-// thread of the workgroup must call it; all receive the sum.
-template <int NW>
-__device__ inline float hy_block_exact_sq_sum8(const float (&xv)[8], HyExactLds& S, int wave, int lane) {
-    static_assert(NW >= 1 && NW <= 4, "up to 4 wavefronts");
+// The sequential fp32 sum of n = 512 * NW non-negative addends (SQ: the squares of the given
+// values), the workgroup's NW wavefronts holding 8 consecutive values per lane (lane l of
+// wavefront w: values 512w + 8l .. +8), bit for bit the one-lane loop. The same method as
+// hy_wave_exact_sq_sum_v with 8-addend segments, the estimates and the exact prefix sums
+// carried across wavefronts through LDS. The proof there holds unchanged up to n = 4096: the
+// float estimates and the sequential sum stay within 2^-12 of the exact prefix sums, inside
+// the 2^-9 classification margin. Every thread of the workgroup must call it; all receive the
+// sum.
+template <int NW, bool SQ>
+__device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW>& S, int wave, int lane) {
+    static_assert(NW >= 1 && NW <= 8, "up to 8 wavefronts (n <= 4096)");
     float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = xv[i] * xv[i];
+    for (int i = 0; i < 8; i++) v[i] = SQ ? xv[i] * xv[i] : xv[i];
     const float g = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     // 1. estimate of the running sum before this segment (float sums of non-negative values)
     const float estw = hy_wave_incl_scan(
@@ -500,7 +504,7 @@ __device__ inline float hy_block_exact_sq_sum8(const float (&xv)[8], HyExactLds&
         float s = 0.f;
         for (int base = 0; base < nd; base += 64) {
             float r[9];
-            const int kk0 = min(base + lane, 255);
+            const int kk0 = min(base + lane, 64 * NW - 1);
 #pragma unroll
             for (int i = 0; i < 9; i++) r[i] = S.rows[kk0][i];
             const int cnt = min(64, nd - base);
@@ -523,4 +527,10 @@ __device__ inline float hy_block_exact_sq_sum8(const float (&xv)[8], HyExactLds&
     }
     __syncthreads();
     return S.result;
+}
+
+// The RMSNorm form: the sequential sum of squares of 512 * NW values.
+template <int NW>
+__device__ inline float hy_block_exact_sq_sum8(const float (&xv)[8], HyExactLdsT<NW>& S, int wave, int lane) {
+    return hy_block_exact_sum8<NW, true>(xv, S, wave, lane);
 }

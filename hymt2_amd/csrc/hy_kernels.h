@@ -164,6 +164,7 @@ struct Attn1Args {
     const float* rope_cos;
     const float* rope_sin;
     const int* pos_dev;    // optional: position read from device memory (graph replay)
+    const float* rope_cur; // with pos_dev: that position's RoPE row (cos[half], sin[half])
     int pos0;
     float* ao;             // [qdim] attention output
     int heads, kv_heads, hdim, rope_half, ctx;
@@ -192,6 +193,10 @@ struct FinishArgs {
     float* h;              // next step's input [H]
     int H;
     int n_total;
+    const float* rope_cos; // RoPE tables [ctx][half]; the next position's row is copied to
+    const float* rope_sin; // rope_cur (cos then sin) for the next step's attention
+    float* rope_cur;
+    int rope_half, ctx;
 };
 hipError_t launch_finish(const FinishArgs& a, hipStream_t s);
 hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16, const float* embd32, float* h,

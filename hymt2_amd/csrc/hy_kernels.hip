@@ -939,8 +939,8 @@ __device__ void embed_row(const uint16_t* e16, const float* e32, int tok, float*
 }
 
 // Greedy step tail: token = argmax key; the next input is the next prompt id while the prompt
-// lasts, else the argmax (recorded in ids). Embeds the next token's row into h, advances the
-// device step counter and clears the key.
+// lasts, else the argmax (recorded in ids). Embeds the next token's row into h, copies the next
+// position's RoPE row, advances the device step counter and clears the key.
 __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
     __shared__ int next_tok, next_pos;
     if (threadIdx.x == 0) {
@@ -960,6 +960,12 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
     }
     __syncthreads();
     embed_row(a.embd, a.embd32, next_tok, a.h, a.H);
+    if (a.rope_cur && next_pos < a.ctx) {
+        for (int i = threadIdx.x; i < a.rope_half; i += blockDim.x) {
+            a.rope_cur[i] = a.rope_cos[(size_t)next_pos * a.rope_half + i];
+            a.rope_cur[a.rope_half + i] = a.rope_sin[(size_t)next_pos * a.rope_half + i];
+        }
+    }
     if (threadIdx.x == 0) {
         *a.step = next_pos;
         *a.argmax_key = 0ull;
@@ -1058,9 +1064,24 @@ __global__ __launch_bounds__(256) void k_selftest_sqsum_block(const float* x, in
     if (threadIdx.x == 0) out[blockIdx.x] = s;
 }
 
+// Method 3: the plain (non-squared) sequential sum of n <= 4096 non-negative addends by the
+// 8-wavefront form, as the decode attention's softmax denominator uses it.
+__global__ __launch_bounds__(512) void k_selftest_sum_block8(const float* x, int n, float* out) {
+    __shared__ HyExactLdsT<8> lds;
+    const float* p = x + (size_t)blockIdx.x * n;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, e0 = 512 * wave + 8 * lane;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = e0 + i < n ? p[e0 + i] : 0.f;
+    const float s = hy_block_exact_sum8<8, false>(v, lds, wave, lane);
+    if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
 hipError_t launch_selftest_sqsum(const float* x, int n, int m, float* out, int method, hipStream_t s) {
-    if (n < 1 || n > 2048 || (n & 3) || m < 1 || method < 0 || method > 2) return hipErrorInvalidValue;
-    if (method == 2) k_selftest_sqsum_block<<<m, 256, 0, s>>>(x, n, out);
+    if (n < 1 || (n & 3) || m < 1 || method < 0 || method > 3 || n > (method == 3 ? 4096 : 2048))
+        return hipErrorInvalidValue;
+    if (method == 3) k_selftest_sum_block8<<<m, 512, 0, s>>>(x, n, out);
+    else if (method == 2) k_selftest_sqsum_block<<<m, 256, 0, s>>>(x, n, out);
     else k_selftest_sqsum<<<m, 64, 0, s>>>(x, n, out, method);
     return hipGetLastError();
 }

@@ -138,7 +138,9 @@ HYMT2_HIP_API int hymt2_hip_selftest_expf(void *impl, const float *src_dev, floa
 /* The RMSNorm sum of squares of m vectors x[m][n] (n <= 2048, n % 4 == 0): out[v] = the
  * sequential fp32 sum x0*x0 + x1*x1 + ... (src/model.c:719-739), by the lane-serial chain
  * (method 0), the one-wavefront exact segmented form (method 1) or the workgroup-wide exact
- * form of the decode matvec's RMSNorm (method 2). */
+ * form of the decode matvec's RMSNorm (method 2). Method 3: the plain sequential sum
+ * x0 + x1 + ... of n <= 4096 non-negative values by the 8-wavefront exact form of the decode
+ * attention's softmax denominator (src/model.c:781-789). */
 HYMT2_HIP_API int hymt2_hip_selftest_sqsum(void *impl, const float *x_dev, int n, int m, float *out_dev, int method);
 
 /* Device-resident greedy generation (no host round trip per token). Each step runs one

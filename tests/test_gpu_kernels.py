@@ -8,6 +8,7 @@ LM head with its fused argmax (src/kernels.c:1279-1289, src/model.c:945-948) and
 points' argument checks."""
 import ctypes as C
 import os
+import zlib
 
 import numpy as np
 import pytest
@@ -109,7 +110,7 @@ def _sq_inputs(mode, m, n, g):
 def test_rmsnorm_sum_of_squares(backend, mode, n):
     """The RMSNorm's sequential sum of squares (src/model.c:719-739) by the lane-serial chain and
     by the exact segmented form, against numpy's sequential float32 accumulation."""
-    g = np.random.default_rng(abs(hash((mode, n))) % 2**32)
+    g = np.random.default_rng(zlib.crc32(f"{mode}/{n}".encode()))
     m = 4096 if n == 2048 else 512
     x = _sq_inputs(mode, m, n, g)
     sq = (x * x).astype(np.float32)
@@ -124,6 +125,53 @@ def test_rmsnorm_sum_of_squares(backend, mode, n):
         nan = np.isnan(want)
         assert np.array_equal(np.isnan(got), nan)
         assert np.array_equal(bits(got)[~nan], bits(want)[~nan]), f"method {method}"
+
+
+def _softmax_addends(mode, m, n, g):
+    """Non-negative addends like the attention's e_j = expf(s_j - max) in (0, 1], plus hard cases
+    for the exact sum: long runs below half an ulp of the running sum (ties to even), equal
+    values, zeros."""
+    if mode == "uniform":
+        s = g.standard_normal((m, n)).astype(np.float32)
+    elif mode == "peaked":
+        s = (g.standard_normal((m, n)) * 10).astype(np.float32)
+    elif mode == "flat":
+        s = (g.standard_normal((m, n)) * 1e-3).astype(np.float32)
+    else:
+        s = None
+    if s is not None:
+        s -= s.max(axis=1, keepdims=True)
+        return np.exp(s).astype(np.float32)
+    x = np.zeros((m, n), dtype=np.float32)
+    if mode == "ties":      # 1, then addends of exactly half an ulp (and a quarter) of the sum
+        x[:, 0] = 1.0
+        x[:, 1:] = np.float32(2.0 ** -24)
+        x[m // 2:, 1::3] = np.float32(2.0 ** -25)
+    elif mode == "ones":
+        x[:] = 1.0
+        x[:, n // 2:] = np.float32(0.5)
+    elif mode == "sparse":
+        x[g.random((m, n)) < 0.05] = 1.0
+        x[:, n - n // 4:] = 0.0
+        x *= g.random((m, n)).astype(np.float32)
+    return np.ascontiguousarray(x)
+
+
+@pytest.mark.parametrize("mode", ["uniform", "peaked", "flat", "ties", "ones", "sparse"])
+@pytest.mark.parametrize("n", [4096, 1280, 1000, 132, 4])
+def test_softmax_denominator_sum(backend, mode, n):
+    """The attention's softmax denominator: the sequential sum of e_j in position order
+    (src/model.c:785-787) by the 8-wavefront exact form, against numpy's sequential float32
+    accumulation."""
+    g = np.random.default_rng(zlib.crc32(f"sm/{mode}/{n}".encode()))
+    m = 256
+    x = _softmax_addends(mode, m, n, g)
+    want = np.add.accumulate(x, axis=1, dtype=np.float32)[:, -1]
+    xd = dev(x)
+    out = empty_f32(m)
+    assert backend.L.hymt2_hip_selftest_sqsum(backend.impl, xd.data_ptr(), n, m, out.data_ptr(), 3) == 0
+    sync()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want))
 
 
 # ----------------------------------------------------------------------------- Q8_K
