@@ -116,33 +116,47 @@ __device__ __forceinline__ void a1_load_v(uint4 (&v)[HD / 32], const uint16_t* V
 }
 
 // o += row[0] + row[1] + ... + row[cnt - 1] in order, the LDS reads running 32 positions ahead
-// of the adds (FULL: cnt = kA1Tile, no per-position test)
+// of the adds for a full tile; a partial tile reads 32 positions at a time up to cnt.
 template <bool FULL>
 __device__ __forceinline__ void a1_chain(const float4* pr, int cnt, float& o) {
-    float4 w0[8], w1[8];
+    if constexpr (FULL) {
+        float4 w0[8], w1[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) w0[i] = pr[i];
+        for (int i = 0; i < 8; i++) w0[i] = pr[i];
 #pragma unroll
-    for (int q = 0; q < kA1Tile / 4; q += 16) {
+        for (int q = 0; q < kA1Tile / 4; q += 16) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) w1[i] = pr[min(q + 8 + i, kA1Tile / 4 - 1)];
+            for (int i = 0; i < 8; i++) w1[i] = pr[min(q + 8 + i, kA1Tile / 4 - 1)];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int b = 4 * (q + i);
-            if (FULL || b < cnt) o += w0[i].x;
-            if (FULL || b + 1 < cnt) o += w0[i].y;
-            if (FULL || b + 2 < cnt) o += w0[i].z;
-            if (FULL || b + 3 < cnt) o += w0[i].w;
+            for (int i = 0; i < 8; i++) {
+                o += w0[i].x;
+                o += w0[i].y;
+                o += w0[i].z;
+                o += w0[i].w;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) w0[i] = pr[min(q + 16 + i, kA1Tile / 4 - 1)];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                o += w1[i].x;
+                o += w1[i].y;
+                o += w1[i].z;
+                o += w1[i].w;
+            }
         }
+    } else {
+        for (int q = 0; q < cnt; q += 32) {
+            float4 w[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) w0[i] = pr[min(q + 16 + i, kA1Tile / 4 - 1)];
+            for (int i = 0; i < 8; i++) w[i] = pr[min(q / 4 + i, kA1Tile / 4 - 1)];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int b = 4 * (q + 8 + i);
-            if (FULL || b < cnt) o += w1[i].x;
-            if (FULL || b + 1 < cnt) o += w1[i].y;
-            if (FULL || b + 2 < cnt) o += w1[i].z;
-            if (FULL || b + 3 < cnt) o += w1[i].w;
+            for (int i = 0; i < 8; i++) {
+                const int b = q + 4 * i;
+                if (b < cnt) o += w[i].x;
+                if (b + 1 < cnt) o += w[i].y;
+                if (b + 2 < cnt) o += w[i].z;
+                if (b + 3 < cnt) o += w[i].w;
+            }
         }
     }
 }
@@ -175,61 +189,54 @@ __device__ __forceinline__ void a1_tile(const uint4 (&v)[HD / 32], float* prod, 
     __syncthreads();
 }
 
+// LDS of one head's attention.
 template <int HD>
-__global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
+struct A1Smem {
+    alignas(16) float ex[kA1MaxCtx];      // e_j = expf(s_j - max)
+    alignas(16) float prod[HD * kA1Row];  // products of one tile, [d][j]
+    HyExactLdsT<kA1Waves> exs;
+    alignas(16) float scr[2][HD];
+    alignas(16) float qn[HD];
+    alignas(16) uint16_t kb[HD];
+    alignas(16) uint16_t vb[HD];
+    float red[kA1Waves];
+    float stat;
+};
+
+// Phases 1-4 of one head's attention, every thread of the workgroup: this token's rows (x:
+// q / k / v elements lane + 64 i for wavefronts 0 / 1 / 2), its RoPE row (rc, rs) and the q / k
+// norm weights (nw) are loaded; the key rows of the first pass (kA, rows below pos) and the
+// first V tile (v0) are in flight.
+template <int HD>
+__device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const float (&x)[HD / 64],
+                                        const float (&rc)[HD / 64], const float (&rs)[HD / 64],
+                                        const float (&nw)[HD / 64], uint4 (&kA)[HD / 8], uint4 (&v0)[HD / 32],
+                                        int pos) {
     constexpr int KV4 = HD / 8;                 // 16-byte pieces of one K / V row
     constexpr int RPL = HD / 64;                // row elements per lane
     constexpr int PPT = KV4 / 4;                // V pieces per thread per tile
     constexpr int PASSES = kA1MaxCtx / kA1Threads;
     static_assert(kA1Waves == 8 && KV4 % 4 == 0, "8 wavefronts: 2 x 64 positions x 4 piece columns");
-    __shared__ __align__(16) float ex[kA1MaxCtx];       // e_j = expf(s_j - max)
-    __shared__ __align__(16) float prod[HD * kA1Row];   // products of one tile, [d][j]
-    __shared__ HyExactLdsT<kA1Waves> exs;
-    __shared__ __align__(16) float scr[2][HD];
-    __shared__ __align__(16) float qn[HD];
-    __shared__ __align__(16) uint16_t kb[HD];
-    __shared__ __align__(16) uint16_t vb[HD];
-    __shared__ float red[kA1Waves];
-    __shared__ float stat;
+    float* ex = S.ex;
+    float* prod = S.prod;
+    float(&scr)[2][HD] = S.scr;
+    float* qn = S.qn;
+    uint16_t* kb = S.kb;
+    uint16_t* vb = S.vb;
+    float* red = S.red;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x;
     const int group = a.heads / a.kv_heads;
     const int g = h / group;
     const int half = a.rope_half;
-    const int cap = a.ctx - 1;  // loads issued before the position is known stay within the cache
+    const int cap = a.ctx - 1;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
-    // product-tile role of this thread: position jj of the tile, piece columns pc0 + 4 i
     const int jj = lane + 64 * (wave & 1), pc0 = wave >> 1;
-
-    // 0. loads: the position (scalar), this token's q / k / v row for wavefronts 0 / 1 / 2
-    //    with the norm weights and the position's RoPE row (rope_cur when the position lives in
-    //    device memory), then the key rows of the first pass and the first V tile, only those
-    //    below the position
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
-    float x[RPL], rc[RPL], rs[RPL], nw[RPL];
-    {
-        const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
-        const float* nsrc = wave == 0 ? a.q_norm : a.k_norm;
-        const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
-        const float* sn = a.rope_cur ? a.rope_cur + half : a.rope_sin + (size_t)pos * half;
-#pragma unroll
-        for (int i = 0; i < RPL; i++) {
-            const int d = lane + 64 * i, t = d < half ? d : (d < 2 * half ? d - half : 0);
-            x[i] = src[d];
-            nw[i] = nsrc[d];
-            rc[i] = cs[t];
-            rs[i] = sn[t];
-        }
-    }
     const int n = pos + 1;
-    a1_fence();  // the row loads go out first: loads return in issue order
-    uint4 kA[KV4], kB[KV4];
-    if (tid < pos) a1_load_key<HD>(kA, K, tid);
-    uint4 v0[PPT], v1[PPT], v2[PPT];
-    if (jj < pos) a1_load_v<HD>(v0, V, 0, jj, pc0, cap);
-    a1_fence();
+    uint4 kB[KV4];
+    uint4 v1[PPT], v2[PPT];
 
     // 1. RoPE + RMSNorm of q (wavefront 0) and k (1), bf16 of k and v
     if (wave < 2) {
@@ -300,10 +307,10 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
         if (n <= kA1SerialSum) {
             if (wave == 0) {
                 const float sum = hy_wave_seq_sum(ex, n, lane);
-                if (lane == 0) stat = 1.0f / sum;
+                if (lane == 0) S.stat = 1.0f / sum;
             }
             __syncthreads();
-            inv = stat;
+            inv = S.stat;
         } else {
             const int e0 = 8 * tid;
             float e[8];
@@ -316,7 +323,7 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? ev[i] : 0.f;
             }
-            inv = 1.0f / hy_block_exact_sum8<kA1Waves, false>(e, exs, wave, lane);
+            inv = 1.0f / hy_block_exact_sum8<kA1Waves, false>(e, S.exs, wave, lane);
         }
     }
 
@@ -336,6 +343,47 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
         }
     }
     if (tid < HD) a.ao[(size_t)h * HD + tid] = o;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
+    constexpr int RPL = HD / 64;
+    __shared__ A1Smem<HD> S;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x;
+    const int g = h / (a.heads / a.kv_heads);
+    const int half = a.rope_half;
+    const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
+    const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
+    const int jj = lane + 64 * (wave & 1), pc0 = wave >> 1;
+
+    // 0. loads: the position (scalar), this token's q / k / v row for wavefronts 0 / 1 / 2
+    //    with the norm weights and the position's RoPE row (rope_cur when the position lives in
+    //    device memory), then the key rows of the first pass and the first V tile, only those
+    //    below the position
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
+    float x[RPL], rc[RPL], rs[RPL], nw[RPL];
+    {
+        const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
+        const float* nsrc = wave == 0 ? a.q_norm : a.k_norm;
+        const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
+        const float* sn = a.rope_cur ? a.rope_cur + half : a.rope_sin + (size_t)pos * half;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int d = lane + 64 * i, t = d < half ? d : (d < 2 * half ? d - half : 0);
+            x[i] = src[d];
+            nw[i] = nsrc[d];
+            rc[i] = cs[t];
+            rs[i] = sn[t];
+        }
+    }
+    a1_fence();  // the row loads go out first: loads return in issue order
+    uint4 kA[HD / 8];
+    if (tid < pos) a1_load_key<HD>(kA, K, tid);
+    uint4 v0[HD / 32];
+    if (jj < pos) a1_load_v<HD>(v0, V, 0, jj, pc0, a.ctx - 1);
+    a1_fence();
+    a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, pos);
 }
 
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {

@@ -585,14 +585,11 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, attn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
             o1.act = f->act_h;
         }
-        if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_multi(c, qkv, 3, false, nt, o1))) return false;
         // single token: one workgroup per head (k_attn1), fp32 output quantized by the o matvec;
         // else the 256-output-block attention kernel, else the general path
         const bool head_attn = nt == 1 && (f->hdim == 64 || f->hdim == 128) && f->ctx <= kA1MaxCtx;
-        const bool fused_attn = nt == 1 && 256 % f->hdim == 0 && (f->heads / f->kv_heads) % (256 / f->hdim) == 0 &&
-                                attn_decode_lds(f->hdim, f->ctx) <= 96 * 1024;
+        Attn1Args aa{};
         if (head_attn) {
-            Attn1Args aa{};
             aa.q = f->q;
             aa.k = f->k;
             aa.v = f->v;
@@ -612,6 +609,11 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             aa.rope_half = f->rope_half;
             aa.ctx = f->ctx;
             aa.eps = f->eps;
+        }
+        if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_multi(c, qkv, 3, false, nt, o1))) return false;
+        const bool fused_attn = nt == 1 && 256 % f->hdim == 0 && (f->heads / f->kv_heads) % (256 / f->hdim) == 0 &&
+                                attn_decode_lds(f->hdim, f->ctx) <= 96 * 1024;
+        if (head_attn) {
             HIPCHK(c, launch_attn1(aa, c->s));
         } else if (fused_attn) {
             AttnDecodeArgs ad{};
