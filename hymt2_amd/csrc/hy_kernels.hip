@@ -4,6 +4,7 @@
 // in one lane, while the parallel work (loads, int8 dot products, exponentials, elementwise
 // ops) is spread over the wavefronts.
 #include "hy_kernels.h"
+#include "hy_mv_parts.h"
 
 namespace hy {
 
@@ -100,6 +101,26 @@ __device__ void quantize_lds_blocks(const float* xs, HyQ8K* act, int K) {
     for (int b = wave; b < K / HY_QK; b += nw) q8k_quantize_wave(xs + b * HY_QK, act + b, lane);
 }
 
+// H = 2048, Q8_K output only: the decode matvec's prologue per token. Lane l of wavefront w
+// holds values 512 w + 8 l .. + 8: the workgroup-wide exact sum of squares, x * scale * w, then
+// each wavefront quantizes its two blocks.
+__global__ __launch_bounds__(256) void k_rmsnorm_q8k_2048(const float* h, const float* w, float eps,
+                                                          HyQ8K* act_out) {
+    __shared__ HyExactLds ex;
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int off = 512 * wave + 8 * lane;
+    const float* x = h + (size_t)t * 2048 + off;
+    const float4 a0 = *reinterpret_cast<const float4*>(x), a1 = *reinterpret_cast<const float4*>(x + 4);
+    const float4 u0 = *reinterpret_cast<const float4*>(w + off), u1 = *reinterpret_cast<const float4*>(w + off + 4);
+    float e[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float nw[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const float sum = hy_block_exact_sq_sum8<4>(e, ex, wave, lane);
+    const float scale = 1.0f / sqrtf(sum / 2048.0f + eps);
+#pragma unroll
+    for (int i = 0; i < 8; i++) e[i] = e[i] * scale * nw[i];
+    q8k_quantize_halves(e, act_out + (size_t)t * 8 + 2 * wave, lane);
+}
+
 __global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float* w, float eps, int H,
                                                      float* xn_out, HyQ8K* act_out) {
     extern __shared__ __align__(16) float xs[];  // [H] values, [H] squares
@@ -114,7 +135,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float
 
 hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, int nt, float* xn_out,
                               HyQ8K* act_out, hipStream_t s) {
-    k_rmsnorm_q8k<<<nt, 256, (2 * H) * sizeof(float), s>>>(h, w, eps, H, xn_out, act_out);
+    if (H == 2048 && !xn_out && act_out) k_rmsnorm_q8k_2048<<<nt, 256, 0, s>>>(h, w, eps, act_out);
+    else k_rmsnorm_q8k<<<nt, 256, (2 * H) * sizeof(float), s>>>(h, w, eps, H, xn_out, act_out);
     return hipGetLastError();
 }
 
@@ -592,7 +614,152 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     }
 }
 
+// Chunk attention (nt tokens at consecutive positions, causal): one 512-thread workgroup per
+// (KV head, token) computes the `group` query heads that share the KV head, so each K row and
+// V tile is read once for all of them. The arithmetic is attn_task's (src/model.c:767-795) per
+// (token, head): scores by dot_bf16's four partial sums in order (src/kernels.c:1111-1121)
+// times 1/sqrtf(hd), max, expf, the sum in position order, p_j = e_j * (1 / sum) once per
+// position, then o[d] += p_j * V_j[d] in position order (axpy_bf16, :1122-1124).
+// Wavefront w works for head w % group: scores of keys (w / group) * 64 + lane + 64 * G p
+// (G = 8 / group key columns), its head's sum (wavefront h for head h), and the output
+// chains of head w / (8 / group)... with group = 4 and hd = 128: wavefronts 2h and 2h + 1 hold
+// head h's 128 dimensions, one per lane.
+constexpr int kAcThreads = 512;
+constexpr int kAcTile = 64;     // positions per V tile in LDS
+constexpr int kAcMaxCtx = 2048;
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));  // arrays of it stay in registers
+
+template <int HD, int GRP>
+__global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
+    constexpr int NW = kAcThreads / 64;
+    constexpr int KC = NW / GRP;             // key columns: wavefronts per head in the score pass
+    constexpr int KV4 = HD / 8;
+    constexpr int DW = HD / 64;              // wavefronts per head in the output (one dim per lane)
+    static_assert(GRP * DW <= NW && NW % GRP == 0, "heads x dims fit the workgroup");
+    constexpr int VPT = kAcTile * KV4 / kAcThreads;  // 16-byte V pieces per thread per tile
+    static_assert(VPT >= 1, "tile split");
+    __shared__ __align__(16) float qs[GRP][HD];
+    __shared__ __align__(16) float sc[GRP][kAcMaxCtx];
+    __shared__ __align__(16) uint16_t vt[2][kAcTile * HD];
+    __shared__ float red[NW];
+    __shared__ float inv_s[GRP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = blockIdx.x, t = blockIdx.y;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
+    const int n = pos + 1;
+    const int qdim = a.heads * HD;
+    const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
+    const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
+
+    // q rows of the group's heads (RoPE'd and normed by k_rope_norm_store)
+    for (int i = tid; i < GRP * HD; i += kAcThreads) qs[i / HD][i % HD] = a.q[(size_t)t * qdim + (size_t)(g * GRP) * HD + i];
+    // first V tile
+    v4u vr[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const int f = tid + kAcThreads * i, j = f / KV4;
+        vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
+    }
+    __syncthreads();
+
+    // scores
+    const int sh = wave % GRP, kc = wave / GRP;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float lmax = -__builtin_inff();
+    for (int j = kc * 64 + lane; j < n; j += KC * 64) {
+        const uint16_t* kr = K + (size_t)j * HD;
+        int qo = 0;
+        asm volatile("" : "+v"(qo));  // q is read per key, not held in registers across keys
+        const float* qh = &qs[sh][0] + qo;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < KV4; i++) {
+            const uint4 kv = *reinterpret_cast<const uint4*>(kr + 8 * i);
+            const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * i);
+            const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * i + 4);
+            a0 += qa.x * hy_bitsf(kv.x << 16);
+            a1 += qa.y * hy_bitsf(kv.x & 0xffff0000u);
+            a2 += qa.z * hy_bitsf(kv.y << 16);
+            a3 += qa.w * hy_bitsf(kv.y & 0xffff0000u);
+            a0 += qb.x * hy_bitsf(kv.z << 16);
+            a1 += qb.y * hy_bitsf(kv.z & 0xffff0000u);
+            a2 += qb.z * hy_bitsf(kv.w << 16);
+            a3 += qb.w * hy_bitsf(kv.w & 0xffff0000u);
+        }
+        const float sj = ((a0 + a1) + (a2 + a3)) * scale;
+        sc[sh][j] = sj;
+        lmax = fmaxf(lmax, sj);
+    }
+    lmax = hy_wave_max(lmax);
+    if (lane == 0) red[wave] = lmax;
+    __syncthreads();
+    // e_j = expf(s_j - max) per head
+    {
+        float mx = red[sh];
+#pragma unroll
+        for (int c = 1; c < KC; c++) mx = fmaxf(mx, red[sh + GRP * c]);
+        for (int j = kc * 64 + lane; j < n; j += KC * 64) sc[sh][j] = hy_expf(sc[sh][j] - mx);
+    }
+    __syncthreads();
+    // the sum of head h in position order by wavefront h
+    if (wave < GRP) {
+        const float sum = hy_wave_seq_sum(sc[wave], n, lane);
+        if (lane == 0) inv_s[wave] = 1.0f / sum;
+    }
+    // output chains: head oh, dimension od; V tiles through LDS, the next tile's loads in
+    // flight while the current one is summed
+    const int oh = wave / DW, od = (wave % DW) * 64 + lane;
+    float o = 0.f;
+    for (int t0 = 0, buf = 0; t0 < n; t0 += kAcTile, buf ^= 1) {
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int f = tid + kAcThreads * i;
+            *reinterpret_cast<v4u*>(&vt[buf][(f / KV4) * HD + 8 * (f % KV4)]) = vr[i];
+        }
+        if (t0 + kAcTile < n) {
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                const int f = tid + kAcThreads * i, j = t0 + kAcTile + f / KV4;
+                vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
+            }
+        }
+        __syncthreads();  // tile in LDS (and, the first time, inv_s and the e_j)
+        if (oh < GRP) {
+            const float inv = inv_s[oh];
+            const float* pe = sc[oh] + t0;
+            const uint16_t* vd = vt[buf] + od;
+            const int cnt = min(kAcTile, n - t0);
+            int q = 0;
+            for (; q + 8 <= cnt; q += 8) {
+                float vv[8], pj[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    vv[k] = hy_bf16(vd[(q + k) * HD]);
+                    pj[k] = pe[q + k] * inv;
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) o += pj[k] * vv[k];
+            }
+            for (; q < cnt; q++) o += (pe[q] * inv) * hy_bf16(vd[q * HD]);
+        }
+    }
+    if (oh < GRP) a.ao[(size_t)t * qdim + (size_t)(g * GRP + oh) * HD + od] = o;
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+    // causal chunk attention per (KV head, token) where it applies
+    int grp = a.heads % a.kv_heads == 0 ? a.heads / a.kv_heads : 0;
+    if (a.ctx <= kAcMaxCtx) {
+        const dim3 grid(a.kv_heads, a.nt);
+        if (a.hdim == 128 && grp == 4) k_attn_chunk<128, 4><<<grid, kAcThreads, 0, s>>>(a);
+        else if (a.hdim == 128 && grp == 2) k_attn_chunk<128, 2><<<grid, kAcThreads, 0, s>>>(a);
+        else if (a.hdim == 64 && grp == 4) k_attn_chunk<64, 4><<<grid, kAcThreads, 0, s>>>(a);
+        else if (a.hdim == 64 && grp == 2) k_attn_chunk<64, 2><<<grid, kAcThreads, 0, s>>>(a);
+        else grp = 0;
+        if (grp) return hipGetLastError();
+    }
     const size_t lds = (256 + (size_t)a.ctx + 4) * sizeof(float);
     if (lds > 160 * 1024 || a.heads % a.kv_heads) return hipErrorInvalidValue;
     const dim3 grid(a.nt, a.heads);

@@ -31,7 +31,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
-constexpr int kGemmMaxNb = 64;  // K <= 16384 (LDS for the row scales)
 
 __device__ __forceinline__ v4i chunk_codes(const uint4& p, int l) {
     const int sh = 2 * l;
@@ -58,20 +57,59 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-constexpr int kTokRow = 272;  // LDS bytes per token row of qp: 256 + 16, so the 16 rows a
-                              // B-fragment read touches start in 16 different bank groups
+// Direct global -> LDS loads: lane L's 16 (4) bytes from src land at LDS address dst + 16 L
+// (4 L), dst uniform (an LDS byte address). Written as assembly so that the compiler does not
+// order the workgroup's LDS reads behind them: the kernel waits for them itself (wait_vm), for
+// the block it is about to read, and the LDS they fill is not read before that wait.
+__device__ __forceinline__ void dma16(const void* src, uint32_t dst) {
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)dst);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t dst) {
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)dst);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
 
-template <int MT, int NT, int WR, int WT, bool PAIR>
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Waits until at most N of this wave's vector memory operations (loads, LDS-direct loads) are
+// outstanding. They complete in issue order.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One K-block of operands in LDS, filled by direct loads (no registers):
+//   q: the workgroup's TOK tokens x 16 pieces of 16 qp bytes; piece c of token t sits at slot
+//      16 t + (c ^ (t & 15)), so the 16 tokens of a B-fragment read hit 16 bank groups;
+//   a: the workgroup's ROWS panel rows x 4 pieces of 16 bytes; piece g of row r at slot
+//      4 r + (g ^ ((r >> 2) & 3)), conflict-free the same way for the A-fragment reads;
+//   d, sum: the tokens' Q8_K scale and sum; ps: the rows' block scale (one 64-lane direct load
+//   each, so sized for 64).
+template <int ROWS, int TOK>
+struct GemmStage {
+    alignas(16) uint8_t q[TOK * 256];
+    alignas(16) uint8_t a[ROWS * 64];
+    alignas(16) float d[64];
+    alignas(16) int sum[64];
+    alignas(16) float ps[64];
+};
+
+template <int MT, int NT, int WR, int WT, bool PAIR, int RING>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
     static_assert(WR * WT == kGemmThreads / 64, "4 wavefronts per workgroup");
     static_assert(!PAIR || MT == 2, "pair mode: one gate and one up tile per wavefront");
     constexpr int SLOTS = WR * MT * 16;  // row slots of the workgroup
     constexpr int TOK = WT * NT * 16;    // tokens of the workgroup
-    constexpr int BCH = TOK * 16 / kGemmThreads;  // 16-byte qp pieces per thread per block
-    static_assert(BCH >= 1 && TOK <= kGemmThreads, "token tile");
-    __shared__ __align__(16) float ps_lds[kGemmMaxNb * SLOTS];
-    __shared__ __align__(16) uint8_t q_lds[2][TOK * kTokRow];
-    __shared__ __align__(16) int2 ds_lds[2][TOK];
+    // direct loads of one block: QN of qp, AN of panel bytes, then d, sum and the rows' block
+    // scales (64 lanes each), dealt round-robin to the wavefronts: load k goes to wavefront k % 4
+    constexpr int QN = TOK / 4, AN = SLOTS / 16, TOTAL = QN + AN + 3;
+    constexpr int MAXI = (TOTAL + 3) / 4;
+    static_assert(TOK % 4 == 0 && SLOTS % 16 == 0 && TOK <= 64, "tile shape");
+    using Stage = GemmStage<SLOTS, TOK>;
+    __shared__ Stage ring[RING];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave % WR, wt = wave / WR;
@@ -88,6 +126,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
     const int tokw = (int)blockIdx.y * TOK;  // first token of the workgroup
 
     auto slot_job = [&](int mt) { return PAIR ? mt : j; };
+    // weight row of local row slot s = w_r * MT * 16 + mt * 16 + rr
     auto slot_row = [&](int w_r, int mt, int rr) {
         return PAIR ? row0 + w_r * 16 + rr : row0 + w_r * MT * 16 + mt * 16 + rr;
     };
@@ -107,72 +146,62 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
         pof[mt] = W.poff;
     }
 
-    // Activations of one block for the workgroup's tokens: thread t loads 16-byte pieces
-    // t, t + 256, ... of the TOK x 256 qp bytes (16 threads per token, coalesced), the first TOK
-    // threads also (d, sum) of one token. Token indices are clamped to valid memory.
-    v4i qreg[BCH];
-    int2 dreg = make_int2(0, 0);
-    const int8_t* qsrc[BCH];
+    // Sources of this thread's direct loads for block 0 (block b adds b times the stride) and
+    // their LDS destinations (offsets in a stage)
+    const char* src[MAXI];
+    size_t stride[MAXI];
+    uint32_t dst[MAXI];
 #pragma unroll
-    for (int i = 0; i < BCH; i++) {
-        const int q = tid + i * kGemmThreads;
-        qsrc[i] = act[(size_t)min(tokw + (q >> 4), nt - 1) * nb].qp + 16 * (q & 15);
-    }
-    const int2* dsrc = reinterpret_cast<const int2*>(&act[(size_t)min(tokw + (tid % TOK), nt - 1) * nb].d);
-    auto qload = [&](int b) __attribute__((always_inline)) {
+    for (int i = 0; i < MAXI; i++) {
+        const int k = min(wave + 4 * i, TOTAL - 1);
+        if (k < QN) {
+            const int sl = k * 64 + lane, t = sl >> 4, c = (sl & 15) ^ (t & 15);
+            src[i] = reinterpret_cast<const char*>(act[(size_t)min(tokw + t, nt - 1) * nb].qp + 16 * c);
+            stride[i] = sizeof(HyQ8K);
+            dst[i] = offsetof(Stage, q) + k * 1024;
+        } else if (k < QN + AN) {
+            const int sl = (k - QN) * 64 + lane, r = sl >> 2, gg = (sl & 3) ^ ((r >> 2) & 3);
+            const int w_r = r / (MT * 16), mt = (r / 16) % MT, rr = r % 16;
+            // mt is per lane here: select among the row tiles' bases with constant indices
+            const uint8_t* wb = wbase[0];
+            int nr = nrow[0];
 #pragma unroll
-        for (int i = 0; i < BCH; i++)
-            qreg[i] = *reinterpret_cast<const v4i*>(qsrc[i] + (size_t)b * sizeof(HyQ8K));
-        if (tid < TOK) dreg = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(dsrc) + (size_t)b * sizeof(HyQ8K));
-    };
-    auto qstore = [&](int buf) __attribute__((always_inline)) {
+            for (int m = 1; m < MT; m++)
+                if (mt == m) wb = wbase[m], nr = nrow[m];
+            src[i] = reinterpret_cast<const char*>(wb + (size_t)min(slot_row(w_r, mt, rr), nr - 1) * nb * 64 + 16 * gg);
+            stride[i] = 64;
+            dst[i] = offsetof(Stage, a) + (k - QN) * 1024;
+        } else if (k < QN + AN + 2) {
+            src[i] = reinterpret_cast<const char*>(&act[(size_t)min(tokw + lane, nt - 1) * nb].d) + (k == QN + AN ? 0 : 4);
+            stride[i] = sizeof(HyQ8K);
+            dst[i] = k == QN + AN ? offsetof(Stage, d) : offsetof(Stage, sum);
+        } else {  // block scale of row slot `lane` (slots past SLOTS load a valid row, unused)
+            const int sl = min(lane, SLOTS - 1);
+            const int w_r = sl / (MT * 16), mt = (sl / 16) % MT, rr = sl % 16;
+            const float* pb = psbase[0];
+            int nr = nrow[0];
 #pragma unroll
-        for (int i = 0; i < BCH; i++) {
-            const int q = tid + i * kGemmThreads;
-            *reinterpret_cast<v4i*>(&q_lds[buf][(q >> 4) * kTokRow + 16 * (q & 15)]) = qreg[i];
+            for (int m = 1; m < MT; m++)
+                if (mt == m) pb = psbase[m], nr = nrow[m];
+            src[i] = reinterpret_cast<const char*>(pb + (size_t)min(slot_row(w_r, mt, rr), nr - 1) * nb);
+            stride[i] = 4;
+            dst[i] = offsetof(Stage, ps);
         }
-        if (tid < TOK) ds_lds[buf][tid] = dreg;
+    }
+    const uint32_t ring0 = lds_addr(&ring[0]);
+    auto issue = [&](int b, int buf) __attribute__((always_inline)) {
+        const uint32_t base = ring0 + buf * (uint32_t)sizeof(Stage);
+#pragma unroll
+        for (int i = 0; i < MAXI; i++) {
+            const int k = wave + 4 * i;
+            if (k < QN + AN) dma16(src[i] + (size_t)b * stride[i], base + dst[i]);
+            else if (k < TOTAL) dma4(src[i] + (size_t)b * stride[i], base + dst[i]);
+        }
     };
 
-    // this lane's weight rows (clamped; results outside are dropped)
-    const uint8_t* arow[MT];
+    // the first RING - 1 blocks (clamped: a block past the end repeats the last, unused)
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int r = min(slot_row(wr, mt, lane & 15), nrow[mt] - 1);
-        arow[mt] = wbase[mt] + (size_t)r * nb * 64 + 16 * (lane >> 4);
-    }
-    uint4 a0[MT], a1[MT];
-    auto aload = [&](uint4 (&a)[MT], int b) __attribute__((always_inline)) {
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) a[mt] = *reinterpret_cast<const uint4*>(arow[mt] + (size_t)b * 64);
-    };
-
-    // first block's operands, then the block scales of the workgroup's rows: ps_lds[b][slot]
-    qload(0);
-    aload(a0, 0);
-    {
-        constexpr int ROWS = WR * 16;                          // rows of one row-tile slice
-        constexpr int CNT = kGemmMaxNb * ROWS / kGemmThreads;  // entries per thread per slice
-        float v[MT][CNT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < CNT; i++) {
-                const int idx = tid + i * kGemmThreads;
-                const int b = min(idx / ROWS, nb - 1), q = idx % ROWS;
-                const int r = min(slot_row(q / 16, mt, q % 16), nrow[mt] - 1);
-                v[mt][i] = psbase[mt][(size_t)r * nb + b];
-            }
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < CNT; i++) {
-                const int idx = tid + i * kGemmThreads;
-                const int b = idx / ROWS, q = idx % ROWS;
-                if (b < nb) ps_lds[b * SLOTS + (q / 16) * MT * 16 + mt * 16 + q % 16] = v[mt][i];
-            }
-    }
-    qstore(0);
+    for (int b = 0; b < RING - 1; b++) issue(min(b, nb - 1), b);
 
     float accf[MT][NT][4];
 #pragma unroll
@@ -183,72 +212,74 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
             for (int r = 0; r < 4; r++) accf[mt][n][r] = 0.f;
 
     const int tl = lane & 15, g = lane >> 4;
-    // one block: MFMAs over its four K = 64 chunks, then the fp32 terms added in block order
-    // (src/kernels.c:576: ps * d * (float)((enc << pshift) - poff * sum))
-    auto compute = [&](const uint4 (&a)[MT], int b, int buf) __attribute__((always_inline)) {
+    for (int b = 0; b < nb; b++) {
+        const int buf = b % RING;
+        // block b's direct loads are the oldest RING - 1 issues ago: wait for them, then the
+        // barrier makes every wavefront's share visible (and ends the reads of block b - 1,
+        // whose buffer the next issue refills)
+        // this wavefront's loads per block: the k < TOTAL with k % 4 == wave
+        if (wave == 0) wait_vm<(RING - 2) * ((TOTAL + 3) / 4)>();
+        else if (wave == 1) wait_vm<(RING - 2) * ((TOTAL + 2) / 4)>();
+        else if (wave == 2) wait_vm<(RING - 2) * ((TOTAL + 1) / 4)>();
+        else wait_vm<(RING - 2) * (TOTAL / 4)>();
+        lds_barrier();
+        issue(min(b + RING - 1, nb - 1), (b + RING - 1) % RING);
+        const Stage& S = ring[buf];
+
+        // MFMAs over the block's four K = 64 chunks
         v4i acc[MT][NT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int n = 0; n < NT; n++) acc[mt][n] = v4i{0, 0, 0, 0};
+        uint4 ap[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int r = wr * MT * 16 + mt * 16 + tl;
+            ap[mt] = *reinterpret_cast<const uint4*>(S.a + (4 * r + (g ^ ((r >> 2) & 3))) * 16);
+        }
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-            uint4 qv[NT];
+            v4i qv[NT];
 #pragma unroll
-            for (int n = 0; n < NT; n++)
-                qv[n] = *reinterpret_cast<const uint4*>(
-                    &q_lds[buf][(wt * NT * 16 + n * 16 + tl) * kTokRow + 64 * l + 16 * g]);
+            for (int n = 0; n < NT; n++) {
+                const int t = wt * NT * 16 + n * 16 + tl;
+                qv[n] = *reinterpret_cast<const v4i*>(S.q + (16 * t + ((4 * l + g) ^ tl)) * 16);
+            }
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const v4i av = chunk_codes(a[mt], l);
+                const v4i av = chunk_codes(ap[mt], l);
 #pragma unroll
                 for (int n = 0; n < NT; n++)
-                    acc[mt][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, as_v4i(qv[n]), acc[mt][n], 0, 0, 0);
+                    acc[mt][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, qv[n], acc[mt][n], 0, 0, 0);
             }
         }
+        // fp32 terms added in block order (src/kernels.c:576: ps * d * (float)((enc << pshift)
+        // - poff * sum))
         float dn[NT];
         int off[NT];
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-            const int2 ds = ds_lds[buf][wt * NT * 16 + n * 16 + tl];
-            dn[n] = __builtin_bit_cast(float, ds.x);
-            off[n] = ds.y;
+            const int t = wt * NT * 16 + n * 16 + tl;
+            dn[n] = S.d[t];
+            off[n] = S.sum[t];
         }
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            const float4 ps4 = *reinterpret_cast<const float4*>(&ps_lds[b * SLOTS + wr * MT * 16 + mt * 16 + 4 * g]);
+            const float4 ps4 = *reinterpret_cast<const float4*>(&S.ps[wr * MT * 16 + mt * 16 + 4 * g]);
             const float psr[4] = {ps4.x, ps4.y, ps4.z, ps4.w};
 #pragma unroll
             for (int n = 0; n < NT; n++) {
-                const int sub = pof[mt] * off[n];
+                const int nsub = -(pof[mt] * off[n]);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float term = psr[r] * dn[n] * (float)((acc[mt][n][r] << psh[mt]) - sub);
+                    const float term = psr[r] * dn[n] * (float)((acc[mt][n][r] << psh[mt]) + nsub);
                     accf[mt][n][r] = accf[mt][n][r] + term;
                 }
             }
         }
-    };
-
-    lds_barrier();  // ps_lds and block 0 in LDS
-    for (int b = 0; b < nb; b += 2) {
-        // block b from buffer 0 with a0; block b + 1 loaded meanwhile (clamped, unused past the end)
-        const int b1 = min(b + 1, nb - 1);
-        qload(b1);
-        aload(a1, b1);
-        compute(a0, b, 0);
-        __builtin_amdgcn_sched_barrier(0);  // the LDS stores wait for the loads: after the terms
-        qstore(1);
-        lds_barrier();
-        if (b + 1 >= nb) break;
-        const int b2 = min(b + 2, nb - 1);
-        qload(b2);
-        aload(a0, b2);
-        compute(a1, b + 1, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        qstore(0);
-        lds_barrier();
     }
+    wait_vm<0>();  // the clamped trailing issues complete before the workgroup ends
 
     // epilogue: lane holds rows 4 g .. 4 g + 3 of each row tile for token tl of each token tile
     float* const out = L.job[j].out;
@@ -295,7 +326,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
     }
 }
 
-template <int MT, int NT, int WR, int WT, bool PAIR>
+template <int MT, int NT, int WR, int WT, bool PAIR, int RING>
 hipError_t gemm_go(GemmLaunch& L, hipStream_t s) {
     const int rows_wg = PAIR ? WR * 16 : WR * MT * 16;
     int tiles = 0;
@@ -306,7 +337,7 @@ hipError_t gemm_go(GemmLaunch& L, hipStream_t s) {
     if (PAIR) L.job[1].tile_begin = 1 << 30;  // never selected by tile index
     const int toks_wg = WT * NT * 16;
     const dim3 grid(tiles, (L.nt + toks_wg - 1) / toks_wg);
-    k_gemm_panel<MT, NT, WR, WT, PAIR><<<grid, kGemmThreads, 0, s>>>(L);
+    k_gemm_panel<MT, NT, WR, WT, PAIR, RING><<<grid, kGemmThreads, 0, s>>>(L);
     return hipGetLastError();
 }
 
@@ -315,15 +346,24 @@ hipError_t gemm_go(GemmLaunch& L, hipStream_t s) {
 hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s) {
     if (L.njobs < 1 || L.njobs > kMaxJobs || L.nt < 1 || !L.act || (L.pair && L.njobs != 2)) return hipErrorInvalidValue;
     const int K = L.job[0].W.k;
-    if (K % 256 || K / 256 > kGemmMaxNb) return hipErrorNotSupported;
+    if (K % 256) return hipErrorNotSupported;
     for (int q = 0; q < L.njobs; q++) {
         const MvWeight& W = L.job[q].W;
         if (W.kind != KIND_PANEL || W.k != K || W.nb != K / 256 || W.n < 1 || !L.job[q].out) return hipErrorNotSupported;
     }
     if (L.pair && L.job[0].W.n != L.job[1].W.n) return hipErrorNotSupported;
     L.nb = K / 256;
-    if (L.pair) return gemm_go<2, 2, 2, 2, true>(L, s);
-    return gemm_go<2, 2, 2, 2, false>(L, s);
+    // the largest tile that still gives a workgroup per CU; else the smallest
+    int rows = 0;
+    for (int q = 0; q < L.njobs; q++)
+        if (!L.pair || q == 0) rows += L.job[q].W.n;
+    auto wgs = [&](int rt, int tt) { return ((rows + rt - 1) / rt) * ((L.nt + tt - 1) / tt); };
+    if (L.pair) {
+        if (wgs(32, 64) >= 256) return gemm_go<2, 2, 2, 2, true, 3>(L, s);
+        return gemm_go<2, 1, 2, 2, true, 3>(L, s);
+    }
+    if (wgs(64, 64) >= 256) return gemm_go<2, 2, 2, 2, false, 3>(L, s);
+    return gemm_go<1, 1, 2, 2, false, 3>(L, s);
 }
 
 }  // namespace hy
