@@ -615,15 +615,13 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 }
 
 // Chunk attention (nt tokens at consecutive positions, causal): one 512-thread workgroup per
-// (KV head, token) computes the `group` query heads that share the KV head, so each K row and
-// V tile is read once for all of them. The arithmetic is attn_task's (src/model.c:767-795) per
-// (token, head): scores by dot_bf16's four partial sums in order (src/kernels.c:1111-1121)
-// times 1/sqrtf(hd), max, expf, the sum in position order, p_j = e_j * (1 / sum) once per
-// position, then o[d] += p_j * V_j[d] in position order (axpy_bf16, :1122-1124).
-// Wavefront w works for head w % group: scores of keys (w / group) * 64 + lane + 64 * G p
-// (G = 8 / group key columns), its head's sum (wavefront h for head h), and the output
-// chains of head w / (8 / group)... with group = 4 and hd = 128: wavefronts 2h and 2h + 1 hold
-// head h's 128 dimensions, one per lane.
+// (KV head, token) computes the GRP query heads that share the KV head, so each K row and V
+// tile is read and converted once for all of them. The arithmetic is attn_task's
+// (src/model.c:767-795) per (token, head): scores by dot_bf16's four partial sums in order
+// (src/kernels.c:1111-1121) times 1/sqrtf(hd), max, expf, the sum in position order,
+// p_j = e_j * (1 / sum) once per position, then o[d] += p_j * V_j[d] in position order
+// (axpy_bf16, :1122-1124). Scores: one key per thread for every head of the group. Sums:
+// wavefront h for head h. Output: one (head, dimension) chain per lane over fp32 V tiles in LDS.
 constexpr int kAcThreads = 512;
 constexpr int kAcTile = 64;     // positions per V tile in LDS
 constexpr int kAcMaxCtx = 2048;
@@ -633,16 +631,15 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));  // arrays of it stay 
 template <int HD, int GRP>
 __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
     constexpr int NW = kAcThreads / 64;
-    constexpr int KC = NW / GRP;             // key columns: wavefronts per head in the score pass
     constexpr int KV4 = HD / 8;
     constexpr int DW = HD / 64;              // wavefronts per head in the output (one dim per lane)
-    static_assert(GRP * DW <= NW && NW % GRP == 0, "heads x dims fit the workgroup");
+    static_assert(GRP * DW <= NW && GRP <= NW, "heads x dims fit the workgroup");
     constexpr int VPT = kAcTile * KV4 / kAcThreads;  // 16-byte V pieces per thread per tile
     static_assert(VPT >= 1, "tile split");
     __shared__ __align__(16) float qs[GRP][HD];
-    __shared__ __align__(16) float sc[GRP][kAcMaxCtx];
-    __shared__ __align__(16) uint16_t vt[2][kAcTile * HD];
-    __shared__ float red[NW];
+    __shared__ __align__(16) float sc[GRP][kAcMaxCtx];   // scores, then e_j, then p_j
+    __shared__ __align__(16) float vt[kAcTile * HD];     // fp32 V tile [j][d]
+    __shared__ float red[GRP][NW];
     __shared__ float inv_s[GRP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -664,43 +661,63 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
     }
     __syncthreads();
 
-    // scores
-    const int sh = wave % GRP, kc = wave / GRP;
+    // scores of key j = tid + 512 p for every head
     const float scale = 1.0f / sqrtf((float)HD);
-    float lmax = -__builtin_inff();
-    for (int j = kc * 64 + lane; j < n; j += KC * 64) {
+    float lmax[GRP];
+#pragma unroll
+    for (int h = 0; h < GRP; h++) lmax[h] = -__builtin_inff();
+    for (int j = tid; j < n; j += kAcThreads) {
         const uint16_t* kr = K + (size_t)j * HD;
         int qo = 0;
         asm volatile("" : "+v"(qo));  // q is read per key, not held in registers across keys
-        const float* qh = &qs[sh][0] + qo;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        float acc[GRP][4];
+#pragma unroll
+        for (int h = 0; h < GRP; h++) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.f;
 #pragma unroll
         for (int i = 0; i < KV4; i++) {
-            const uint4 kv = *reinterpret_cast<const uint4*>(kr + 8 * i);
-            const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * i);
-            const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * i + 4);
-            a0 += qa.x * hy_bitsf(kv.x << 16);
-            a1 += qa.y * hy_bitsf(kv.x & 0xffff0000u);
-            a2 += qa.z * hy_bitsf(kv.y << 16);
-            a3 += qa.w * hy_bitsf(kv.y & 0xffff0000u);
-            a0 += qb.x * hy_bitsf(kv.z << 16);
-            a1 += qb.y * hy_bitsf(kv.z & 0xffff0000u);
-            a2 += qb.z * hy_bitsf(kv.w << 16);
-            a3 += qb.w * hy_bitsf(kv.w & 0xffff0000u);
+            const v4u kv = *reinterpret_cast<const v4u*>(kr + 8 * i);
+            const float kf[8] = {hy_bitsf(kv.x << 16), hy_bitsf(kv.x & 0xffff0000u), hy_bitsf(kv.y << 16),
+                                 hy_bitsf(kv.y & 0xffff0000u), hy_bitsf(kv.z << 16), hy_bitsf(kv.z & 0xffff0000u),
+                                 hy_bitsf(kv.w << 16), hy_bitsf(kv.w & 0xffff0000u)};
+#pragma unroll
+            for (int h = 0; h < GRP; h++) {
+                const float4 qa = *reinterpret_cast<const float4*>(&qs[h][0] + qo + 8 * i);
+                const float4 qb = *reinterpret_cast<const float4*>(&qs[h][0] + qo + 8 * i + 4);
+                acc[h][0] += qa.x * kf[0];
+                acc[h][1] += qa.y * kf[1];
+                acc[h][2] += qa.z * kf[2];
+                acc[h][3] += qa.w * kf[3];
+                acc[h][0] += qb.x * kf[4];
+                acc[h][1] += qb.y * kf[5];
+                acc[h][2] += qb.z * kf[6];
+                acc[h][3] += qb.w * kf[7];
+            }
         }
-        const float sj = ((a0 + a1) + (a2 + a3)) * scale;
-        sc[sh][j] = sj;
-        lmax = fmaxf(lmax, sj);
+#pragma unroll
+        for (int h = 0; h < GRP; h++) {
+            const float sj = ((acc[h][0] + acc[h][1]) + (acc[h][2] + acc[h][3])) * scale;
+            sc[h][j] = sj;
+            lmax[h] = fmaxf(lmax[h], sj);
+        }
     }
-    lmax = hy_wave_max(lmax);
-    if (lane == 0) red[wave] = lmax;
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+        const float m = hy_wave_max(lmax[h]);
+        if (lane == 0) red[h][wave] = m;
+    }
     __syncthreads();
     // e_j = expf(s_j - max) per head
     {
-        float mx = red[sh];
+        float mx[GRP];
 #pragma unroll
-        for (int c = 1; c < KC; c++) mx = fmaxf(mx, red[sh + GRP * c]);
-        for (int j = kc * 64 + lane; j < n; j += KC * 64) sc[sh][j] = hy_expf(sc[sh][j] - mx);
+        for (int h = 0; h < GRP; h++) {
+            mx[h] = red[h][0];
+#pragma unroll
+            for (int w = 1; w < NW; w++) mx[h] = fmaxf(mx[h], red[h][w]);
+        }
+        for (int j = tid; j < n; j += kAcThreads)
+#pragma unroll
+            for (int h = 0; h < GRP; h++) sc[h][j] = hy_expf(sc[h][j] - mx[h]);
     }
     __syncthreads();
     // the sum of head h in position order by wavefront h
@@ -708,15 +725,31 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
         const float sum = hy_wave_seq_sum(sc[wave], n, lane);
         if (lane == 0) inv_s[wave] = 1.0f / sum;
     }
-    // output chains: head oh, dimension od; V tiles through LDS, the next tile's loads in
-    // flight while the current one is summed
+    __syncthreads();
+    // p_j = e_j * inv, once per position (sc[j] * inv)
+    {
+        float inv[GRP];
+#pragma unroll
+        for (int h = 0; h < GRP; h++) inv[h] = inv_s[h];
+        for (int j = tid; j < n; j += kAcThreads)
+#pragma unroll
+            for (int h = 0; h < GRP; h++) sc[h][j] = sc[h][j] * inv[h];
+    }
+    // output chains: head oh, dimension od over fp32 V tiles; the next tile's loads in flight
+    // while the current one is summed
     const int oh = wave / DW, od = (wave % DW) * 64 + lane;
     float o = 0.f;
-    for (int t0 = 0, buf = 0; t0 < n; t0 += kAcTile, buf ^= 1) {
+    for (int t0 = 0; t0 < n; t0 += kAcTile) {
+        __syncthreads();  // previous tile consumed (the first time: the p_j written)
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const int f = tid + kAcThreads * i;
-            *reinterpret_cast<v4u*>(&vt[buf][(f / KV4) * HD + 8 * (f % KV4)]) = vr[i];
+            float* dstv = &vt[(f / KV4) * HD + 8 * (f % KV4)];
+            const v4u w = vr[i];
+            *reinterpret_cast<float4*>(dstv) =
+                make_float4(hy_bitsf(w.x << 16), hy_bitsf(w.x & 0xffff0000u), hy_bitsf(w.y << 16), hy_bitsf(w.y & 0xffff0000u));
+            *reinterpret_cast<float4*>(dstv + 4) =
+                make_float4(hy_bitsf(w.z << 16), hy_bitsf(w.z & 0xffff0000u), hy_bitsf(w.w << 16), hy_bitsf(w.w & 0xffff0000u));
         }
         if (t0 + kAcTile < n) {
 #pragma unroll
@@ -725,24 +758,23 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
                 vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
             }
         }
-        __syncthreads();  // tile in LDS (and, the first time, inv_s and the e_j)
+        __syncthreads();  // tile in LDS
         if (oh < GRP) {
-            const float inv = inv_s[oh];
-            const float* pe = sc[oh] + t0;
-            const uint16_t* vd = vt[buf] + od;
+            const float* pj = sc[oh] + t0;
+            const float* vd = vt + od;
             const int cnt = min(kAcTile, n - t0);
             int q = 0;
             for (; q + 8 <= cnt; q += 8) {
-                float vv[8], pj[8];
+                const float4 p0 = *reinterpret_cast<const float4*>(pj + q);
+                const float4 p1 = *reinterpret_cast<const float4*>(pj + q + 4);
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                float vv[8];
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    vv[k] = hy_bf16(vd[(q + k) * HD]);
-                    pj[k] = pe[q + k] * inv;
-                }
+                for (int k = 0; k < 8; k++) vv[k] = vd[(q + k) * HD];
 #pragma unroll
-                for (int k = 0; k < 8; k++) o += pj[k] * vv[k];
+                for (int k = 0; k < 8; k++) o += pv[k] * vv[k];
             }
-            for (; q < cnt; q++) o += (pe[q] * inv) * hy_bf16(vd[q * HD]);
+            for (; q < cnt; q++) o += pj[q] * vd[q * HD];
         }
     }
     if (oh < GRP) a.ao[(size_t)t * qdim + (size_t)(g * GRP + oh) * HD + od] = o;
