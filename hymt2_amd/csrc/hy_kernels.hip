@@ -1048,31 +1048,21 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
         src[i] = a.W.w + (size_t)min(r0 + rr, n - 1) * rowb + part * 16;
         dst[i] = rr * 20 + part * 4;
     }
-#define HY_LOAD_STAGE(st, p0, p1, p2, p3)                                          \
-    do {                                                                           \
-        p0 = *reinterpret_cast<const uint4*>(src[0] + (size_t)(st) * 64);          \
-        p1 = *reinterpret_cast<const uint4*>(src[1] + (size_t)(st) * 64);          \
-        p2 = *reinterpret_cast<const uint4*>(src[2] + (size_t)(st) * 64);          \
-        p3 = *reinterpret_cast<const uint4*>(src[3] + (size_t)(st) * 64);          \
-    } while (0)
-#define HY_STORE_STAGE(buf, p0, p1, p2, p3)                                        \
-    do {                                                                           \
-        *reinterpret_cast<uint4*>(&tile[buf][dst[0]]) = p0;                        \
-        *reinterpret_cast<uint4*>(&tile[buf][dst[1]]) = p1;                        \
-        *reinterpret_cast<uint4*>(&tile[buf][dst[2]]) = p2;                        \
-        *reinterpret_cast<uint4*>(&tile[buf][dst[3]]) = p3;                        \
-    } while (0)
-    uint4 a0, a1, a2, a3, b0, b1, b2, b3;
-    HY_LOAD_STAGE(0, a0, a1, a2, a3);
-    if (nstage > 1) HY_LOAD_STAGE(1, b0, b1, b2, b3);
-    load_vec_lds(xs, a.h, K);
-    rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);
-    HY_STORE_STAGE(0, a0, a1, a2, a3);
-    __syncthreads();
+    // four register sets in rotation, stage st in set st % 4 (no register copies, so the loads
+    // of the next three stages stay in flight); loads past the last stage repeat it, unused
+    v4u s0[4], s1[4], s2[4], s3[4];
+    auto ld = [&](v4u (&p)[4], int st) __attribute__((always_inline)) {
+        const size_t c = (size_t)min(st, nstage - 1) * 64;
+#pragma unroll
+        for (int i = 0; i < 4; i++) p[i] = *reinterpret_cast<const v4u*>(src[i] + c);
+    };
+    auto stv = [&](const v4u (&p)[4], int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *reinterpret_cast<v4u*>(&tile[buf][dst[i]]) = p[i];
+    };
     float acc = 0.f;
-    for (int st = 0; st < nstage; st++) {
-        const int buf = st & 1;
-        if (st + 2 < nstage) HY_LOAD_STAGE(st + 2, a0, a1, a2, a3);  // two stages ahead
+    auto comp = [&](int st, int buf) __attribute__((always_inline)) {
+        if (st >= nstage) return;
         const uint32_t* tr = &tile[buf][tid * 20];
         if (F16) {
             const float* xk = xs + st * 32;
@@ -1097,15 +1087,33 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
                 acc += hy_bitsf(v.w) * xk[4 * q + 3];
             }
         }
-        if (st + 1 < nstage) HY_STORE_STAGE(buf ^ 1, b0, b1, b2, b3);
+    };
+    load_vec_lds(xs, a.h, K);  // first: loads return in issue order
+    ld(s0, 0);
+    ld(s1, 1);
+    ld(s2, 2);
+    ld(s3, 3);
+    rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);  // while the weights stream
+    stv(s0, 0);
+    __syncthreads();
+    for (int st = 0; st < nstage; st += 4) {
+        comp(st, 0);
+        stv(s1, 1);
+        ld(s0, st + 4);
         __syncthreads();
-        b0 = a0;
-        b1 = a1;
-        b2 = a2;
-        b3 = a3;
+        comp(st + 1, 1);
+        stv(s2, 0);
+        ld(s1, st + 5);
+        __syncthreads();
+        comp(st + 2, 0);
+        stv(s3, 1);
+        ld(s2, st + 6);
+        __syncthreads();
+        comp(st + 3, 1);
+        stv(s0, 0);
+        ld(s3, st + 7);
+        __syncthreads();
     }
-#undef HY_LOAD_STAGE
-#undef HY_STORE_STAGE
     const int r = r0 + tid;
     if (r < n) a.logits[r] = acc;
     if (a.argmax_key) {
