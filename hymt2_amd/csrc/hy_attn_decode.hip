@@ -6,10 +6,12 @@
 // sums in order (src/kernels.c:1111-1121); the first pass's key rows load at kernel entry. Softmax (src/model.c:781-789): max (order-free), expf, the sum in
 // position order by the 8-wavefront exact segmented sum (hy_block_exact_sum8), p_j =
 // e_j * (1 / sum). Output (axpy_bf16, src/kernels.c:1122-1124): o[d] += p_j * V_j[d] in
-// position order. Per tile of 128 positions all threads form the products p_j * V_j[d] (each
-// rounded to fp32, as the reference rounds them) into a [d][j] LDS tile; then one lane per
-// dimension adds its row in position order, four products per LDS read, while the next tile's
-// V rows load. The fp32 output row goes to `ao`; the o-projection quantizes it.
+// position order, as a pipeline over tiles of 96 positions: wavefronts 2-7 form the products
+// p_j * V_j[d] (each rounded to fp32, as the reference rounds them) of tile t + 1 into one half
+// of a double-buffered [d][j] LDS tile while wavefronts 0-1 (one lane per dimension) add tile t
+// from the other half in position order, four products per LDS read; one LDS-only barrier per
+// tile, V rows loaded three tiles ahead. The fp32 output row goes to `ao`; the o-projection
+// quantizes it.
 #include "hy_kernels.h"
 
 namespace hy {
@@ -18,8 +20,11 @@ namespace {
 
 constexpr int kA1Threads = 512;
 constexpr int kA1Waves = kA1Threads / 64;
-constexpr int kA1Tile = 128;           // positions per product tile
-constexpr int kA1Row = kA1Tile + 4;    // floats per [d] row of the product tile (16-byte rows)
+constexpr int kA1Tile = 96;            // positions per product tile
+constexpr int kA1Row = kA1Tile + 4;    // floats per [d] row of a product tile: the 16 lanes of a
+                                       // 16-byte read (rows d..d+15) start in 16 distinct bank quads
+constexpr int kA1Prod = kA1Threads - 128;  // producer threads (wavefronts 2-7)
+constexpr int kA1Chunk = 32;           // positions per chain step (8 LDS reads of 4 products)
 constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
 
 __device__ __forceinline__ void bf16x8f(const uint4& v, float* f) {
@@ -115,18 +120,39 @@ __device__ __forceinline__ void a1_load_v(uint4 (&v)[HD / 32], const uint16_t* V
     for (int i = 0; i < HD / 32; i++) v[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (pc0 + 4 * i));
 }
 
-// o += row[0] + row[1] + ... + row[cnt - 1] in order, the LDS reads running 32 positions ahead
-// of the adds for a full tile; a partial tile reads 32 positions at a time up to cnt.
-template <bool FULL>
-__device__ __forceinline__ void a1_chain(const float4* pr, int cnt, float& o) {
-    if constexpr (FULL) {
-        float4 w0[8], w1[8];
+// o += row[0] + row[1] + ... in order over the first nch chunks of 32 positions of a tile row;
+// the producers zero the products past the row's end, and o + 0 == o exactly (o is never -0:
+// it starts at +0, and a sum of nonzero addends that cancels rounds to +0). The LDS reads of the
+// next chunk are in flight while a chunk is added.
+__device__ __forceinline__ void a1_chain(const float4* pr, int nch, float& o) {
+    static_assert(kA1Tile == 3 * kA1Chunk, "three chunks per tile");
+    float4 w0[8], w1[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) w0[i] = pr[i];
+    for (int i = 0; i < 8; i++) w0[i] = pr[i];
+    if (nch > 1) {
 #pragma unroll
-        for (int q = 0; q < kA1Tile / 4; q += 16) {
+        for (int i = 0; i < 8; i++) w1[i] = pr[8 + i];
+    }
 #pragma unroll
-            for (int i = 0; i < 8; i++) w1[i] = pr[min(q + 8 + i, kA1Tile / 4 - 1)];
+    for (int i = 0; i < 8; i++) {
+        o += w0[i].x;
+        o += w0[i].y;
+        o += w0[i].z;
+        o += w0[i].w;
+    }
+    if (nch > 1) {
+        if (nch > 2) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) w0[i] = pr[16 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o += w1[i].x;
+            o += w1[i].y;
+            o += w1[i].z;
+            o += w1[i].w;
+        }
+        if (nch > 2) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 o += w0[i].x;
@@ -134,67 +160,37 @@ __device__ __forceinline__ void a1_chain(const float4* pr, int cnt, float& o) {
                 o += w0[i].z;
                 o += w0[i].w;
             }
-#pragma unroll
-            for (int i = 0; i < 8; i++) w0[i] = pr[min(q + 16 + i, kA1Tile / 4 - 1)];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                o += w1[i].x;
-                o += w1[i].y;
-                o += w1[i].z;
-                o += w1[i].w;
-            }
-        }
-    } else {
-        for (int q = 0; q < cnt; q += 32) {
-            float4 w[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) w[i] = pr[min(q / 4 + i, kA1Tile / 4 - 1)];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int b = q + 4 * i;
-                if (b < cnt) o += w[i].x;
-                if (b + 1 < cnt) o += w[i].y;
-                if (b + 2 < cnt) o += w[i].z;
-                if (b + 3 < cnt) o += w[i].w;
-            }
         }
     }
 }
 
-// One tile of the output: the products p_j * V_j[d] (p_j = e_j * inv, formed once per position
-// as the reference forms it) into prod[d][j], then one lane per dimension adds its row in
-// position order.
+// The products p_j * V_j[d] of one tile (p_j = e_j * inv, formed once per position as the
+// reference forms it) for this producer thread's position jj and pieces pg + 4 i, into
+// buf[d][jj]; +0 past the row's end.
 template <int HD>
-__device__ __forceinline__ void a1_tile(const uint4 (&v)[HD / 32], float* prod, const float* ex, const uint16_t* vb,
-                                        float inv, int t0, int jj, int pc0, int pos, int n, int tid, float& o) {
-    {
-        const int j = t0 + jj;
-        const float pj = ex[min(j, n - 1)] * inv;
+__device__ __forceinline__ void a1_products(const uint4 (&v)[HD / 32], float* buf, const float* ex,
+                                            const uint16_t* vb, float inv, int t0, int jj, int pg, int pos, int n) {
+    const int j = t0 + jj;
+    const bool live = j < n;
+    const float pj = ex[min(j, n - 1)] * inv;
 #pragma unroll
-        for (int i = 0; i < HD / 32; i++) {
-            const int pc = pc0 + 4 * i;
-            float vf[8];
-            bf16x8f(j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : v[i], vf);
+    for (int i = 0; i < HD / 32; i++) {
+        const int pc = pg + 4 * i;
+        float vf[8];
+        bf16x8f(j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : v[i], vf);
 #pragma unroll
-            for (int e = 0; e < 8; e++) prod[(8 * pc + e) * kA1Row + jj] = pj * vf[e];
-        }
+        for (int e = 0; e < 8; e++) buf[(8 * pc + e) * kA1Row + jj] = live ? pj * vf[e] : 0.f;
     }
-    __syncthreads();
-    if (tid < HD) {
-        const float4* pr = reinterpret_cast<const float4*>(prod + tid * kA1Row);
-        const int cnt = min(kA1Tile, n - t0);
-        if (cnt == kA1Tile) a1_chain<true>(pr, cnt, o);
-        else a1_chain<false>(pr, cnt, o);
-    }
-    __syncthreads();
 }
 
 // LDS of one head's attention.
 template <int HD>
 struct A1Smem {
-    alignas(16) float ex[kA1MaxCtx];      // e_j = expf(s_j - max)
-    alignas(16) float prod[HD * kA1Row];  // products of one tile, [d][j]
-    HyExactLdsT<kA1Waves> exs;
+    alignas(16) float ex[kA1MaxCtx];  // e_j = expf(s_j - max)
+    union {
+        HyExactLdsT<kA1Waves> exs;            // the softmax sum of long rows
+        alignas(16) float prod[2][HD * kA1Row];  // then the products of two tiles, [d][j]
+    };
     alignas(16) float scr[2][HD];
     alignas(16) float qn[HD];
     alignas(16) uint16_t kb[HD];
@@ -205,8 +201,8 @@ struct A1Smem {
 
 // Phases 1-4 of one head's attention, every thread of the workgroup: this token's rows (x:
 // q / k / v elements lane + 64 i for wavefronts 0 / 1 / 2), its RoPE row (rc, rs) and the q / k
-// norm weights (nw) are loaded; the key rows of the first pass (kA, rows below pos) and the
-// first V tile (v0) are in flight.
+// norm weights (nw) are loaded; the key rows of the first pass (kA, rows below pos) and, in the
+// producer wavefronts (2-7), the first V tile (v0) are in flight.
 template <int HD>
 __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const float (&x)[HD / 64],
                                         const float (&rc)[HD / 64], const float (&rs)[HD / 64],
@@ -214,11 +210,11 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
                                         int pos) {
     constexpr int KV4 = HD / 8;                 // 16-byte pieces of one K / V row
     constexpr int RPL = HD / 64;                // row elements per lane
-    constexpr int PPT = KV4 / 4;                // V pieces per thread per tile
+    constexpr int PPT = KV4 / 4;                // V pieces per producer thread per tile
     constexpr int PASSES = kA1MaxCtx / kA1Threads;
-    static_assert(kA1Waves == 8 && KV4 % 4 == 0, "8 wavefronts: 2 x 64 positions x 4 piece columns");
+    static_assert(kA1Waves == 8 && kA1Prod == 4 * kA1Tile && KV4 % 4 == 0,
+                  "producers: 96 positions x 4 piece columns");
     float* ex = S.ex;
-    float* prod = S.prod;
     float(&scr)[2][HD] = S.scr;
     float* qn = S.qn;
     uint16_t* kb = S.kb;
@@ -233,7 +229,8 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     const int cap = a.ctx - 1;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
-    const int jj = lane + 64 * (wave & 1), pc0 = wave >> 1;
+    const bool prd = wave >= 2;
+    const int jj = prd ? (tid - 128) % kA1Tile : 0, pg = prd ? (tid - 128) / kA1Tile : 0;
     const int n = pos + 1;
     uint4 kB[KV4];
     uint4 v1[PPT], v2[PPT];
@@ -282,12 +279,12 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
             lmax = fmaxf(lmax, sv[p + 1]);
         }
     }
-    if (kA1Tile + jj < pos) a1_load_v<HD>(v1, V, kA1Tile, jj, pc0, cap);
-    if (2 * kA1Tile + jj < pos) a1_load_v<HD>(v2, V, 2 * kA1Tile, jj, pc0, cap);
+    if (prd && kA1Tile + jj < pos) a1_load_v<HD>(v1, V, kA1Tile, jj, pg, cap);
+    if (prd && 2 * kA1Tile + jj < pos) a1_load_v<HD>(v2, V, 2 * kA1Tile, jj, pg, cap);
     a1_fence();  // issued here, not next to their first use
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
-    __syncthreads();
+    hy_lds_barrier();
 
     // 3. softmax (src/model.c:781-789): max (order-free), e_j = expf(s_j - max), their sum in
     //    position order, inv = 1 / sum. Short rows: the lane-serial chain of wavefront 0; long
@@ -303,13 +300,13 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
             if (j - tid >= n) break;
             if (j < n) ex[j] = hy_expf(sv[p] - mx);
         }
-        __syncthreads();
+        hy_lds_barrier();
         if (n <= kA1SerialSum) {
             if (wave == 0) {
                 const float sum = hy_wave_seq_sum(ex, n, lane);
                 if (lane == 0) S.stat = 1.0f / sum;
             }
-            __syncthreads();
+            hy_lds_barrier();
             inv = S.stat;
         } else {
             const int e0 = 8 * tid;
@@ -324,25 +321,44 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
                 for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? ev[i] : 0.f;
             }
             inv = 1.0f / hy_block_exact_sum8<kA1Waves, false>(e, S.exs, wave, lane);
+            hy_lds_barrier();  // the product tiles reuse the sum's LDS
         }
     }
 
-    // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16); three V tiles in flight
-    float o = 0.f;
-    const int last = max(pos - 1, 0);
-    for (int t0 = 0; t0 < n; t0 += 3 * kA1Tile) {
-        a1_tile<HD>(v0, prod, ex, vb, inv, t0, jj, pc0, pos, n, tid, o);
-        a1_load_v<HD>(v0, V, t0 + 3 * kA1Tile, jj, pc0, last);
-        if (t0 + kA1Tile < n) {
-            a1_tile<HD>(v1, prod, ex, vb, inv, t0 + kA1Tile, jj, pc0, pos, n, tid, o);
-            a1_load_v<HD>(v1, V, t0 + 4 * kA1Tile, jj, pc0, last);
+    // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16). Barrier t: tile t is in
+    //    buffer t % 2, and tile t - 1's buffer has been read. Wavefronts 0 .. HD/64 - 1 add tile t
+    //    after barrier t; the producers form tile t before it, with V three tiles ahead.
+    const int tiles = (n + kA1Tile - 1) / kA1Tile;
+    if (wave < HD / 64) {
+        __builtin_amdgcn_s_setprio(3);  // the chain is the critical path: its adds issue first
+        float o = 0.f;
+        for (int t = 0; t < tiles; t++) {
+            hy_lds_barrier();
+            const int cnt = min(kA1Tile, n - t * kA1Tile);
+            a1_chain(reinterpret_cast<const float4*>(S.prod[t & 1] + tid * kA1Row), (cnt + kA1Chunk - 1) / kA1Chunk, o);
         }
-        if (t0 + 2 * kA1Tile < n) {
-            a1_tile<HD>(v2, prod, ex, vb, inv, t0 + 2 * kA1Tile, jj, pc0, pos, n, tid, o);
-            a1_load_v<HD>(v2, V, t0 + 5 * kA1Tile, jj, pc0, last);
+        a.ao[(size_t)h * HD + tid] = o;
+    } else if (prd) {
+        const int last = max(pos - 1, 0);
+        for (int t = 0; t < tiles; t += 3) {
+            const int t0 = t * kA1Tile;
+            a1_products<HD>(v0, S.prod[t & 1], ex, vb, inv, t0, jj, pg, pos, n);
+            a1_load_v<HD>(v0, V, t0 + 3 * kA1Tile, jj, pg, last);
+            hy_lds_barrier();
+            if (t + 1 < tiles) {
+                a1_products<HD>(v1, S.prod[(t + 1) & 1], ex, vb, inv, t0 + kA1Tile, jj, pg, pos, n);
+                a1_load_v<HD>(v1, V, t0 + 4 * kA1Tile, jj, pg, last);
+                hy_lds_barrier();
+            }
+            if (t + 2 < tiles) {
+                a1_products<HD>(v2, S.prod[t & 1], ex, vb, inv, t0 + 2 * kA1Tile, jj, pg, pos, n);
+                a1_load_v<HD>(v2, V, t0 + 5 * kA1Tile, jj, pg, last);
+                hy_lds_barrier();
+            }
         }
+    } else {
+        for (int t = 0; t < tiles; t++) hy_lds_barrier();
     }
-    if (tid < HD) a.ao[(size_t)h * HD + tid] = o;
 }
 
 template <int HD>
@@ -355,12 +371,13 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     const int half = a.rope_half;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
-    const int jj = lane + 64 * (wave & 1), pc0 = wave >> 1;
+    const bool prd = wave >= 2;
+    const int jj = prd ? (tid - 128) % kA1Tile : 0, pg = prd ? (tid - 128) / kA1Tile : 0;
 
     // 0. loads: the position (scalar), this token's q / k / v row for wavefronts 0 / 1 / 2
     //    with the norm weights and the position's RoPE row (rope_cur when the position lives in
-    //    device memory), then the key rows of the first pass and the first V tile, only those
-    //    below the position
+    //    device memory), then the key rows of the first pass and (producers) the first V tile,
+    //    only those below the position
     const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
     float x[RPL], rc[RPL], rs[RPL], nw[RPL];
     {
@@ -381,7 +398,7 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     uint4 kA[HD / 8];
     if (tid < pos) a1_load_key<HD>(kA, K, tid);
     uint4 v0[HD / 32];
-    if (jj < pos) a1_load_v<HD>(v0, V, 0, jj, pc0, a.ctx - 1);
+    if (prd && jj < pos) a1_load_v<HD>(v0, V, 0, jj, pg, a.ctx - 1);
     a1_fence();
     a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, pos);
 }

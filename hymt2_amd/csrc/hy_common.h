@@ -58,6 +58,12 @@ __device__ inline uint16_t hy_to_bf16(float f) {
 #define HY_DPP_HMIRROR 0x141
 #define HY_DPP_MIRROR 0x140
 
+// Workgroup barrier for LDS only: waits for this wave's LDS operations, not for its global
+// loads, so prefetches stay in flight across it (a __syncthreads fence would drain them).
+__device__ __forceinline__ void hy_lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int CTRL>
 __device__ inline int hy_dpp(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);

@@ -51,12 +51,6 @@ __device__ __forceinline__ v4i as_v4i(const uint4& u) {
     return r;
 }
 
-// Workgroup barrier for LDS only: waits for this wave's LDS operations, not for its global
-// loads, so prefetches stay in flight across it (a __syncthreads fence would drain them).
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // Direct global -> LDS loads: lane L's 16 (4) bytes from src land at LDS address dst + 16 L
 // (4 L), dst uniform (an LDS byte address). Written as assembly so that the compiler does not
 // order the workgroup's LDS reads behind them: the kernel waits for them itself (wait_vm), for
@@ -222,7 +216,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
         else if (wave == 1) wait_vm<(RING - 2) * ((TOTAL + 2) / 4)>();
         else if (wave == 2) wait_vm<(RING - 2) * ((TOTAL + 1) / 4)>();
         else wait_vm<(RING - 2) * (TOTAL / 4)>();
-        lds_barrier();
+        hy_lds_barrier();
         issue(min(b + RING - 1, nb - 1), (b + RING - 1) % RING);
         const Stage& S = ring[buf];
 

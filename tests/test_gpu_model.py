@@ -170,6 +170,29 @@ def test_hidden2048_chunked_prefill(backend, mode):
         fm.close()
 
 
+def test_hidden2048_long_context_decode(backend):
+    """The single-token attention at hd 128 over long rows: one layer at the 1.8B shapes, a
+    640-token prompt fed one token at a time (every position through the decode attention: up
+    to 7 product tiles of 96 positions, the exact segmented softmax sum past 256 keys), the last
+    logits vs the oracle bit for bit, then 40 device greedy ids (rows up to 680)."""
+    shape = synth.ModelShape(n_layer=1, vocab=1000, ctx=700)
+    model = synth.make_model(shape, mode="stq", seed=59)
+    prompt = synth.rand_prompt(synth.rng(60), 640, shape.vocab)
+    om = O.OracleModel(model, threads=16)
+    ref = None
+    for i in range(0, len(prompt), 16):
+        c = prompt[i:i + 16]
+        ref = om.forward(c, i, want_logits=(i + len(c) == len(prompt)))
+    want = O.OracleModel(model, threads=16).generate(prompt, 40, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt), batch=1)), bits(ref))
+        ids, _ = fm.generate_device(prompt, 40)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
 def test_generate_rejects_overlong_runs(backend):
     model = synth.make_model(synth.ModelShape(n_layer=1, hidden=256, ffn=512, heads=2, kv_heads=1, hdim=128,
                                               vocab=300, ctx=64), mode="stq", seed=45)
