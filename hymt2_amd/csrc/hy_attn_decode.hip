@@ -21,8 +21,6 @@ namespace {
 constexpr int kA1Threads = 512;
 constexpr int kA1Waves = kA1Threads / 64;
 constexpr int kA1Tile = 96;            // positions per product tile
-constexpr int kA1Row = kA1Tile + 4;    // floats per [d] row of a product tile: the 16 lanes of a
-                                       // 16-byte read (rows d..d+15) start in 16 distinct bank quads
 constexpr int kA1Prod = kA1Threads - 128;  // producer threads (wavefronts 2-7)
 constexpr int kA1Chunk = 32;           // positions per chain step (8 LDS reads of 4 products)
 constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
@@ -111,76 +109,116 @@ __device__ __forceinline__ void a1_load_key(uint4 (&k)[HD / 8], const uint16_t* 
     for (int i = 0; i < HD / 8; i++) k[i] = *reinterpret_cast<const uint4*>(K + (size_t)row * HD + 8 * i);
 }
 
-// V pieces of one tile for this thread: row t0 + jj (clamped to `last`), piece columns
-// pc0 + 4 i
+// Producer work split: V rows in quads of 4 dimensions (8 bytes). Producer thread p
+// (0 .. kA1Prod - 1) owns quad p % QPR of rows p / QPR + RSTEP k, k < IPT, of every tile: a
+// wavefront's loads of one k cover whole rows (contiguous global memory), its product stores
+// one contiguous run of the [j][d] tile.
 template <int HD>
-__device__ __forceinline__ void a1_load_v(uint4 (&v)[HD / 32], const uint16_t* V, int t0, int jj, int pc0, int last) {
-    const int j = min(t0 + jj, last);
+struct A1Split {
+    static constexpr int QPR = HD / 4;                   // quads per row
+    static constexpr int IPT = kA1Tile * QPR / kA1Prod;  // quads per producer thread per tile
+    static constexpr int RSTEP = kA1Prod / QPR;          // rows between a thread's quads
+    static_assert(kA1Prod % QPR == 0 && kA1Tile % RSTEP == 0, "whole rows per producer step");
+};
+
+// V quads of one tile for producer thread p: rows t0 + row (clamped to `last`)
+template <int HD>
+__device__ __forceinline__ void a1_load_v(uint2 (&v)[A1Split<HD>::IPT], const uint16_t* V, int t0, int p, int last) {
+    using P = A1Split<HD>;
+    const int r0 = t0 + p / P::QPR, q = p % P::QPR;
 #pragma unroll
-    for (int i = 0; i < HD / 32; i++) v[i] = *reinterpret_cast<const uint4*>(V + (size_t)j * HD + 8 * (pc0 + 4 * i));
+    for (int k = 0; k < P::IPT; k++)
+        v[k] = *reinterpret_cast<const uint2*>(V + (size_t)min(r0 + P::RSTEP * k, last) * HD + 4 * q);
 }
 
-// o += row[0] + row[1] + ... in order over the first nch chunks of 32 positions of a tile row;
-// the producers zero the products past the row's end, and o + 0 == o exactly (o is never -0:
-// it starts at +0, and a sum of nonzero addends that cancels rounds to +0). The LDS reads of the
+// e_j of this producer thread's rows of the tile at t0
+template <int HD>
+__device__ __forceinline__ void a1_load_e(float (&e)[A1Split<HD>::IPT], const float* ex, int t0, int p, int n) {
+    using P = A1Split<HD>;
+    const int r0 = t0 + p / P::QPR;
+#pragma unroll
+    for (int k = 0; k < P::IPT; k++) e[k] = ex[min(r0 + P::RSTEP * k, n - 1)];
+}
+
+// o += col[0] + col[HD] + col[2 HD] + ... in position order over the first nch chunks of 32
+// positions of a tile column ([j][d] layout: lane d reads col = tile + d, two positions per LDS
+// read); the producers zero the products past the row's end, and o + 0 == o exactly (o is never
+// -0: it starts at +0, and a sum of nonzero addends that cancels rounds to +0). The reads of the
 // next chunk are in flight while a chunk is added.
-__device__ __forceinline__ void a1_chain(const float4* pr, int nch, float& o) {
+template <int HD>
+__device__ __forceinline__ void a1_chain(const float* col, int nch, float& o) {
     static_assert(kA1Tile == 3 * kA1Chunk, "three chunks per tile");
-    float4 w0[8], w1[8];
+    float w0[kA1Chunk], w1[kA1Chunk];
 #pragma unroll
-    for (int i = 0; i < 8; i++) w0[i] = pr[i];
+    for (int i = 0; i < kA1Chunk; i++) w0[i] = col[i * HD];
     if (nch > 1) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) w1[i] = pr[8 + i];
+        for (int i = 0; i < kA1Chunk; i++) w1[i] = col[(kA1Chunk + i) * HD];
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        o += w0[i].x;
-        o += w0[i].y;
-        o += w0[i].z;
-        o += w0[i].w;
-    }
+    for (int i = 0; i < kA1Chunk; i++) o += w0[i];
     if (nch > 1) {
         if (nch > 2) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) w0[i] = pr[16 + i];
+            for (int i = 0; i < kA1Chunk; i++) w0[i] = col[(2 * kA1Chunk + i) * HD];
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            o += w1[i].x;
-            o += w1[i].y;
-            o += w1[i].z;
-            o += w1[i].w;
-        }
+        for (int i = 0; i < kA1Chunk; i++) o += w1[i];
         if (nch > 2) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                o += w0[i].x;
-                o += w0[i].y;
-                o += w0[i].z;
-                o += w0[i].w;
-            }
+            for (int i = 0; i < kA1Chunk; i++) o += w0[i];
         }
     }
 }
 
 // The products p_j * V_j[d] of one tile (p_j = e_j * inv, formed once per position as the
-// reference forms it) for this producer thread's position jj and pieces pg + 4 i, into
-// buf[d][jj]; +0 past the row's end.
-template <int HD>
-__device__ __forceinline__ void a1_products(const uint4 (&v)[HD / 32], float* buf, const float* ex,
-                                            const uint16_t* vb, float inv, int t0, int jj, int pg, int pos, int n) {
-    const int j = t0 + jj;
-    const bool live = j < n;
-    const float pj = ex[min(j, n - 1)] * inv;
+// reference forms it) for producer thread p's quads, into buf[j][d] (16-byte stores). EDGE (the
+// tile reaches the row's end): position `pos` takes this token's V row from LDS (vb, all read
+// before any product is stored) and positions past the row are +0.
+template <int HD, bool EDGE>
+__device__ __forceinline__ void a1_products(const uint2 (&v)[A1Split<HD>::IPT], float* buf,
+                                            const float (&e)[A1Split<HD>::IPT], const uint16_t* vb, float inv, int t0,
+                                            int p, int pos, int n) {
+    using P = A1Split<HD>;
+    const int r0 = p / P::QPR, q = p % P::QPR;
+    uint2 w[P::IPT];
 #pragma unroll
-    for (int i = 0; i < HD / 32; i++) {
-        const int pc = pg + 4 * i;
-        float vf[8];
-        bf16x8f(j == pos ? *reinterpret_cast<const uint4*>(vb + 8 * pc) : v[i], vf);
+    for (int k = 0; k < P::IPT; k++) w[k] = v[k];
+    if constexpr (EDGE) {
+        const uint2 b = *reinterpret_cast<const uint2*>(vb + 4 * q);
 #pragma unroll
-        for (int e = 0; e < 8; e++) buf[(8 * pc + e) * kA1Row + jj] = live ? pj * vf[e] : 0.f;
+        for (int k = 0; k < P::IPT; k++) {
+            const bool cur = t0 + r0 + P::RSTEP * k == pos;
+            w[k] = {cur ? b.x : w[k].x, cur ? b.y : w[k].y};
+        }
     }
+#pragma unroll
+    for (int k = 0; k < P::IPT; k++) {
+        const int r = r0 + P::RSTEP * k;
+        const float pj = e[k] * inv;
+        float4 x = {pj * hy_bitsf(w[k].x << 16), pj * hy_bitsf(w[k].x & 0xffff0000u), pj * hy_bitsf(w[k].y << 16),
+                    pj * hy_bitsf(w[k].y & 0xffff0000u)};
+        if (EDGE && t0 + r >= n) x = {0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<float4*>(buf + r * HD + 4 * q) = x;
+    }
+}
+
+// One producer step: when the tile at t0 exists (a uniform branch), its products (the edge form
+// when it reaches the row's end) and its barrier; then, on every path, v refilled with the rows
+// three tiles on and e with the next tile's e_j. The loads are unconditional so that every path
+// through a group of three steps leaves the same loads in flight, and the compiler's wait before
+// a tile's products leaves the later tiles' loads outstanding.
+template <int HD>
+__device__ __forceinline__ void a1_produce(uint2 (&v)[A1Split<HD>::IPT], float* buf, float (&e)[A1Split<HD>::IPT],
+                                           const float* ex, const uint16_t* vb, const uint16_t* V, float inv, int t0,
+                                           int p, int pos, int n, int last) {
+    if (t0 < n) {
+        if (t0 + kA1Tile < n) a1_products<HD, false>(v, buf, e, vb, inv, t0, p, pos, n);
+        else a1_products<HD, true>(v, buf, e, vb, inv, t0, p, pos, n);
+    }
+    a1_load_v<HD>(v, V, t0 + 3 * kA1Tile, p, last);
+    a1_load_e<HD>(e, ex, t0 + kA1Tile, p, n);
+    if (t0 < n) hy_lds_barrier();
 }
 
 // LDS of one head's attention.
@@ -189,7 +227,7 @@ struct A1Smem {
     alignas(16) float ex[kA1MaxCtx];  // e_j = expf(s_j - max)
     union {
         HyExactLdsT<kA1Waves> exs;            // the softmax sum of long rows
-        alignas(16) float prod[2][HD * kA1Row];  // then the products of two tiles, [d][j]
+        alignas(16) float prod[2][kA1Tile * HD];  // then the products of two tiles, [j][d]
     };
     alignas(16) float scr[2][HD];
     alignas(16) float qn[HD];
@@ -206,14 +244,12 @@ struct A1Smem {
 template <int HD>
 __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const float (&x)[HD / 64],
                                         const float (&rc)[HD / 64], const float (&rs)[HD / 64],
-                                        const float (&nw)[HD / 64], uint4 (&kA)[HD / 8], uint4 (&v0)[HD / 32],
+                                        const float (&nw)[HD / 64], uint4 (&kA)[HD / 8], uint2 (&v0)[A1Split<HD>::IPT],
                                         int pos) {
     constexpr int KV4 = HD / 8;                 // 16-byte pieces of one K / V row
     constexpr int RPL = HD / 64;                // row elements per lane
-    constexpr int PPT = KV4 / 4;                // V pieces per producer thread per tile
     constexpr int PASSES = kA1MaxCtx / kA1Threads;
-    static_assert(kA1Waves == 8 && kA1Prod == 4 * kA1Tile && KV4 % 4 == 0,
-                  "producers: 96 positions x 4 piece columns");
+    static_assert(kA1Waves == 8 && KV4 % 4 == 0, "8 wavefronts");
     float* ex = S.ex;
     float(&scr)[2][HD] = S.scr;
     float* qn = S.qn;
@@ -221,7 +257,7 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     uint16_t* vb = S.vb;
     float* red = S.red;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = blockIdx.x;
     const int group = a.heads / a.kv_heads;
     const int g = h / group;
@@ -230,10 +266,10 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
     const bool prd = wave >= 2;
-    const int jj = prd ? (tid - 128) % kA1Tile : 0, pg = prd ? (tid - 128) / kA1Tile : 0;
+    const int pp = prd ? tid - 128 : lane;  // producer index (other wavefronts: any valid one)
     const int n = pos + 1;
     uint4 kB[KV4];
-    uint4 v1[PPT], v2[PPT];
+    uint2 v1[A1Split<HD>::IPT], v2[A1Split<HD>::IPT];
 
     // 1. RoPE + RMSNorm of q (wavefront 0) and k (1), bf16 of k and v
     if (wave < 2) {
@@ -279,8 +315,11 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
             lmax = fmaxf(lmax, sv[p + 1]);
         }
     }
-    if (prd && kA1Tile + jj < pos) a1_load_v<HD>(v1, V, kA1Tile, jj, pg, cap);
-    if (prd && 2 * kA1Tile + jj < pos) a1_load_v<HD>(v2, V, 2 * kA1Tile, jj, pg, cap);
+    // V tiles 1 and 2, unconditionally (rows clamped below the position; every wavefront), so
+    // that on every path the same loads follow tile 0's and the producers' waits leave them out
+    const int last = max(pos - 1, 0);
+    a1_load_v<HD>(v1, V, kA1Tile, pp, last);
+    a1_load_v<HD>(v2, V, 2 * kA1Tile, pp, last);
     a1_fence();  // issued here, not next to their first use
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
@@ -327,7 +366,8 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
 
     // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16). Barrier t: tile t is in
     //    buffer t % 2, and tile t - 1's buffer has been read. Wavefronts 0 .. HD/64 - 1 add tile t
-    //    after barrier t; the producers form tile t before it, with V three tiles ahead.
+    //    after barrier t; the producers form tile t before it, with V three tiles ahead, in
+    //    groups of three steps (one loop exit; steps past the row only load).
     const int tiles = (n + kA1Tile - 1) / kA1Tile;
     if (wave < HD / 64) {
         __builtin_amdgcn_s_setprio(3);  // the chain is the critical path: its adds issue first
@@ -335,26 +375,17 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
         for (int t = 0; t < tiles; t++) {
             hy_lds_barrier();
             const int cnt = min(kA1Tile, n - t * kA1Tile);
-            a1_chain(reinterpret_cast<const float4*>(S.prod[t & 1] + tid * kA1Row), (cnt + kA1Chunk - 1) / kA1Chunk, o);
+            a1_chain<HD>(S.prod[t & 1] + tid, (cnt + kA1Chunk - 1) / kA1Chunk, o);
         }
         a.ao[(size_t)h * HD + tid] = o;
     } else if (prd) {
-        const int last = max(pos - 1, 0);
+        float e[A1Split<HD>::IPT];
+        a1_load_e<HD>(e, ex, 0, pp, n);
         for (int t = 0; t < tiles; t += 3) {
             const int t0 = t * kA1Tile;
-            a1_products<HD>(v0, S.prod[t & 1], ex, vb, inv, t0, jj, pg, pos, n);
-            a1_load_v<HD>(v0, V, t0 + 3 * kA1Tile, jj, pg, last);
-            hy_lds_barrier();
-            if (t + 1 < tiles) {
-                a1_products<HD>(v1, S.prod[(t + 1) & 1], ex, vb, inv, t0 + kA1Tile, jj, pg, pos, n);
-                a1_load_v<HD>(v1, V, t0 + 4 * kA1Tile, jj, pg, last);
-                hy_lds_barrier();
-            }
-            if (t + 2 < tiles) {
-                a1_products<HD>(v2, S.prod[t & 1], ex, vb, inv, t0 + 2 * kA1Tile, jj, pg, pos, n);
-                a1_load_v<HD>(v2, V, t0 + 5 * kA1Tile, jj, pg, last);
-                hy_lds_barrier();
-            }
+            a1_produce<HD>(v0, S.prod[t & 1], e, ex, vb, V, inv, t0, pp, pos, n, last);
+            a1_produce<HD>(v1, S.prod[(t + 1) & 1], e, ex, vb, V, inv, t0 + kA1Tile, pp, pos, n, last);
+            a1_produce<HD>(v2, S.prod[t & 1], e, ex, vb, V, inv, t0 + 2 * kA1Tile, pp, pos, n, last);
         }
     } else {
         for (int t = 0; t < tiles; t++) hy_lds_barrier();
@@ -365,20 +396,23 @@ template <int HD>
 __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     constexpr int RPL = HD / 64;
     __shared__ A1Smem<HD> S;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = blockIdx.x;
     const int g = h / (a.heads / a.kv_heads);
     const int half = a.rope_half;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
     const bool prd = wave >= 2;
-    const int jj = prd ? (tid - 128) % kA1Tile : 0, pg = prd ? (tid - 128) / kA1Tile : 0;
+    const int pp = prd ? tid - 128 : lane;
 
     // 0. loads: the position (scalar), this token's q / k / v row for wavefronts 0 / 1 / 2
     //    with the norm weights and the position's RoPE row (rope_cur when the position lives in
-    //    device memory), then the key rows of the first pass and (producers) the first V tile,
-    //    only those below the position
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
+    //    device memory), then the key rows of the first pass (those below the position) and the
+    //    first V tile
+    // readfirstlane: the position is one value for the workgroup; loaded through a pointer the
+    // compiler could not tell that, and every loop bound and branch derived from it would compile
+    // as divergent (exec-masked exits that merge back into the loops)
+    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
     float x[RPL], rc[RPL], rs[RPL], nw[RPL];
     {
         const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
@@ -397,8 +431,8 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     a1_fence();  // the row loads go out first: loads return in issue order
     uint4 kA[HD / 8];
     if (tid < pos) a1_load_key<HD>(kA, K, tid);
-    uint4 v0[HD / 32];
-    if (prd && jj < pos) a1_load_v<HD>(v0, V, 0, jj, pg, a.ctx - 1);
+    uint2 v0[A1Split<HD>::IPT];
+    a1_load_v<HD>(v0, V, 0, pp, max(pos - 1, 0));
     a1_fence();
     a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, pos);
 }

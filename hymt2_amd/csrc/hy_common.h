@@ -370,8 +370,10 @@ __device__ inline float hy_wave_exact_sq_sum_v(const float (&xv)[32], int lane) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // 6. the walk: s + delta is exact; then the segment's addends one fp32 add at a time
-    float s = 0.f;
+    // 6. the walk: s + delta is exact; then the segment's addends one fp32 add at a time. Lane
+    //    k holds row k of a batch of 64; step k adds row k to the running sum rotated in from
+    //    lane k - 1 (DPP wave_ror:1; lane 0 takes lane 63's, the previous batch's end).
+    float t = 0.f;
     for (int base = 0; base < nd; base += 64) {
         float r[17];
         const int k = min(base + lane, 127);
@@ -379,12 +381,13 @@ __device__ inline float hy_wave_exact_sq_sum_v(const float (&xv)[32], int lane) 
         for (int i = 0; i < 17; i++) r[i] = rows[k][i];
         const int cnt = min(64, nd - base);
         for (int kk = 0; kk < cnt; kk++) {
-            float t = s + r[0];
+            t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x13C, 0xF, 0xF,
+                                                                      false)) + r[0];
 #pragma unroll
             for (int i = 1; i < 17; i++) t += r[i];
-            s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), kk));
         }
     }
+    const float s = nd ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), (nd - 1) & 63)) : 0.f;
     // 7. the clean tail after the last dirty segment
     const double p_end = hy_readlane_d(pin, 63);
     double before_last = 0.0;
@@ -505,22 +508,28 @@ __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW
         for (int i = 0; i < 8; i++) S.rows[r][1 + i] = v[i];
     }
     __syncthreads();
-    // 5. wavefront 0 walks the dirty rows, then adds the clean tail
+    // 5. wavefront 0 walks the dirty rows, then adds the clean tail. Lane k holds row k of a
+    //    batch of 64; step k adds row k to the running sum rotated in from lane k - 1 (DPP
+    //    wave_ror:1, folded into the first add; lane 0 takes lane 63's, the previous batch's
+    //    end), so the walk is one chain of fp32 adds with no cross-lane round trips.
     if (wave == 0) {
-        float s = 0.f;
-        for (int base = 0; base < nd; base += 64) {
+        const int ndu = __builtin_amdgcn_readfirstlane(nd);
+        float t = 0.f;
+        for (int base = 0; base < ndu; base += 64) {
             float r[9];
             const int kk0 = min(base + lane, 64 * NW - 1);
 #pragma unroll
             for (int i = 0; i < 9; i++) r[i] = S.rows[kk0][i];
-            const int cnt = min(64, nd - base);
+            const int cnt = min(64, ndu - base);
             for (int kk = 0; kk < cnt; kk++) {
-                float t = s + r[0];
+                t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x13C, 0xF,
+                                                                          0xF, false)) + r[0];
 #pragma unroll
                 for (int i = 1; i < 9; i++) t += r[i];
-                s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), kk));
             }
         }
+        const float s =
+            ndu ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), (ndu - 1) & 63)) : 0.f;
         double ptot = 0.0, plast = 0.0, kw = 0.0;
 #pragma unroll
         for (int w = 0; w < NW; w++) {

@@ -292,13 +292,39 @@ GEMM_SHAPES = [
 def test_gemm_vs_oracle(backend, gt, n, k):
     """Chunks above 16 tokens run panel weights on the int8-MFMA GEMM (k_gemm_panel): every
     token's row equals panel_rows_scalar (src/kernels.c:565-581) bit for bit, for token counts
-    that fill, straddle and undershoot the 64-token tiles."""
+    that fill, straddle and undershoot the 64-token tiles. Each call runs three times: a result
+    that depends on wave timing shows up as a repeat that differs."""
     g = synth.rng(gt * 11 + n + k)
     w = synth.make_weight(g, gt, n, k)
     for nt in (17, 64, 77, 128):
         x = synth.activations(g, nt, k)
         out, xq = run_matvec(backend, w, x)
         assert np.array_equal(bits(out), bits(O.matvec(w, x, xq, nt))), f"nt={nt}"
+        for rep in range(2):
+            again, _ = run_matvec(backend, w, x)
+            assert np.array_equal(bits(again), bits(out)), f"nt={nt} repeat {rep}"
+
+
+def test_gemm_small_grid_repeats(backend):
+    """The smallest GEMM grids (one row tile, one or two token tiles: one wavefront per SIMD,
+    the tightest instruction timing) give the same bits on every one of 40 calls."""
+    g = synth.rng(977)
+    for gt, n, k in ((abi.GT_Q2_0C, 1, 256), (abi.GT_STQ1_0, 16, 512)):
+        w = synth.make_weight(g, gt, n, k)
+        h = backend.upload(w)
+        try:
+            for nt in (20, 64):
+                x = synth.activations(g, nt, k)
+                act, xq = q8k_dev(backend, x)
+                want = bits(O.matvec(w, x, xq, nt))
+                out = empty_f32(nt * n)
+                for rep in range(20):
+                    backend.matvec(h, act.data_ptr(), out.data_ptr(), nt)
+                    sync()
+                    got = bits(out.cpu().numpy().reshape(nt, n))
+                    assert np.array_equal(got, want), f"type {gt} n={n} k={k} nt={nt} call {rep}"
+        finally:
+            backend.release(h)
 
 
 def test_gemm_full_gate_up_vs_single_token(backend):
