@@ -412,12 +412,11 @@ __device__ inline float hy_wave_exact_sq_sum(const float* x, int n, int lane) {
 // LDS of hy_block_exact_sum8 for a workgroup of NW wavefronts.
 template <int NW>
 struct HyExactLdsT {
-    float wtot[NW];          // estimate of each wavefront's total
-    double ktot[NW];         // each wavefront's clean contributions
-    uint64_t dmask[NW];      // dirty segments of each wavefront
-    double lpex[64 * NW];    // wavefront-local exclusive prefix of clean contributions per segment
-    float rows[64 * NW][12]; // dirty segments in order: [delta, 8 addends]
-    float result;
+    float wtot[NW];            // estimate of each wavefront's total
+    double ktot[NW];           // each wavefront's clean contributions
+    int dcnt[NW];              // dirty segments of each wavefront
+    double rp[64 * NW];        // dirty rows of wavefront w from 64 w: the wavefront-local exclusive
+    alignas(16) float rv[64 * NW][8];  // prefix of clean contributions, and the 8 addends
 };
 using HyExactLds = HyExactLdsT<4>;
 
@@ -428,7 +427,7 @@ using HyExactLds = HyExactLdsT<4>;
 // carried across wavefronts through LDS. The proof there holds unchanged up to n = 4096: the
 // float estimates and the sequential sum stay within 2^-12 of the exact prefix sums, inside
 // the 2^-9 classification margin. Every thread of the workgroup must call it; all receive the
-// sum.
+// sum. It ends without a barrier: S must not be written again before the next workgroup barrier.
 template <int NW, bool SQ>
 __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW>& S, int wave, int lane) {
     static_assert(NW >= 1 && NW <= 8, "up to 8 wavefronts (n <= 4096)");
@@ -465,83 +464,84 @@ __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW
     }
     const bool zero = g == 0.f;
     const bool clean = zero || (ok && !tie);
-    // 3. exact prefix sums of the clean contributions
+    // 3. exact prefix sums of the clean contributions within the wavefront; the dirty segments
+    //    go to this wavefront's rows in LDS with their local prefix (no cross-wavefront lookup)
     const double kd = clean && !zero ? (double)k : 0.0;
     const double pin = hy_wave_incl_scan_d(kd);
-    const double pex = pin - kd;
-    S.lpex[64 * wave + lane] = pex;
-    if (lane == 63) S.ktot[wave] = pin;
+    const double pex = pin - kd;  // exact: the same sums taken apart
     const uint64_t dm = __builtin_amdgcn_ballot_w64(!clean);
-    if (lane == 0) S.dmask[wave] = dm;
+    if (lane == 63) S.ktot[wave] = pin;
+    if (lane == 0) S.dcnt[wave] = __builtin_popcountll(dm);
+    if (!clean) {
+        const int r = 64 * wave + __builtin_popcountll(dm & ((1ull << lane) - 1));
+        S.rp[r] = pex;
+        float4* dst = reinterpret_cast<float4*>(S.rv[r]);
+        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
     __syncthreads();
-    double koff = 0.0;
-    int rank = 0, nd = 0;
+    // 4. every wavefront: the wavefronts' offsets (one batch of LDS reads), then the dirty rows in
+    //    order, global row k on lane k of a batch of 64 with its global prefix P_k. Row k adds
+    //    delta_k = P_k - P_{k-1}, the clean contribution since the previous dirty segment: between
+    //    two dirty segments every non-zero clean segment lies in one binade [M, 2M) (two clean
+    //    neighbours in different binades would need a gap between their margins), so delta_k is a
+    //    multiple of that binade's ulp below M, exact as a float, and s + delta_k is exact. Then
+    //    its addends one fp32 add at a time. The walk is one chain: step k adds row k to the
+    //    running sum rotated in from lane k - 1 (DPP wave_ror:1, folded into the first add; lane 0
+    //    takes lane 63's, the previous batch's end). Every wavefront walks, so all hold the sum.
+    double koff[NW];
+    int roff[NW];
+    double ptot = 0.0;
+    int nd = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-        const int c = __builtin_popcountll(S.dmask[w]);
-        if (w < wave) {
-            koff += S.ktot[w];
-            rank += c;
-        }
-        nd += c;
+        koff[w] = ptot;
+        roff[w] = nd;
+        ptot += S.ktot[w];
+        nd += S.dcnt[w];
     }
-    // 4. dirty segments: the clean contribution since the previous dirty one, then a row of LDS
-    if (!clean) {
-        const uint64_t below = dm & ((1ull << lane) - 1);
-        double prev = 0.0;
-        if (below) {
-            prev = S.lpex[64 * wave + (63 - __builtin_clzll(below))] + koff;
-        } else {
-            double kw = koff;
-            for (int w = wave - 1; w >= 0; w--) {
-                kw -= S.ktot[w];  // exact: the same sums taken apart
-                const uint64_t m = S.dmask[w];
-                if (m) {
-                    prev = S.lpex[64 * w + (63 - __builtin_clzll(m))] + kw;
-                    break;
-                }
-            }
-        }
-        const int r = rank + __builtin_popcountll(below);
-        S.rows[r][0] = (float)((pex + koff) - prev);
+    nd = __builtin_amdgcn_readfirstlane(nd);
+    float t = 0.f;
+    double pprev = 0.0, plast = 0.0;  // P of the row before this batch; P of the last row
+    for (int base = 0; base < nd; base += 64) {
+        const int gk = min(base + lane, nd - 1);
+        int w = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) S.rows[r][1 + i] = v[i];
+        for (int q = 1; q < NW; q++)
+            if (gk >= roff[q]) w = q;
+        double kw = koff[0];
+#pragma unroll
+        for (int q = 1; q < NW; q++)
+            if (w == q) kw = koff[q];
+        const int r = 64 * w + (gk - roff[w]);
+        const double P = S.rp[r] + kw;
+        const float4 a0 = reinterpret_cast<const float4*>(S.rv[r])[0];
+        const float4 a1 = reinterpret_cast<const float4*>(S.rv[r])[1];
+        // P_{k-1}: lane k - 1's (wave_shr:1; lane 0 gets the previous batch's last)
+        const uint64_t pu = __builtin_bit_cast(uint64_t, P);
+        const uint32_t plo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)pu, 0x138, 0xF, 0xF, true);
+        const uint32_t phi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(pu >> 32), 0x138, 0xF, 0xF, true);
+        const double pm = lane ? __builtin_bit_cast(double, ((uint64_t)phi << 32) | plo) : pprev;
+        const float delta = (float)(P - pm);
+        const int cnt = min(64, nd - base);
+        for (int kk = 0; kk < cnt; kk++) {
+            t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x13C, 0xF,
+                                                                      0xF, false)) + delta;
+            t += a0.x;
+            t += a0.y;
+            t += a0.z;
+            t += a0.w;
+            t += a1.x;
+            t += a1.y;
+            t += a1.z;
+            t += a1.w;
+        }
+        pprev = hy_readlane_d(P, 63);
+        plast = hy_readlane_d(P, cnt - 1);
     }
-    __syncthreads();
-    // 5. wavefront 0 walks the dirty rows, then adds the clean tail. Lane k holds row k of a
-    //    batch of 64; step k adds row k to the running sum rotated in from lane k - 1 (DPP
-    //    wave_ror:1, folded into the first add; lane 0 takes lane 63's, the previous batch's
-    //    end), so the walk is one chain of fp32 adds with no cross-lane round trips.
-    if (wave == 0) {
-        const int ndu = __builtin_amdgcn_readfirstlane(nd);
-        float t = 0.f;
-        for (int base = 0; base < ndu; base += 64) {
-            float r[9];
-            const int kk0 = min(base + lane, 64 * NW - 1);
-#pragma unroll
-            for (int i = 0; i < 9; i++) r[i] = S.rows[kk0][i];
-            const int cnt = min(64, ndu - base);
-            for (int kk = 0; kk < cnt; kk++) {
-                t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x13C, 0xF,
-                                                                          0xF, false)) + r[0];
-#pragma unroll
-                for (int i = 1; i < 9; i++) t += r[i];
-            }
-        }
-        const float s =
-            ndu ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), (ndu - 1) & 63)) : 0.f;
-        double ptot = 0.0, plast = 0.0, kw = 0.0;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const uint64_t m = S.dmask[w];
-            if (m) plast = S.lpex[64 * w + (63 - __builtin_clzll(m))] + kw;
-            kw += S.ktot[w];
-        }
-        ptot = kw;
-        if (lane == 0) S.result = s + (float)(ptot - plast);
-    }
-    __syncthreads();
-    return S.result;
+    const float s = nd ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), (nd - 1) & 63)) : 0.f;
+    // 5. the clean tail after the last dirty segment (one binade, as above)
+    return s + (float)(ptot - plast);
 }
 
 // The RMSNorm form: the sequential sum of squares of 512 * NW values.
