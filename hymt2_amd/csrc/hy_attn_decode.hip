@@ -24,6 +24,7 @@ constexpr int kA1Tile = 96;            // positions per product tile
 constexpr int kA1Prod = kA1Threads - 128;  // producer threads (wavefronts 2-7)
 constexpr int kA1Chunk = 32;           // positions per chain step (8 LDS reads of 4 products)
 constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
+constexpr int kA1PairRow = kA1Threads / 2;  // rows up to this length: two lanes per key
 
 __device__ __forceinline__ void bf16x8f(const uint4& v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -101,6 +102,32 @@ __device__ __forceinline__ float a1_score(const uint4 (&k)[HD / 8], const float*
         a3 += qb.w * kf[7];
     }
     return ((a0 + a1) + (a2 + a3)) * scale;
+}
+
+// The same score with the key split over a pair of adjacent lanes: lane parity 0 forms the
+// partial sums a0, a1 (elements 4k, 4k + 1), parity 1 forms a2, a3, each in dot_bf16's order;
+// the pair swaps its halves and both lanes form ((a0 + a1) + (a2 + a3)) * scale, with the
+// operands in the same positions, so both hold the same bits.
+template <int HD>
+__device__ __forceinline__ float a1_score_pair(const uint4 (&k)[HD / 8], const float* qn, int par, float scale) {
+    int qo = 0;
+    asm volatile("" : "+v"(qo));
+    qn += qo + 2 * par;
+    float x0 = 0.f, x1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) {
+        const uint32_t wa = par ? k[i].y : k[i].x;  // elements 8i + 2 par, + 1
+        const uint32_t wb = par ? k[i].w : k[i].z;  // elements 8i + 4 + 2 par, + 1
+        const float2 qa = *reinterpret_cast<const float2*>(qn + 8 * i);
+        const float2 qb = *reinterpret_cast<const float2*>(qn + 8 * i + 4);
+        x0 += qa.x * hy_bitsf(wa << 16);
+        x1 += qa.y * hy_bitsf(wa & 0xffff0000u);
+        x0 += qb.x * hy_bitsf(wb << 16);
+        x1 += qb.y * hy_bitsf(wb & 0xffff0000u);
+    }
+    const float own = x0 + x1;
+    const float other = __builtin_bit_cast(float, hy_dpp<HY_DPP_QSWAP1>(__builtin_bit_cast(int, own)));
+    return (par ? other + own : own + other) * scale;
 }
 
 template <int HD>
@@ -297,8 +324,18 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     const float scale = 1.0f / sqrtf((float)HD);
     float sv[PASSES];
     float lmax = -__builtin_inff();
+    const bool pair = n <= kA1PairRow;  // short rows: key tid / 2 on a pair of lanes (loaded at entry)
+    if (pair) {
+        const int m = tid >> 1;
+        if (m < n) {
+            if (m == pos) a1_load_key<HD>(kA, kb, 0);
+            sv[0] = a1_score_pair<HD>(kA, qn, tid & 1, scale);
+            lmax = sv[0];
+        }
+    }
 #pragma unroll
     for (int p = 0; p < PASSES; p += 2) {
+        if (pair) break;
         const int j0 = p * kA1Threads + tid, j1 = j0 + kA1Threads;
         if (j0 - tid >= n) break;
         if (j1 - tid < n) a1_load_key<HD>(kB, K, min(j1, cap));
@@ -336,6 +373,10 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
 #pragma unroll
         for (int p = 0; p < PASSES; p++) {
             const int j = p * kA1Threads + tid;
+            if (pair) {
+                if ((tid & 1) == 0 && (tid >> 1) < n) ex[tid >> 1] = hy_expf(sv[0] - mx);
+                break;
+            }
             if (j - tid >= n) break;
             if (j < n) ex[j] = hy_expf(sv[p] - mx);
         }
@@ -430,7 +471,11 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     }
     a1_fence();  // the row loads go out first: loads return in issue order
     uint4 kA[HD / 8];
-    if (tid < pos) a1_load_key<HD>(kA, K, tid);
+    if (pos < kA1PairRow) {  // the score phase's pair form: key tid / 2
+        if ((tid >> 1) < pos) a1_load_key<HD>(kA, K, tid >> 1);
+    } else if (tid < pos) {
+        a1_load_key<HD>(kA, K, tid);
+    }
     uint2 v0[A1Split<HD>::IPT];
     a1_load_v<HD>(v0, V, 0, pp, max(pos - 1, 0));
     a1_fence();
