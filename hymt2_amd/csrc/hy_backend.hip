@@ -658,9 +658,11 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             at.rope_half = f->rope_half;
             at.ctx = f->ctx;
             at.eps = f->eps;
+            const bool fused_q = attention_quantizes(at);
+            if (fused_q) at.act_out = f->act_q;
             HIPCHK(c, launch_rope_norm_store(at, c->s));
             HIPCHK(c, launch_attention(at, c->s));
-            HIPCHK(c, launch_quantize_q8k(f->ao, Q, f->act_q, Q, nt, c->s));
+            if (!fused_q) HIPCHK(c, launch_quantize_q8k(f->ao, Q, f->act_q, Q, nt, c->s));
         }
         JobSpec o{wo, f->d_h, H, EPI_ADD};
         MvOpts o2;

@@ -125,8 +125,12 @@ struct AttnArgs {
     const int* pos_dev;    // optional: pos0 read from device memory (graph replay)
     int pos0, nt, heads, kv_heads, hdim, rope_half, ctx;
     float eps;
+    HyQ8K* act_out;        // optional [nt][qdim / 256]: Q8_K blocks of ao, where attention_quantizes()
 };
 hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s);
+// True when launch_attention also writes a.act_out (the chunk kernel's head group covers whole
+// Q8_K blocks); otherwise the caller quantizes ao itself.
+bool attention_quantizes(const AttnArgs& a);
 
 struct AttnDecodeArgs {
     const float* q;        // [qdim] fp32 (before RoPE)

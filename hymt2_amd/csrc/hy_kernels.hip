@@ -778,6 +778,25 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
         }
     }
     if (oh < GRP) a.ao[(size_t)t * qdim + (size_t)(g * GRP + oh) * HD + od] = o;
+    // the group's GRP * HD outputs are whole Q8_K blocks of the row: quantize them here
+    // (quantize_q8k, src/kernels.c:128-165) for the o-projection
+    if constexpr (GRP * HD % HY_QK == 0) {
+        if (a.act_out) {
+            constexpr int NB = GRP * HD / HY_QK;
+            static_assert(NB <= NW, "one wavefront per block");
+            __syncthreads();  // every chain has read its last V tile
+            if (oh < GRP) vt[oh * HD + od] = o;
+            __syncthreads();
+            if (wave < NB) q8k_quantize_wave(vt + wave * HY_QK, a.act_out + (size_t)t * (qdim / HY_QK) + g * NB + wave, lane);
+        }
+    }
+}
+
+bool attention_quantizes(const AttnArgs& a) {
+    if (a.ctx > kAcMaxCtx || a.heads % a.kv_heads) return false;
+    const int grp = a.heads / a.kv_heads;
+    if (!((a.hdim == 128 || a.hdim == 64) && (grp == 4 || grp == 2))) return false;
+    return grp * a.hdim % HY_QK == 0;
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
