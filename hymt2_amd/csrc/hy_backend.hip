@@ -182,16 +182,15 @@ static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
         q6k_to_planes(w->data, nblk, host.data(), host.data() + nblk * 128,
                       reinterpret_cast<int8_t*>(host.data() + nblk * 192),
                       reinterpret_cast<uint16_t*>(host.data() + nblk * 208));
-    } else if (w->type == GT_F16 && w->k % 32 == 0) {
-        m.kind = KIND_F16;
+    } else if ((w->type == GT_F16 && w->k % 32 == 0) || (w->type == GT_F32 && w->k % 16 == 0)) {
+        // row tiles (hy_tile_offset): the LM head reads each group's rows piece by piece
+        m.kind = w->type == GT_F16 ? KIND_F16 : KIND_F32;
         m.nb = w->k / 256;
-        d->bytes = n * w->k * 2;
-        host.assign(w->data, w->data + d->bytes);
-    } else if (w->type == GT_F32 && w->k % 16 == 0) {
-        m.kind = KIND_F32;
-        m.nb = w->k / 256;
-        d->bytes = n * w->k * 4;
-        host.assign(w->data, w->data + d->bytes);
+        const size_t rowb = (size_t)w->k * (w->type == GT_F16 ? 2 : 4);
+        d->bytes = hy_tile_bytes(n, rowb);
+        host.assign(d->bytes, 0);
+        for (size_t r = 0; r < n; r++)
+            for (size_t b = 0; b < rowb; b += 64) memcpy(host.data() + hy_tile_offset(r, b, rowb), w->data + r * rowb + b, 64);
     } else {
         set_err(c, "upload: unsupported weight type %d (k=%d, panel=%d)", w->type, w->k, w->pk != nullptr);
         delete d;

@@ -17,7 +17,9 @@ enum Pro : int { PRO_NONE = 0, PRO_NORM = 1, PRO_QUANT = 2 };
 //   Q4K:   w = reference blocks [n][nb][144 B]
 //   Q6K:   planes, all indexed by block id n*nb+b: w = ql [..][128], w2 = qh [..][64],
 //          sc = int8 scales [..][16], dh = f16 d [..] (same 210 bytes per block, aligned)
-//   F16/F32: w = rows [n][k]
+//   F16/F32: w = row tiles (hy_tile_offset): rows in groups of kRowTile, each group stored as
+//          its rows' 64-byte pieces, piece by piece, so that the LM head, which walks all rows
+//          of a group one piece at a time, streams contiguous memory
 struct MvWeight {
     int kind, n, k, nb;
     int pshift, poff;
@@ -27,6 +29,17 @@ struct MvWeight {
     const uint16_t* dh;
     const float* ps;
 };
+
+// Row-tiled layout of F16/F32 weights: byte b of row r sits at
+//   ((r / kRowTile * (rowbytes / 64) + b / 64) * kRowTile + r % kRowTile) * 64 + b % 64,
+// the last group padded with zero rows to kRowTile rows (rowbytes a multiple of 64).
+constexpr int kRowTile = 256;
+__host__ __device__ inline size_t hy_tile_offset(size_t r, size_t b, size_t rowbytes) {
+    return ((r / kRowTile * (rowbytes / 64) + b / 64) * kRowTile + r % kRowTile) * 64 + b % 64;
+}
+__host__ __device__ inline size_t hy_tile_bytes(size_t n, size_t rowbytes) {
+    return (n + kRowTile - 1) / kRowTile * kRowTile * rowbytes;
+}
 
 struct MvJob {
     MvWeight W;
@@ -177,7 +190,7 @@ struct Attn1Args {
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s);
 
 struct HeadArgs {
-    MvWeight W;            // F16 or F32 rows
+    MvWeight W;            // F16 or F32 row tiles
     const float* h;        // last token's hidden state [K]
     const float* norm_w;   // output norm
     float eps;
@@ -192,7 +205,7 @@ struct FinishArgs {
     int* ids;              // token ids [n_total]
     int* step;             // device step counter (position of the token just processed)
     int n_prompt;
-    const uint16_t* embd;  // F16 embedding rows [vocab][H]
+    const uint16_t* embd;  // F16 embedding rows [vocab][H], row-tiled (hy_tile_offset)
     const float* embd32;   // or F32 rows
     float* h;              // next step's input [H]
     int H;

@@ -1043,10 +1043,11 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long v) {
 }
 
 // One lane per vocabulary row: logits[r] = sum_j f16(W[r][j]) * xn[j] accumulated sequentially
-// (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). Rows stream
-// through LDS 64 bytes per row per stage, two stages in flight ahead of the one being summed,
-// so each lane reads its own row without uncoalesced global loads. Optionally folds the greedy
-// argmax (first index on ties, src/model.c:945-948) into a 64-bit atomicMax key.
+// (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). A workgroup owns
+// one row tile (kRowTile rows); stage st is piece st (64 bytes) of each of its rows, contiguous
+// in the row-tiled layout, staged through LDS with three stages in flight ahead of the one being
+// summed. Optionally folds the greedy argmax (first index on ties, src/model.c:945-948) into a
+// 64-bit atomicMax key.
 template <bool F16>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
@@ -1054,24 +1055,26 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     __shared__ float scale_slot;
     const int tid = threadIdx.x;
     const int K = a.W.k, n = a.W.n;
-    const int r0 = blockIdx.x * 256;
+    static_assert(kRowTile == 256, "one row per thread");
+    const int r0 = blockIdx.x * kRowTile;
     const int rowb = F16 ? 2 * K : 4 * K;
     const int nstage = rowb / 64;
-    // this thread's 4 x 16 bytes of every stage: rows (tid + 256 i) / 4, 16-byte part tid % 4
+    // this thread's 4 x 16 bytes of every stage: rows (tid + 256 i) / 4, 16-byte part tid % 4,
+    // i.e. bytes 16 (tid + 256 i) of the stage's contiguous kRowTile x 64 bytes
     const uint8_t* src[4];
     int dst[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int f = tid + 256 * i;
         const int rr = f >> 2, part = f & 3;
-        src[i] = a.W.w + (size_t)min(r0 + rr, n - 1) * rowb + part * 16;
+        src[i] = a.W.w + hy_tile_offset((size_t)r0 + rr, (size_t)part * 16, rowb);
         dst[i] = rr * 20 + part * 4;
     }
     // four register sets in rotation, stage st in set st % 4 (no register copies, so the loads
     // of the next three stages stay in flight); loads past the last stage repeat it, unused
     v4u s0[4], s1[4], s2[4], s3[4];
     auto ld = [&](v4u (&p)[4], int st) __attribute__((always_inline)) {
-        const size_t c = (size_t)min(st, nstage - 1) * 64;
+        const size_t c = (size_t)min(st, nstage - 1) * (kRowTile * 64);
 #pragma unroll
         for (int i = 0; i < 4; i++) p[i] = *reinterpret_cast<const v4u*>(src[i] + c);
     };
@@ -1159,9 +1162,13 @@ hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
 
 // =========================================================================== step finish
 
+// Row tok of a row-tiled F16 or F32 embedding (hy_tile_offset) into h.
 __device__ void embed_row(const uint16_t* e16, const float* e32, int tok, float* h, int H) {
-    for (int i = threadIdx.x; i < H; i += blockDim.x)
-        h[i] = e16 ? hy_f16(e16[(size_t)tok * H + i]) : e32[(size_t)tok * H + i];
+    if (e16) {
+        for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = hy_f16(e16[hy_tile_offset(tok, 2 * (size_t)i, 2 * (size_t)H) / 2]);
+    } else {
+        for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = e32[hy_tile_offset(tok, 4 * (size_t)i, 4 * (size_t)H) / 4];
+    }
 }
 
 // Greedy step tail: token = argmax key; the next input is the next prompt id while the prompt
