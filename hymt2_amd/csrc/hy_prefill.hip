@@ -55,13 +55,16 @@ __device__ __forceinline__ v4i as_v4i(const uint4& u) {
 // (4 L), dst uniform (an LDS byte address). Written as assembly so that the compiler does not
 // order the workgroup's LDS reads behind them: the kernel waits for them itself (wait_vm), for
 // the block it is about to read, and the LDS they fill is not read before that wait.
+// An LDS-DMA load that reads M0 right after a scalar write of M0 needs one wait state on this
+// family (the compiler's hazard pass does not look inside the assembly): the s_nop provides it;
+// without it the load may take the previous M0 and fill another piece's slot.
 __device__ __forceinline__ void dma16(const void* src, uint32_t dst) {
     const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)dst);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* src, uint32_t dst) {
     const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)dst);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
