@@ -19,9 +19,10 @@
 // Work layout: 256-thread workgroups of 4 wavefronts in a WR x WT grid; a wavefront owns MT
 // row tiles x NT token tiles of 16 x 16. In gate/up pair mode MT = 2 and the two row tiles of a
 // wavefront are the gate and up rows of the same 16 outputs, so the SwiGLU epilogue
-// (src/model.c:873-876) has both values in one register. The per-row block scales of the
-// workgroup's rows are staged in LDS once; everything else streams from L2 through registers,
-// the next block's fragments loaded while the current block's MFMAs run.
+// (src/model.c:873-876) has both values in one register. Each K-block's operands (activation
+// pieces, panel bytes, token scales and sums, row block scales) land in a stage of an LDS ring
+// by direct global -> LDS loads, the next blocks' in flight while the current block's MFMAs
+// run.
 #include "hy_kernels.h"
 
 namespace hy {
@@ -350,15 +351,14 @@ hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s) {
     }
     if (L.pair && L.job[0].W.n != L.job[1].W.n) return hipErrorNotSupported;
     L.nb = K / 256;
-    // the largest tile that still gives a workgroup per CU; else the smallest
+    // tiles and ring depths as measured fastest in chunked prefill (128 tokens): gate/up pairs in
+    // 32-token tiles with two ring stages, the other contractions in the largest tile that still
+    // gives a workgroup per CU (else the smallest) with three
     int rows = 0;
     for (int q = 0; q < L.njobs; q++)
         if (!L.pair || q == 0) rows += L.job[q].W.n;
     auto wgs = [&](int rt, int tt) { return ((rows + rt - 1) / rt) * ((L.nt + tt - 1) / tt); };
-    if (L.pair) {
-        if (wgs(32, 64) >= 256) return gemm_go<2, 2, 2, 2, true, 3>(L, s);
-        return gemm_go<2, 1, 2, 2, true, 3>(L, s);
-    }
+    if (L.pair) return gemm_go<2, 1, 2, 2, true, 2>(L, s);
     if (wgs(64, 64) >= 256) return gemm_go<2, 2, 2, 2, false, 3>(L, s);
     return gemm_go<1, 1, 2, 2, false, 3>(L, s);
 }
