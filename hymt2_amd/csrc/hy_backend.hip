@@ -190,7 +190,7 @@ static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
         d->bytes = hy_tile_bytes(n, rowb);
         host.assign(d->bytes, 0);
         for (size_t r = 0; r < n; r++)
-            for (size_t b = 0; b < rowb; b += 64) memcpy(host.data() + hy_tile_offset(r, b, rowb), w->data + r * rowb + b, 64);
+            for (size_t b = 0; b < rowb; b += 16) memcpy(host.data() + hy_tile_offset(r, b, rowb), w->data + r * rowb + b, 16);
     } else {
         set_err(c, "upload: unsupported weight type %d (k=%d, panel=%d)", w->type, w->k, w->pk != nullptr);
         delete d;

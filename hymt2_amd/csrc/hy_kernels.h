@@ -18,8 +18,8 @@ enum Pro : int { PRO_NONE = 0, PRO_NORM = 1, PRO_QUANT = 2 };
 //   Q6K:   planes, all indexed by block id n*nb+b: w = ql [..][128], w2 = qh [..][64],
 //          sc = int8 scales [..][16], dh = f16 d [..] (same 210 bytes per block, aligned)
 //   F16/F32: w = row tiles (hy_tile_offset): rows in groups of kRowTile, each group stored as
-//          its rows' 64-byte pieces, piece by piece, so that the LM head, which walks all rows
-//          of a group one piece at a time, streams contiguous memory
+//          its rows' 16-byte pieces, piece by piece, so that the LM head (one thread per row,
+//          all rows of a group stepping through their pieces together) reads contiguous memory
 struct MvWeight {
     int kind, n, k, nb;
     int pshift, poff;
@@ -31,11 +31,11 @@ struct MvWeight {
 };
 
 // Row-tiled layout of F16/F32 weights: byte b of row r sits at
-//   ((r / kRowTile * (rowbytes / 64) + b / 64) * kRowTile + r % kRowTile) * 64 + b % 64,
+//   ((r / kRowTile * (rowbytes / 16) + b / 16) * kRowTile + r % kRowTile) * 16 + b % 16,
 // the last group padded with zero rows to kRowTile rows (rowbytes a multiple of 64).
 constexpr int kRowTile = 256;
 __host__ __device__ inline size_t hy_tile_offset(size_t r, size_t b, size_t rowbytes) {
-    return ((r / kRowTile * (rowbytes / 64) + b / 64) * kRowTile + r % kRowTile) * 64 + b % 64;
+    return ((r / kRowTile * (rowbytes / 16) + b / 16) * kRowTile + r % kRowTile) * 16 + b % 16;
 }
 __host__ __device__ inline size_t hy_tile_bytes(size_t n, size_t rowbytes) {
     return (n + kRowTile - 1) / kRowTile * kRowTile * rowbytes;

@@ -1044,54 +1044,39 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long v) {
 
 // One lane per vocabulary row: logits[r] = sum_j f16(W[r][j]) * xn[j] accumulated sequentially
 // (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). A workgroup owns
-// one row tile (kRowTile rows); stage st is piece st (64 bytes) of each of its rows, contiguous
-// in the row-tiled layout, staged through LDS with three stages in flight ahead of the one being
-// summed. Optionally folds the greedy argmax (first index on ties, src/model.c:945-948) into a
-// 64-bit atomicMax key.
+// one row tile (kRowTile rows, one per thread). In the row-tiled layout piece q (16 bytes) of
+// the tile's rows is one contiguous 4 KB run, so every thread reads its own row straight into
+// registers with coalesced loads: a stage is 64 bytes of the row (four pieces), and four
+// register sets rotate, three stages in flight while one is summed. No LDS staging and no
+// barriers past the norm. Optionally folds the greedy argmax (first index on ties,
+// src/model.c:945-948) into a 64-bit atomicMax key.
 template <bool F16>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
-    __shared__ __align__(16) uint32_t tile[2][256 * 20];
     __shared__ float scale_slot;
+    static_assert(kRowTile == 256, "one row per thread");
     const int tid = threadIdx.x;
     const int K = a.W.k, n = a.W.n;
-    static_assert(kRowTile == 256, "one row per thread");
     const int r0 = blockIdx.x * kRowTile;
     const int rowb = F16 ? 2 * K : 4 * K;
     const int nstage = rowb / 64;
-    // this thread's 4 x 16 bytes of every stage: rows (tid + 256 i) / 4, 16-byte part tid % 4,
-    // i.e. bytes 16 (tid + 256 i) of the stage's contiguous kRowTile x 64 bytes
-    const uint8_t* src[4];
-    int dst[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int f = tid + 256 * i;
-        const int rr = f >> 2, part = f & 3;
-        src[i] = a.W.w + hy_tile_offset((size_t)r0 + rr, (size_t)part * 16, rowb);
-        dst[i] = rr * 20 + part * 4;
-    }
-    // four register sets in rotation, stage st in set st % 4 (no register copies, so the loads
-    // of the next three stages stay in flight); loads past the last stage repeat it, unused
+    // piece q of this thread's row
+    const uint8_t* src = a.W.w + (size_t)blockIdx.x * kRowTile * rowb + (size_t)tid * 16;
     v4u s0[4], s1[4], s2[4], s3[4];
+    // stage st = pieces 4 st .. 4 st + 3; stages past the last repeat it, unused
     auto ld = [&](v4u (&p)[4], int st) __attribute__((always_inline)) {
-        const size_t c = (size_t)min(st, nstage - 1) * (kRowTile * 64);
+        const size_t c = (size_t)min(st, nstage - 1) * 4 * (kRowTile * 16);
 #pragma unroll
-        for (int i = 0; i < 4; i++) p[i] = *reinterpret_cast<const v4u*>(src[i] + c);
-    };
-    auto stv = [&](const v4u (&p)[4], int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) *reinterpret_cast<v4u*>(&tile[buf][dst[i]]) = p[i];
+        for (int i = 0; i < 4; i++) p[i] = *reinterpret_cast<const v4u*>(src + c + (size_t)i * (kRowTile * 16));
     };
     float acc = 0.f;
-    auto comp = [&](int st, int buf) __attribute__((always_inline)) {
+    auto comp = [&](const v4u (&p)[4], int st) __attribute__((always_inline)) {
         if (st >= nstage) return;
-        const uint32_t* tr = &tile[buf][tid * 20];
         if (F16) {
             const float* xk = xs + st * 32;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const uint4 v = *reinterpret_cast<const uint4*>(tr + 4 * q);
-                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+                const uint32_t w[4] = {p[q].x, p[q].y, p[q].z, p[q].w};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     acc += hy_f16((uint16_t)(w[e] & 0xffffu)) * xk[8 * q + 2 * e];
@@ -1102,11 +1087,10 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
             const float* xk = xs + st * 16;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const uint4 v = *reinterpret_cast<const uint4*>(tr + 4 * q);
-                acc += hy_bitsf(v.x) * xk[4 * q + 0];
-                acc += hy_bitsf(v.y) * xk[4 * q + 1];
-                acc += hy_bitsf(v.z) * xk[4 * q + 2];
-                acc += hy_bitsf(v.w) * xk[4 * q + 3];
+                acc += hy_bitsf(p[q].x) * xk[4 * q + 0];
+                acc += hy_bitsf(p[q].y) * xk[4 * q + 1];
+                acc += hy_bitsf(p[q].z) * xk[4 * q + 2];
+                acc += hy_bitsf(p[q].w) * xk[4 * q + 3];
             }
         }
     };
@@ -1116,25 +1100,15 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     ld(s2, 2);
     ld(s3, 3);
     rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);  // while the weights stream
-    stv(s0, 0);
-    __syncthreads();
     for (int st = 0; st < nstage; st += 4) {
-        comp(st, 0);
-        stv(s1, 1);
+        comp(s0, st);
         ld(s0, st + 4);
-        __syncthreads();
-        comp(st + 1, 1);
-        stv(s2, 0);
+        comp(s1, st + 1);
         ld(s1, st + 5);
-        __syncthreads();
-        comp(st + 2, 0);
-        stv(s3, 1);
+        comp(s2, st + 2);
         ld(s2, st + 6);
-        __syncthreads();
-        comp(st + 3, 1);
-        stv(s0, 0);
+        comp(s3, st + 3);
         ld(s3, st + 7);
-        __syncthreads();
     }
     const int r = r0 + tid;
     if (r < n) a.logits[r] = acc;
