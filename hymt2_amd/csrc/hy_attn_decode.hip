@@ -25,6 +25,7 @@ constexpr int kA1Prod = kA1Threads - 128;  // producer threads (wavefronts 2-7)
 constexpr int kA1Chunk = 32;           // positions per chain step (8 LDS reads of 4 products)
 constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
 constexpr int kA1PairRow = kA1Threads / 2;  // rows up to this length: two lanes per key
+constexpr int kA1ShortRow = 2 * kA1Tile;    // rows up to this length: V staged whole, direct chains
 
 __device__ __forceinline__ void bf16x8f(const uint4& v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -230,6 +231,76 @@ __device__ __forceinline__ void a1_products(const uint2 (&v)[A1Split<HD>::IPT], 
     }
 }
 
+// Short rows: V of the tile at t0 as fp32 into stage[j][d] for producer thread p's quads (rows
+// below n; position `pos` from this token's V row in LDS, vb).
+template <int HD>
+__device__ __forceinline__ void a1_stage_v(const uint2 (&v)[A1Split<HD>::IPT], float* stage, const uint16_t* vb,
+                                           int t0, int p, int pos, int n) {
+    using P = A1Split<HD>;
+    const int r0 = t0 + p / P::QPR, q = p % P::QPR;
+    const uint2 b = *reinterpret_cast<const uint2*>(vb + 4 * q);
+#pragma unroll
+    for (int k = 0; k < P::IPT; k++) {
+        const int r = r0 + P::RSTEP * k;
+        if (r < n) {
+            const uint2 w = r == pos ? b : v[k];
+            *reinterpret_cast<float4*>(stage + r * HD + 4 * q) =
+                make_float4(hy_bitsf(w.x << 16), hy_bitsf(w.x & 0xffff0000u), hy_bitsf(w.y << 16), hy_bitsf(w.y & 0xffff0000u));
+        }
+    }
+}
+
+// Short rows: o = sum_j p_j * V_j[d] in position order for lane d (col = stage + d, p_j in
+// LDS). Chunks of 16 positions in two register sets: the next chunk's LDS reads are in flight
+// while a chunk is added (a loop over chunk pairs, so that no exit sits between a prefetch and
+// its use for the compiler to sink the prefetch behind); each step is one multiply independent
+// of the chain and one add on it. Reads stay inside the stage (positions < kA1ShortRow).
+template <int HD>
+__device__ __forceinline__ float a1_short_chain(const float* col, const float* pj, int n) {
+    constexpr int C = 16, LIM = kA1ShortRow - C;
+    float ea[C], va[C], eb[C], vb[C];
+    auto ld = [&](float (&e)[C], float (&v)[C], int j0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < C; i += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(pj + j0 + i);
+            e[i] = q.x, e[i + 1] = q.y, e[i + 2] = q.z, e[i + 3] = q.w;
+        }
+#pragma unroll
+        for (int i = 0; i < C; i++) v[i] = col[(j0 + i) * HD];
+    };
+    float o = 0.f;
+    auto add = [&](const float (&e)[C], const float (&v)[C]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < C; i++) o += e[i] * v[i];
+    };
+    // the partial last chunk: positions past the row add +0, which leaves o unchanged (o is
+    // never -0: it starts at +0, and a sum that cancels rounds to +0)
+    auto add_tail = [&](const float (&e)[C], const float (&v)[C], int j0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            const float t = e[i] * v[i];
+            o += j0 + i < n ? t : 0.f;
+        }
+    };
+    const int nfull = n / C;
+    ld(ea, va, 0);
+    int c = 0;
+    for (; c + 2 <= nfull; c += 2) {  // no exit inside the body: the prefetches stay where written
+        ld(eb, vb, (c + 1) * C);
+        add(ea, va);
+        ld(ea, va, min((c + 2) * C, LIM));
+        add(eb, vb);
+    }
+    if (c < nfull) {
+        ld(eb, vb, min((c + 1) * C, LIM));
+        add(ea, va);
+        add_tail(eb, vb, (c + 1) * C);
+    } else {
+        add_tail(ea, va, c * C);
+    }
+    return o;
+}
+
 // One producer step: when the tile at t0 exists (a uniform branch), its products (the edge form
 // when it reaches the row's end) and its barrier; then, on every path, v refilled with the rows
 // three tiles on and e with the next tile's e_j. The loads are unconditional so that every path
@@ -352,11 +423,20 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
             lmax = fmaxf(lmax, sv[p + 1]);
         }
     }
-    // V tiles 1 and 2, unconditionally (rows clamped below the position; every wavefront), so
-    // that on every path the same loads follow tile 0's and the producers' waits leave them out
+    // V tiles 1 and 2 (rows clamped below the position), by the producer wavefronts only: the
+    // chain wavefronts never use them (loads left in flight there would hold registers that the
+    // short rows' chains reuse, and make them wait). Long rows: both, so that the same loads
+    // follow tile 0's on every path and the producers' waits leave them out; short rows: tile 1
+    // when the row reaches it.
     const int last = max(pos - 1, 0);
-    a1_load_v<HD>(v1, V, kA1Tile, pp, last);
-    a1_load_v<HD>(v2, V, 2 * kA1Tile, pp, last);
+    if (prd) {
+        if (n > kA1ShortRow) {
+            a1_load_v<HD>(v1, V, kA1Tile, pp, last);
+            a1_load_v<HD>(v2, V, 2 * kA1Tile, pp, last);
+        } else if (n > kA1Tile) {
+            a1_load_v<HD>(v1, V, kA1Tile, pp, last);
+        }
+    }
     a1_fence();  // issued here, not next to their first use
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
@@ -383,8 +463,15 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
         hy_lds_barrier();
         if (n <= kA1SerialSum) {
             if (wave == 0) {
-                const float sum = hy_wave_seq_sum(ex, n, lane);
+                const float sum = hy_wave_seq_sum(ex, n, lane);  // the same value in every lane
                 if (lane == 0) S.stat = 1.0f / sum;
+                if (n <= kA1ShortRow) {  // short rows: p_j = e_j * (1 / sum) in place, once per position
+                    const float iv = 1.0f / sum;
+                    for (int j = lane; j < n; j += 64) ex[j] = ex[j] * iv;
+                }
+            } else if (n <= kA1ShortRow && prd) {  // meanwhile the producers stage V whole
+                a1_stage_v<HD>(v0, &S.prod[0][0], vb, 0, pp, pos, n);
+                if (n > kA1Tile) a1_stage_v<HD>(v1, &S.prod[0][0], vb, kA1Tile, pp, pos, n);
             }
             hy_lds_barrier();
             inv = S.stat;
@@ -409,6 +496,12 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     //    buffer t % 2, and tile t - 1's buffer has been read. Wavefronts 0 .. HD/64 - 1 add tile t
     //    after barrier t; the producers form tile t before it, with V three tiles ahead, in
     //    groups of three steps (one loop exit; steps past the row only load).
+    // Short rows: every lane of wavefronts 0 .. HD/64 - 1 walks its dimension over the staged V.
+    if (n <= kA1ShortRow) {
+        static_assert(kA1ShortRow <= kA1SerialSum && kA1ShortRow * HD <= 2 * kA1Tile * HD, "staged V fits");
+        if (wave < HD / 64) a.ao[(size_t)h * HD + tid] = a1_short_chain<HD>(&S.prod[0][0] + tid, ex, n);
+        return;
+    }
     const int tiles = (n + kA1Tile - 1) / kA1Tile;
     if (wave < HD / 64) {
         __builtin_amdgcn_s_setprio(3);  // the chain is the critical path: its adds issue first
