@@ -539,25 +539,35 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     const bool prd = wave >= 2;
     const int pp = prd ? tid - 128 : lane;
 
-    // 0. loads: the position (scalar), this token's q / k / v row for wavefronts 0 / 1 / 2
-    //    with the norm weights and the position's RoPE row (rope_cur when the position lives in
-    //    device memory), then the key rows of the first pass (those below the position) and the
-    //    first V tile
+    // 0. loads: this token's q / k / v row for wavefronts 0 / 1 / 2 with the norm weights, the
+    //    position (scalar) and its RoPE row (rope_cur when the position lives in device memory),
+    //    then the key rows of the first pass (those below the position) and the first V tile
     // readfirstlane: the position is one value for the workgroup; loaded through a pointer the
     // compiler could not tell that, and every loop bound and branch derived from it would compile
     // as divergent (exec-masked exits that merge back into the loops)
-    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    // The rows and norm weights first, before the position is read: scalar loads are waited
+    // for all together, so a row load issued after the position's load would wait for it.
     float x[RPL], rc[RPL], rs[RPL], nw[RPL];
     {
         const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
         const float* nsrc = wave == 0 ? a.q_norm : a.k_norm;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int d = lane + 64 * i;
+            x[i] = src[d];
+            nw[i] = nsrc[d];
+        }
+    }
+    // instruction order only (a memory clobber here would turn the position's scalar load into
+    // a vector load whose wait covers the rows)
+    __builtin_amdgcn_sched_barrier(0);
+    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    {
         const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
         const float* sn = a.rope_cur ? a.rope_cur + half : a.rope_sin + (size_t)pos * half;
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
             const int d = lane + 64 * i, t = d < half ? d : (d < 2 * half ? d - half : 0);
-            x[i] = src[d];
-            nw[i] = nsrc[d];
             rc[i] = cs[t];
             rs[i] = sn[t];
         }
