@@ -158,7 +158,9 @@ static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
     m.k = w->k;
     const size_t n = (size_t)w->n;
     std::vector<uint8_t> host;
-    if ((w->type == GT_STQ1_0 || w->type == GT_Q2_0C) && w->pk && w->ps && w->k % 256 == 0) {
+    // row lengths whole blocks of the type: STQ1_0 256 weights a block, Q2_0C 512
+    // (src/model.c:138, src/kernels.c:121); the panel then has k / 256 pieces a row
+    if ((w->type == GT_STQ1_0 || w->type == GT_Q2_0C) && w->pk && w->ps && w->k % (w->type == GT_Q2_0C ? 512 : 256) == 0) {
         m.kind = KIND_PANEL;
         m.nb = w->k / 256;
         m.pshift = w->pshift;

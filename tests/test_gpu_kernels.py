@@ -283,7 +283,8 @@ GEMM_SHAPES = [
     (abi.GT_STQ1_0, 3072, 2048),  # qkv of the 1.8B layer
     (abi.GT_Q2_0C, 2048, 6144),   # config 4: down
     (abi.GT_STQ1_0, 129, 512),    # ragged rows (row tiles of 32 / 64)
-    (abi.GT_Q2_0C, 1, 256),       # one row, one block
+    (abi.GT_STQ1_0, 1, 256),      # one row, one block
+    (abi.GT_Q2_0C, 1, 512),       # one row, one Q2_0C block (two panel pieces)
     (abi.GT_STQ1_0, 100, 1536),
 ]
 
@@ -305,11 +306,21 @@ def test_gemm_vs_oracle(backend, gt, n, k):
             assert np.array_equal(bits(again), bits(out)), f"nt={nt} repeat {rep}"
 
 
+def test_upload_rejects_partial_q2_0c_block(backend):
+    """A Q2_0C row is whole 512-weight blocks (src/model.c:138): K = 256 is refused before
+    any host bytes are read."""
+    w = synth.Weight(abi.GT_Q2_0C, 256, 1, np.zeros((1, 0), dtype=np.uint8))
+    w.pk = np.zeros((1, 1, 64), dtype=np.uint8)
+    w.ps = np.zeros((1, 1), dtype=np.float32)
+    with pytest.raises(RuntimeError):
+        backend.upload(w)
+
+
 def test_gemm_small_grid_repeats(backend):
     """The smallest GEMM grids (one row tile, one or two token tiles: one wavefront per SIMD,
     the tightest instruction timing) give the same bits on every one of 40 calls."""
     g = synth.rng(977)
-    for gt, n, k in ((abi.GT_Q2_0C, 1, 256), (abi.GT_STQ1_0, 16, 512)):
+    for gt, n, k in ((abi.GT_STQ1_0, 1, 256), (abi.GT_Q2_0C, 16, 512)):
         w = synth.make_weight(g, gt, n, k)
         h = backend.upload(w)
         try:
