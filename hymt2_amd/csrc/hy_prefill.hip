@@ -95,9 +95,15 @@ struct GemmStage {
     alignas(16) float ps[64];
 };
 
-template <int MT, int NT, int WR, int WT, bool PAIR, int RING>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
-    static_assert(WR * WT == kGemmThreads / 64, "4 wavefronts per workgroup");
+// KS = 2 splits K inside the workgroup: two sets of 4 wavefronts own the same output tile,
+// set 0 the first NBH blocks, set 1 the last NBH, stepping together through one barrier per
+// block pair. Set 0 keeps the running sum in block order; set 1 keeps its NBH fp32 block terms
+// in registers and, after set 0 hands its sums over through LDS, adds them in block order, so
+// each output is the same sequential sum as with KS = 1.
+template <int MT, int NT, int WR, int WT, bool PAIR, int RING, int KS = 1, int NBH = 0>
+__global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunch L) {
+    static_assert(WR * WT == kGemmThreads / 64, "4 wavefronts per workgroup (per K set)");
+    static_assert(KS == 1 || (KS == 2 && NBH >= 1), "K split in two halves of NBH blocks");
     static_assert(!PAIR || MT == 2, "pair mode: one gate and one up tile per wavefront");
     constexpr int SLOTS = WR * MT * 16;  // row slots of the workgroup
     constexpr int TOK = WT * NT * 16;    // tokens of the workgroup
@@ -107,11 +113,15 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
     constexpr int MAXI = (TOTAL + 3) / 4;
     static_assert(TOK % 4 == 0 && SLOTS % 16 == 0 && TOK <= 64, "tile shape");
     using Stage = GemmStage<SLOTS, TOK>;
-    __shared__ Stage ring[RING];
+    __shared__ Stage ring[RING * KS];
+    __shared__ __align__(16) float xch[KS == 2 ? kGemmThreads * MT * NT * 4 : 4];  // set 0's sums
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
+    const int half = KS == 2 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;  // K set
     const int wr = wave % WR, wt = wave / WR;
     const int nb = L.nb, nt = L.nt;
+    const int nbh = KS == 2 ? NBH : nb;  // blocks of this K set, from block hb0
+    const int hb0 = half * nbh;
     const HyQ8K* const act = L.act;
 
     // job of this row tile (uniform)
@@ -187,19 +197,20 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
         }
     }
     const uint32_t ring0 = lds_addr(&ring[0]);
+    // block hb0 + b of this K set into ring slot buf
     auto issue = [&](int b, int buf) __attribute__((always_inline)) {
-        const uint32_t base = ring0 + buf * (uint32_t)sizeof(Stage);
+        const uint32_t base = ring0 + (buf * KS + half) * (uint32_t)sizeof(Stage);
 #pragma unroll
         for (int i = 0; i < MAXI; i++) {
             const int k = wave + 4 * i;
-            if (k < QN + AN) dma16(src[i] + (size_t)b * stride[i], base + dst[i]);
-            else if (k < TOTAL) dma4(src[i] + (size_t)b * stride[i], base + dst[i]);
+            if (k < QN + AN) dma16(src[i] + (size_t)(hb0 + b) * stride[i], base + dst[i]);
+            else if (k < TOTAL) dma4(src[i] + (size_t)(hb0 + b) * stride[i], base + dst[i]);
         }
     };
 
     // the first RING - 1 blocks (clamped: a block past the end repeats the last, unused)
 #pragma unroll
-    for (int b = 0; b < RING - 1; b++) issue(min(b, nb - 1), b);
+    for (int b = 0; b < RING - 1; b++) issue(min(b, nbh - 1), b);
 
     float accf[MT][NT][4];
 #pragma unroll
@@ -210,7 +221,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
             for (int r = 0; r < 4; r++) accf[mt][n][r] = 0.f;
 
     const int tl = lane & 15, g = lane >> 4;
-    for (int b = 0; b < nb; b++) {
+    // one block step: the fp32 terms of block hb0 + b for this wavefront's outputs
+    auto step = [&](int b, float (&term)[MT][NT][4]) __attribute__((always_inline)) {
         const int buf = b % RING;
         // block b's direct loads are the oldest RING - 1 issues ago: wait for them, then the
         // barrier makes every wavefront's share visible (and ends the reads of block b - 1,
@@ -221,8 +233,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
         else if (wave == 2) wait_vm<(RING - 2) * ((TOTAL + 1) / 4)>();
         else wait_vm<(RING - 2) * (TOTAL / 4)>();
         hy_lds_barrier();
-        issue(min(b + RING - 1, nb - 1), (b + RING - 1) % RING);
-        const Stage& S = ring[buf];
+        issue(min(b + RING - 1, nbh - 1), (b + RING - 1) % RING);
+        const Stage& S = ring[buf * KS + half];
 
         // MFMAs over the block's four K = 64 chunks
         v4i acc[MT][NT];
@@ -270,14 +282,54 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
             for (int n = 0; n < NT; n++) {
                 const int nsub = -(pof[mt] * off[n]);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float term = psr[r] * dn[n] * (float)((acc[mt][n][r] << psh[mt]) + nsub);
-                    accf[mt][n][r] = accf[mt][n][r] + term;
-                }
+                for (int r = 0; r < 4; r++) term[mt][n][r] = psr[r] * dn[n] * (float)((acc[mt][n][r] << psh[mt]) + nsub);
             }
         }
+    };
+    auto accumulate = [&](const float (&term)[MT][NT][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) accf[mt][n][r] = accf[mt][n][r] + term[mt][n][r];
+    };
+    if constexpr (KS == 1) {
+        for (int b = 0; b < nb; b++) {
+            float term[MT][NT][4];
+            step(b, term);
+            accumulate(term);
+        }
+        wait_vm<0>();  // the clamped trailing issues complete before the workgroup ends
+    } else {
+        float tm[NBH][MT][NT][4];
+#pragma unroll
+        for (int b = 0; b < NBH; b++) {
+            step(b, tm[b]);
+            if (half == 0) accumulate(tm[b]);
+        }
+        wait_vm<0>();
+        // set 0 hands its sums over; set 1 adds its terms after them, in block order, and stores
+        float4* xv = reinterpret_cast<float4*>(xch) + (size_t)(wave * 64 + lane) * (MT * NT);
+        if (half == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+                    xv[mt * NT + n] = make_float4(accf[mt][n][0], accf[mt][n][1], accf[mt][n][2], accf[mt][n][3]);
+        }
+        __syncthreads();
+        if (half == 0) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const float4 p = xv[mt * NT + n];
+                accf[mt][n][0] = p.x, accf[mt][n][1] = p.y, accf[mt][n][2] = p.z, accf[mt][n][3] = p.w;
+            }
+#pragma unroll
+        for (int b = 0; b < NBH; b++) accumulate(tm[b]);
     }
-    wait_vm<0>();  // the clamped trailing issues complete before the workgroup ends
 
     // epilogue: lane holds rows 4 g .. 4 g + 3 of each row tile for token tl of each token tile
     float* const out = L.job[j].out;
@@ -324,7 +376,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_panel(GemmLaunch L) {
     }
 }
 
-template <int MT, int NT, int WR, int WT, bool PAIR, int RING>
+template <int MT, int NT, int WR, int WT, bool PAIR, int RING, int KS = 1, int NBH = 0>
 hipError_t gemm_go(GemmLaunch& L, hipStream_t s) {
     const int rows_wg = PAIR ? WR * 16 : WR * MT * 16;
     int tiles = 0;
@@ -335,7 +387,7 @@ hipError_t gemm_go(GemmLaunch& L, hipStream_t s) {
     if (PAIR) L.job[1].tile_begin = 1 << 30;  // never selected by tile index
     const int toks_wg = WT * NT * 16;
     const dim3 grid(tiles, (L.nt + toks_wg - 1) / toks_wg);
-    k_gemm_panel<MT, NT, WR, WT, PAIR, RING><<<grid, kGemmThreads, 0, s>>>(L);
+    k_gemm_panel<MT, NT, WR, WT, PAIR, RING, KS, NBH><<<grid, kGemmThreads * KS, 0, s>>>(L);
     return hipGetLastError();
 }
 
@@ -358,8 +410,11 @@ hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s) {
     for (int q = 0; q < L.njobs; q++)
         if (!L.pair || q == 0) rows += L.job[q].W.n;
     auto wgs = [&](int rt, int tt) { return ((rows + rt - 1) / rt) * ((L.nt + tt - 1) / tt); };
-    if (L.pair) return gemm_go<2, 1, 2, 2, true, 2>(L, s);
+    // K = 2048 and 6144 (8 and 24 blocks): K split in two inside the workgroup
+    if (L.pair) return L.nb == 8 ? gemm_go<2, 1, 2, 2, true, 2, 2, 4>(L, s) : gemm_go<2, 1, 2, 2, true, 2>(L, s);
     if (wgs(64, 64) >= 256) return gemm_go<2, 2, 2, 2, false, 3>(L, s);
+    if (L.nb == 8) return gemm_go<1, 1, 2, 2, false, 3, 2, 4>(L, s);
+    if (L.nb == 24) return gemm_go<1, 1, 2, 2, false, 3, 2, 12>(L, s);
     return gemm_go<1, 1, 2, 2, false, 3>(L, s);
 }
 
