@@ -410,8 +410,9 @@ hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s) {
     for (int q = 0; q < L.njobs; q++)
         if (!L.pair || q == 0) rows += L.job[q].W.n;
     auto wgs = [&](int rt, int tt) { return ((rows + rt - 1) / rt) * ((L.nt + tt - 1) / tt); };
-    // K = 2048 and 6144 (8 and 24 blocks): K split in two inside the workgroup
-    if (L.pair) return L.nb == 8 ? gemm_go<2, 1, 2, 2, true, 2, 2, 4>(L, s) : gemm_go<2, 1, 2, 2, true, 2>(L, s);
+    // K = 2048 and 6144 (8 and 24 blocks) outside pair mode: K split in two inside the
+    // workgroup (measured slower for the gate/up pairs)
+    if (L.pair) return gemm_go<2, 1, 2, 2, true, 2>(L, s);
     if (wgs(64, 64) >= 256) return gemm_go<2, 2, 2, 2, false, 3>(L, s);
     if (L.nb == 8) return gemm_go<1, 1, 2, 2, false, 3, 2, 4>(L, s);
     if (L.nb == 24) return gemm_go<1, 1, 2, 2, false, 3, 2, 12>(L, s);
