@@ -2,7 +2,7 @@
 //
 // Work layout: 256-thread workgroups, one weight row per half-wavefront per iteration, ITERS
 // iterations per wave, so a workgroup covers 8 * ITERS rows (4 * ITERS gate/up pairs) and a
-// launch has a few hundred workgroups. Lane j of a half-wavefront owns the 16-byte weight
+// launch has at most 192 workgroups where K = 2048 allows (256 for K = 6144). Lane j of a half-wavefront owns the 16-byte weight
 // segments j, j + 32, ... of every row it visits; those always meet the same Q8_K activation
 // values, which therefore live in registers, loaded once. Every weight load of the thread is
 // issued before the prologue (RMSNorm + Q8_K, or Q8_K alone), so HBM streams while the
@@ -22,7 +22,7 @@ namespace {
 
 constexpr int kMv1Threads = 256;
 constexpr int kMv1Waves = kMv1Threads / 64;
-constexpr int kMv1MaxWgs = 512;
+constexpr int kMv1MaxWgs = 192;
 
 }  // namespace
 
@@ -196,6 +196,8 @@ static hipError_t mv1_iters(const Mv1Launch& L, int pro, int iters, int grid, hi
         case 2: return mv1_pro<KIND, SPL, 2>(L, pro, grid, s);
         case 3: return mv1_pro<KIND, SPL, 3>(L, pro, grid, s);
         case 4: return mv1_pro<KIND, SPL, 4>(L, pro, grid, s);
+        case 6: return mv1_pro<KIND, SPL, 6>(L, pro, grid, s);
+        case 8: return mv1_pro<KIND, SPL, 8>(L, pro, grid, s);
         default: return hipErrorNotSupported;
         }
     }
@@ -218,10 +220,11 @@ hipError_t launch_mv1(Mv1Launch& L, int pro, hipStream_t s) {
     if (K != 2048 && K != 6144) return hipErrorNotSupported;
     if (pro == PRO_NORM && K != 2048) return hipErrorNotSupported;
     if (pro != PRO_NONE && !L.x) return hipErrorInvalidValue;
-    // smallest ITERS whose grid fits a few workgroups per CU
+    // the smallest ITERS whose grid is at most kMv1MaxWgs workgroups: every workgroup repeats
+    // the prologue (load, RMSNorm, Q8_K), so fewer, longer workgroups measured faster
     int iters = 0, grid = 0;
-    const int max_iters = K == 2048 ? 4 : 1;
-    for (int it = 1; it <= max_iters; it++) {
+    const int max_iters = K == 2048 ? 8 : 1;
+    for (int it = 1; it <= max_iters; it += it < 4 ? 1 : 2) {
         const int per = L.pair ? kMv1Waves * it : kMv1Waves * 2 * it;
         int g = 0;
         for (int j = 0; j < (L.pair ? 1 : L.njobs); j++) {
