@@ -8,8 +8,8 @@
 // e_j * (1 / sum). Output (axpy_bf16, src/kernels.c:1122-1124): o[d] += p_j * V_j[d] in
 // position order, as a pipeline over tiles of 96 positions: wavefronts 2-7 form the products
 // p_j * V_j[d] (each rounded to fp32, as the reference rounds them) of tile t + 1 into one half
-// of a double-buffered [d][j] LDS tile while wavefronts 0-1 (one lane per dimension) add tile t
-// from the other half in position order, four products per LDS read; one LDS-only barrier per
+// of a double-buffered [j][d] LDS tile while wavefronts 0-1 (one lane per dimension) add tile t
+// from the other half in position order, two products per LDS read; one LDS-only barrier per
 // tile, V rows loaded three tiles ahead. The fp32 output row goes to `ao`; the o-projection
 // quantizes it.
 #include "hy_kernels.h"
@@ -22,7 +22,7 @@ constexpr int kA1Threads = 512;
 constexpr int kA1Waves = kA1Threads / 64;
 constexpr int kA1Tile = 96;            // positions per product tile
 constexpr int kA1Prod = kA1Threads - 128;  // producer threads (wavefronts 2-7)
-constexpr int kA1Chunk = 32;           // positions per chain step (8 LDS reads of 4 products)
+constexpr int kA1Chunk = 32;           // positions per chain step (16 LDS reads of 2 products)
 constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
 constexpr int kA1PairRow = kA1Threads / 2;  // rows up to this length: two lanes per key
 constexpr int kA1ShortRow = 2 * kA1Tile;    // rows up to this length: V staged whole, direct chains
