@@ -286,7 +286,7 @@ class ModelShape:
         return self.hdim // 2
 
 
-# Hy-MT2-1.8B shapes (BASELINE.json configs 3 and 4)
+# Hy-MT2-1.8B shapes (the 1.8B decode and chunked-prefill benchmark workloads)
 HYMT2_1_8B = ModelShape()
 
 LAYER_TYPES = {
