@@ -3,14 +3,16 @@
 One step = one greedy decode token at batch 1: the full 32-layer forward (STQ1_0 panel
 matvecs, RoPE, q/k norms, bf16 KV, GQA attention, SwiGLU), the tied F16 LM head and the
 argmax, all on the device with no host round trip (hymt2_hip_gen_steps). Weights are random
-(seeded) with the config's shapes; the prompt is 64 random ids. Prints one JSON line.
+(seeded) with the config's shapes; the prompt is 64 random chat-template ids (hymt2_amd.synth
+CONFIG3). The greedy ids are checked against the reference's own greedy loop on the same model
+(tests/golden/baseline_config3.npz). Prints one JSON line.
 
   python bench.py [--steps K] [--warmup W] [--no-cpu]
 
 The cpu_baseline leg times the reference library itself (oracle/_ref/libhymt2_ref.so, built
 from the reference's sources) on the host with HYMT2_DEVICE=cpu, HYMT2_REPACK=1, the ISA it
-auto-detects and HYMT2_THREADS = the host's physical cores, on a bounded number of decode
-tokens of the same model.
+auto-detects and HYMT2_THREADS = the host's physical cores, on the same workload: the chat
+text that encodes to the same 64 prompt ids, then 128 greedy decode tokens.
 """
 import argparse
 import ctypes as C
@@ -33,16 +35,30 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_model(ctx: int, seed: int = 3):
+def build_model(ctx: int):
+    """BASELINE config 3's model (hymt2_amd.synth.CONFIG3): 1.8B shapes, STQ1_0 layers, tied F16
+    head whose EOS row is damped so that both legs decode their full length."""
     from hymt2_amd import synth
-    shape = synth.ModelShape(ctx=ctx)
-    model = synth.make_model(shape, mode="stq", seed=seed)
-    # the reference stops greedy decoding at its eos id (2): shrink that row of the tied
-    # embedding/head so it never wins, as the reference's own model test does with its
-    # special-token rows, so both legs decode the same number of tokens
-    e = model["embd"].data.view(np.float16)
-    e[2] = (e[2].astype(np.float32) * 1e-3).astype(np.float16)
-    return shape, model
+    model = synth.baseline_model(synth.CONFIG3, ctx)
+    return model["shape"], model
+
+
+FIXTURE = os.path.join(ROOT, "tests", "golden", "baseline_config3.npz")
+
+
+def check_against_fixture(prompt, ids):
+    """The device loop's greedy ids against the reference's own greedy loop at the scalar ISA on
+    the same model and prompt (tests/golden/baseline_config3.npz, written by
+    tests/golden/make_golden.py --baseline). Raises on any difference."""
+    f = np.load(FIXTURE, allow_pickle=False)
+    if not np.array_equal(f["prompt"], prompt):
+        raise RuntimeError("bench prompt differs from the fixture's prompt")
+    n = min(len(ids), len(f["greedy"]))
+    bad = np.nonzero(ids[:n] != f["greedy"][:n])[0]
+    if len(bad):
+        raise RuntimeError(f"greedy id {bad[0]} differs from the reference: {ids[bad[0]]} != {f['greedy'][bad[0]]}")
+    return dict(checked_ids=int(n), identical=True, reference=f"reference gen_ids at ISA scalar ({f['info']})",
+                min_top2_gap_at_prompt_end=float(f["prompt_logits_top2_gap"]))
 
 
 def _timed_launches(stream, launch, n):
@@ -243,21 +259,28 @@ def gemm_roofline(b, nt: int = 128, copies: int = 8, reps: int = 64):
                                        f"weight copies")
 
 
-def config4(b, seed: int = 4, n_prompt: int = 1024, n_gen: int = 256, chunk: int = 128):
-    """the 1.8B-shaped model with Q2_0C weights, a 1024-token prompt of random
-    ids in 128-token chunks on the device (hymt2_hip_generate_chunked: int8-MFMA GEMMs, causal GQA
-    attention over the growing KV cache, LM head + argmax on the last position), then 256 greedy
-    decode tokens. Prefill and decode are timed separately with HIP events on the backend stream.
-    MFMA utilisation of the prefill = int8 ops of all layer contractions / (time x peak)."""
+def config4(b):
+    """BASELINE config 4 (hymt2_amd.synth.CONFIG4): the 1.8B-shaped model with Q2_0C weights, a
+    1024-token prompt (random chat-template ids) in 128-token chunks on the device
+    (hymt2_hip_generate_chunked: int8-MFMA GEMMs, causal GQA attention over the growing KV cache,
+    LM head + argmax on the last position), then 256 greedy decode tokens. Prefill and decode are
+    timed separately with HIP events on the backend stream. MFMA utilisation of the prefill =
+    int8 ops of all layer contractions / (time x peak). The first greedy ids are checked against
+    the reference's own greedy loop (tests/golden/baseline_config4.npz)."""
     from hymt2_amd import lib, synth
-    shape = synth.ModelShape(ctx=n_prompt + n_gen + 64)
+    cfg = synth.CONFIG4
+    n_prompt, n_gen, chunk = cfg["n_prompt"], cfg["n_gen"], cfg["chunk"]
     t = time.time()
-    model = synth.make_model(shape, mode="q2", seed=seed)
+    model = synth.baseline_model(cfg, n_prompt + n_gen + 64)
+    shape = model["shape"]
     log(f"config 4 model built in {time.time() - t:.1f} s")
     fm = lib.FusedModel(b, model)
-    prompt = synth.rand_prompt(synth.rng(4096), n_prompt, shape.vocab)
+    prompt, _ = synth.baseline_prompt(cfg)
     fm.generate_device(prompt[:chunk + 5], 4, chunk=chunk)  # warm: kernels loaded, graphs captured
     ids, st = fm.generate_device(prompt, n_gen, chunk=chunk)
+    f = np.load(os.path.join(ROOT, "tests", "golden", "baseline_config4.npz"), allow_pickle=False)
+    if not (np.array_equal(f["prompt"], prompt) and np.array_equal(ids[:len(f["greedy"])], f["greedy"])):
+        raise RuntimeError("config 4: greedy ids differ from the reference's (tests/golden/baseline_config4.npz)")
     _, st1 = fm.generate_device(prompt, 2, chunk=1)          # the same prompt one position per step
     weights = sum(L[nm].n * L[nm].k for L in model["layers"] for nm in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"))
     ops = 2.0 * weights * n_prompt
@@ -269,6 +292,7 @@ def config4(b, seed: int = 4, n_prompt: int = 1024, n_gen: int = 256, chunk: int
     fm.close()
     return dict(workload=f"config4: Hy-MT2-1.8B-shaped Q2_0C, {n_prompt}-token random prompt in {chunk}-token "
                          f"chunks, then {n_gen} greedy tokens (device loop)",
+                greedy_parity=f"first {len(f['greedy'])} ids identical to the reference's gen_ids at ISA scalar",
                 prefill_tok_s=round(n_prompt / pre_s, 1), prefill_ms=round(st.prefill_ms, 3),
                 prefill_int8_ops=int(ops), prefill_mfma_util=round(ops / pre_s / 1e12 / INT8_PEAK_TOPS, 4),
                 prefill_stepwise_tok_s=round(st1.prefill_steps / (st1.prefill_ms / 1e3), 1),
@@ -312,7 +336,7 @@ def kernels_only(args):
     calibrates the FETCH_SIZE / WRITE_SIZE counters."""
     import torch
     from hymt2_amd import lib
-    shape, model = build_model(64, args.seed)
+    shape, model = build_model(64)
     b = lib.Backend()
     roof = ffn_in_roofline(model, b, copies=64, passes=1)
     log(f"ffn_in: {roof['avg_us']} us, {roof['achieved']} GB/s")
@@ -325,34 +349,51 @@ def kernels_only(args):
     b.close()
 
 
-def cpu_baseline(model, shape, n_tokens: int):
-    """The reference's own CPU decode loop on the same weights (bounded sample)."""
+def cpu_baseline(model, prompt, text, gpu_ids, n_tokens: int):
+    """The reference's own greedy loop (gen_ids, src/model.c:914-958, compiled from the
+    reference's sources into oracle/_ref/libhymt2_ref.so) on the host cores, on the same weights
+    and the same 64 prompt ids: the chat text it is given encodes to exactly the GPU leg's prompt
+    (checked), then n_tokens greedy tokens. HYMT2_DEVICE=cpu, HYMT2_REPACK=1, the ISA it detects,
+    HYMT2_THREADS = the host's physical cores. Rate = decode tokens / decode time, as
+    hymt2_model_stats and the reference's CLI report it (tools/hymt2_cli.c:92)."""
     from oracle import refbind
     from hymt2_amd import gguf
     if not refbind.available():
-        return None
-    threads = None
+        raise RuntimeError("cpu baseline: oracle/_ref/libhymt2_ref.so is not built (run __graft_entry__.build() "
+                           "where the reference tree is present, or pass --no-cpu)")
     os.environ.update(HYMT2_DEVICE="cpu", HYMT2_REPACK="1")
     os.environ.pop("HYMT2_ISA", None)
     L = refbind.load()
+    isa = refbind.set_isa("auto")
     threads = int(os.environ.get("HYMT2_THREADS") or L.hy_physical_cpu_count())
     os.environ["HYMT2_THREADS"] = str(threads)
+    ctx = len(prompt) + n_tokens + 64
     with tempfile.TemporaryDirectory() as td:
         path = os.path.join(td, "cfg3.gguf")
         gguf.write_model(path, model)
-        rm = refbind.RefModel(path, threads=threads, ctx=shape.ctx)
-        isa = L.hymt2_isa().decode()
-        text = " ".join(["a"] * 31)  # encodes to ~64 prompt ids with the placeholder vocabulary
-        ids, st = rm.generate_text(text, 4)  # warm (page faults, thread pool)
+        rm = refbind.RefModel(path, threads=threads, ctx=ctx)
+        if not np.array_equal(rm.encode_chat(text), prompt):
+            raise RuntimeError("cpu baseline: the chat text does not encode to the GPU leg's prompt ids")
+        rm.generate_text(text, 4)  # warm: page faults, thread pool (the prompt KV is then reused)
+        rm.logits([0])             # reset the prefix cache so the timed run prefills the whole prompt
         t0 = time.perf_counter()
         ids, st = rm.generate_text(text, n_tokens)
         wall = time.perf_counter() - t0
+        info = rm.info()
         rm.close()
-    tok_s = st["decode_tokens"] / (st["decode_ms"] / 1000.0) if st["decode_ms"] > 0 else None
-    return dict(value=round(tok_s, 2) if tok_s else None, unit="tok/s", cores=threads, kind="reference",
-                sample=f"reference hymt2 gen_ids (HYMT2_DEVICE=cpu, ISA {isa}, HYMT2_REPACK=1, {threads} threads): "
-                       f"{st['prefill_tokens'] + st['cached_tokens']}-token prompt then {st['decode_tokens']} greedy decode tokens "
-                       f"of the same model, {wall:.1f} s wall")
+    if len(ids) != n_tokens or st["decode_tokens"] != n_tokens or st["decode_ms"] <= 0 or st["prefill_tokens"] != len(prompt):
+        raise RuntimeError(f"cpu baseline: reference decoded {len(ids)} tokens ({st}), expected a "
+                           f"{len(prompt)}-token prompt and {n_tokens} tokens")
+    tok_s = st["decode_tokens"] / (st["decode_ms"] / 1000.0)
+    n = min(len(ids), len(gpu_ids))
+    agree = int(np.argmin(np.append(ids[:n] == gpu_ids[:n], False)))
+    return dict(value=round(tok_s, 2), unit="tok/s", cores=threads, kind="reference",
+                sample=f"reference hymt2 gen_ids ({info}, HYMT2_DEVICE=cpu, ISA {isa}): {st['prefill_tokens']}-token "
+                       f"prompt then {st['decode_tokens']} greedy decode tokens of the same model and prompt ids, "
+                       f"{wall:.1f} s wall",
+                prefill_tok_s=round(st["prefill_tokens"] / (st["prefill_ms"] / 1000.0), 2),
+                ids_agree_with_gpu=f"{agree} of {n} leading ids (the auto ISA's fp32 order differs from the "
+                                   f"scalar order the GPU matches)")
 
 
 def main():
@@ -360,10 +401,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--prompt", type=int, default=64)
     ap.add_argument("--cpu-tokens", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--no-layer-sets", action="store_true", help="skip the configs 0-2 matvec timings")
     ap.add_argument("--no-config4", action="store_true", help="skip the config 4 chunked-prefill run")
     ap.add_argument("--config4-only", action="store_true",
@@ -388,18 +427,17 @@ def main():
         print(json.dumps(c4), flush=True)
         b.close()
         return
-    n_total = args.prompt + args.warmup + args.steps + 1  # steps fill positions 1..n_total-1
-    ctx = (max(n_total, args.prompt + 33) + 63) // 64 * 64  # also room for the host-loop sample
+    prompt, text = synth.baseline_prompt(synth.CONFIG3)
+    n_total = len(prompt) + args.warmup + args.steps + 1  # steps fill positions 1..n_total-1
+    ctx = (max(n_total, len(prompt) + 33) + 63) // 64 * 64  # also room for the host-loop sample
     t = time.time()
-    shape, model = build_model(ctx, args.seed)
+    shape, model = build_model(ctx)
     log(f"model built in {time.time() - t:.1f} s")
     b = lib.Backend()
     fm = lib.FusedModel(b, model)
     log(f"backend {b.info}; weights uploaded")
-    prompt = synth.rand_prompt(synth.rng(1234), args.prompt, shape.vocab)
-    prompt[prompt == 2] = 3
     fm.gen_begin(prompt, n_total)
-    fm.gen_steps(args.prompt)          # prefill, one position per step (untimed)
+    fm.gen_steps(len(prompt))          # prefill, one position per step (untimed)
     fm.gen_read(0, 1)
     fm.gen_steps(args.warmup)          # warmup decode steps
     fm.gen_read(0, 1)
@@ -409,7 +447,9 @@ def main():
     fm.gen_read(0, 1)                  # waits for the stream
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ids = fm.gen_read(args.prompt, args.warmup + args.steps + 1)
+    ids = fm.gen_read(len(prompt), args.warmup + args.steps + 1)
+    parity = check_against_fixture(prompt, ids)
+    log(f"greedy ids identical to the reference for the first {parity['checked_ids']}")
     tok_s = args.steps / dt
     wb = synth.model_weight_bytes(model)
     log(f"decode: {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token), {len(set(ids.tolist()))} distinct ids")
@@ -431,9 +471,9 @@ def main():
     cpu = None
     if not args.no_cpu:
         t = time.time()
-        cpu = cpu_baseline(model, shape, args.cpu_tokens)
+        cpu = cpu_baseline(model, prompt, text, ids, args.cpu_tokens)
         log(f"cpu baseline in {time.time() - t:.1f} s: {cpu}")
-    avg_pos = args.prompt + args.warmup + (args.steps - 1) / 2.0
+    avg_pos = len(prompt) + args.warmup + (args.steps - 1) / 2.0
     kv_read = 2 * shape.n_layer * shape.kvdim * 2 * (avg_pos + 1)
     token_bytes = wb["layers"] + wb["head"] + kv_read
     out = {
@@ -444,10 +484,10 @@ def main():
         "config": {"workload": "config3: Hy-MT2-1.8B-shaped STQ1_0 greedy decode at batch 1 on the device-resident "
                                "loop (32 layers, hidden 2048, 16/4 heads, hd 128, ffn 6144, vocab 120818, tied F16 "
                                "head, bf16 KV), 64 random prompt ids, random seeded weights",
-                   "global_batch": 1, "prompt": args.prompt, "parallelism": "single GPU",
+                   "global_batch": 1, "prompt": len(prompt), "parallelism": "single GPU",
                    "decode_bytes_per_token": int(token_bytes),
                    "decode_effective_GBs": round(token_bytes * tok_s / 1e9, 1),
-                   "distinct_ids": len(set(ids.tolist()))},
+                   "distinct_ids": len(set(ids.tolist())), "greedy_parity": parity},
         "roofline": roof,
         "head_roofline": head,
         "host_loop": host,

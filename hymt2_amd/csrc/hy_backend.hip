@@ -39,7 +39,7 @@ extern "C" hy_device* hy_device_wrap(int kind, const char* name, void* impl, con
 static constexpr int kDevKindCuda = 2;  // HY_DEV_CUDA, src/device.h:15-21
 
 // ggml type codes, src/internal.h:46
-enum { GT_F32 = 0, GT_F16 = 1, GT_Q4_K = 12, GT_Q6_K = 14, GT_Q2_0C = 40, GT_STQ1_0 = 43 };
+enum { GT_F32 = 0, GT_F16 = 1, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q6_K = 14, GT_Q2_0C = 40, GT_STQ1_0 = 43 };
 
 struct Ctx;
 
@@ -49,6 +49,10 @@ struct DW {  // hy_dweight
     MvWeight mw{};
     void* mem = nullptr;
     size_t bytes = 0;
+    // weight_out: pinned, device-mapped output rows [HY_MAX_BATCH][n] (allocated on first use);
+    // matmul writes them from the kernels directly when the host passes them as the output
+    float* op_host = nullptr;
+    float* op_dev = nullptr;
 };
 
 // Input staging layout (device in_dev and pinned in_host): the position, its RoPE row, then the
@@ -77,8 +81,7 @@ struct Fused {
     int gen_total = 0;   // positions of the current device loop (0: no loop begun)
     int gen_steps = 0;   // steps enqueued so far
     int gen_prompt = 0, gen_vocab = 0;
-    const uint16_t* gen_e16 = nullptr;
-    const float* gen_e32 = nullptr;
+    MvWeight gen_embd{};  // embedding of the current device loop
     hipGraphExec_t g_fwd = nullptr, g_step = nullptr;
     std::vector<const void*> sig_fwd, sig_step;
     float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
@@ -135,6 +138,20 @@ static bool dalloc(Ctx* c, T** p, size_t bytes) {
 
 // ----------------------------------------------------------------------------------- upload
 
+// Kinds the per-op matmul runs: the reference multiplies them with the host's Q8_K activations.
+static bool quant_kind(int kind) { return kind == KIND_PANEL || kind == KIND_Q4K || kind == KIND_Q6K; }
+
+// True when the host will not take the fused path: HYMT2_FUSED=0/off/no forbids it
+// (src/model.c:330-333). The per-op matmul receives only Q8_K activations, so without the fused
+// path a weight that takes fp32 activations (F16, F32, Q8_0: the LM head) is declined at upload
+// and the host computes it on the CPU, as it does with the reference CUDA backend
+// (src/cuda.c:209-212). Accepting it would make the host's first matmul on it fail and turn the
+// device off for the whole run (src/model.c:674-681).
+static bool fused_forbidden() {
+    const char* fe = getenv("HYMT2_FUSED");
+    return fe && (!strcmp(fe, "0") || !strcmp(fe, "off") || !strcmp(fe, "no"));
+}
+
 // Q6_K blocks (210 B, src/internal.h:23: ql[128] qh[64] scales[16] d) -> four aligned planes of
 // the same bytes, so every lane issues 16-byte loads.
 static void q6k_to_planes(const uint8_t* src, size_t nblk, uint8_t* ql, uint8_t* qh, int8_t* sc, uint16_t* d) {
@@ -184,6 +201,10 @@ static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
         q6k_to_planes(w->data, nblk, host.data(), host.data() + nblk * 128,
                       reinterpret_cast<int8_t*>(host.data() + nblk * 192),
                       reinterpret_cast<uint16_t*>(host.data() + nblk * 208));
+    } else if ((w->type == GT_F16 || w->type == GT_F32 || w->type == GT_Q8_0) && fused_forbidden()) {
+        set_err(c, "upload: type %d takes fp32 activations and HYMT2_FUSED forbids the fused path", w->type);
+        delete d;
+        return nullptr;
     } else if ((w->type == GT_F16 && w->k % 32 == 0) || (w->type == GT_F32 && w->k % 16 == 0)) {
         // row tiles (hy_tile_offset): the LM head reads each group's rows piece by piece
         m.kind = w->type == GT_F16 ? KIND_F16 : KIND_F32;
@@ -193,6 +214,22 @@ static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
         host.assign(d->bytes, 0);
         for (size_t r = 0; r < n; r++)
             for (size_t b = 0; b < rowb; b += 16) memcpy(host.data() + hy_tile_offset(r, b, rowb), w->data + r * rowb + b, 16);
+    } else if (w->type == GT_Q8_0 && w->k % 256 == 0) {
+        // 34-byte blocks (f16 d, int8 qs[32], src/internal.h:22) -> row-tiled int8 weights and
+        // row-tiled f16 scales, read by the LM head one thread per row
+        m.kind = KIND_Q8_0;
+        m.nb = w->k / 256;
+        const size_t qrow = (size_t)w->k, drow = (size_t)w->k / 16, qb = hy_tile_bytes(n, qrow);
+        d->bytes = qb + hy_tile_bytes(n, drow);
+        host.assign(d->bytes, 0);
+        for (size_t r = 0; r < n; r++) {
+            const uint8_t* row = w->data + r * (size_t)(w->k / 32) * 34;
+            for (int b = 0; b < w->k / 32; b++) {
+                memcpy(host.data() + qb + hy_tile_offset(r, 2 * (size_t)b, drow), row + 34 * b, 2);
+                for (int piece = 0; piece < 2; piece++)
+                    memcpy(host.data() + hy_tile_offset(r, 32 * (size_t)b + 16 * piece, qrow), row + 34 * b + 2 + 16 * piece, 16);
+            }
+        }
     } else {
         set_err(c, "upload: unsupported weight type %d (k=%d, panel=%d)", w->type, w->k, w->pk != nullptr);
         delete d;
@@ -214,23 +251,54 @@ static hy_dweight* hip_upload(void* impl, const hymt2_weight* w) {
         m.w2 = base + nblk * 128;
         m.sc = reinterpret_cast<const int8_t*>(base + nblk * 192);
         m.dh = reinterpret_cast<const uint16_t*>(base + nblk * 208);
+    } else if (m.kind == KIND_Q8_0) {
+        m.w2 = base + hy_tile_bytes(n, (size_t)w->k);
     }
     return reinterpret_cast<hy_dweight*>(d);
 }
 
+static void free_graphs(Fused* f);
+
+// Frees a device weight. The context's captured graphs may name it (their signatures hold
+// weight handles, and a later upload can reuse the address), so they are dropped too.
 static void hip_release(hy_dweight* w) {
     DW* d = reinterpret_cast<DW*>(w);
     if (!d) return;
+    if (d->c && d->c->f) {
+        if (d->c->s) (void)hipStreamSynchronize(d->c->s);
+        free_graphs(d->c->f);
+    }
     if (d->mem) (void)hipFree(d->mem);
+    if (d->op_host) (void)hipHostFree(d->op_host);
     delete d;
 }
 
 static bool hip_is_sw(const void*) { return false; }
-static float* hip_weight_out(hy_dweight*) { return nullptr; }
+
+// weight_out (src/device.h:76; the reference's cu_weight_out, src/cuda.c:107): a host-visible
+// output buffer of HY_MAX_BATCH rows for this weight. The host hands it back to matmul as the
+// output (gpu_out, src/model.c:662-667), and matmul's kernels then write it over PCIe directly:
+// no device output buffer and no copy. NULL (the host then uses its own buffer) for weights the
+// per-op path does not run, or when the pinned allocation fails.
+static float* hip_weight_out(hy_dweight* w) {
+    DW* d = reinterpret_cast<DW*>(w);
+    if (!d || !quant_kind(d->mw.kind)) return nullptr;
+    if (!d->op_host) {
+        void* p = nullptr;
+        const size_t bytes = (size_t)d->mw.n * HY_MAX_BATCH * sizeof(float);
+        if (hipHostMalloc(&p, bytes, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) return nullptr;
+        void* pd = nullptr;
+        if (hipHostGetDevicePointer(&pd, p, 0) != hipSuccess) {
+            (void)hipHostFree(p);
+            return nullptr;
+        }
+        d->op_host = static_cast<float*>(p);
+        d->op_dev = static_cast<float*>(pd);
+    }
+    return d->op_host;
+}
 
 // ----------------------------------------------------------------------------------- matvec
-
-static bool quant_kind(int kind) { return kind == KIND_PANEL || kind == KIND_Q4K || kind == KIND_Q6K; }
 
 struct JobSpec {
     const DW* w;
@@ -385,6 +453,38 @@ static bool ensure_scratch(Ctx* c, size_t act_bytes, size_t out_bytes) {
     return true;
 }
 
+// One per-op group on the given device staging: the host's Q8_K activations are copied to act,
+// each weight's output goes to its pinned weight_out rows when the host passed those (written by
+// the kernels directly), else to `out` and back to the host's buffer; one synchronisation.
+static bool matmul_group(Ctx* c, hy_dweight* const* ws, float* const* outs, int cnt, const hymt2_q8k_block* xq, int nt,
+                         HyQ8K* act, float* out) {
+    const DW* w0 = reinterpret_cast<const DW*>(ws[0]);
+    HIPCHK(c, hipMemcpyAsync(act, xq, (size_t)nt * w0->mw.nb * sizeof(HyQ8K), hipMemcpyHostToDevice, c->s));
+    size_t off = 0;
+    for (int i = 0; i < cnt; i++) {
+        const DW* w = reinterpret_cast<const DW*>(ws[i]);
+        const bool direct = w->op_host && outs[i] == w->op_host && nt <= HY_MAX_BATCH;
+        JobSpec j{w, direct ? w->op_dev : out + off, w->mw.n, EPI_STORE};
+        MvOpts o;
+        o.act = act;
+        if (!run_multi(c, &j, 1, false, nt, o)) {
+            c->broken = true;
+            return false;
+        }
+        if (!direct) off += (size_t)w->mw.n * nt;
+    }
+    off = 0;
+    for (int i = 0; i < cnt; i++) {
+        const DW* w = reinterpret_cast<const DW*>(ws[i]);
+        if (w->op_host && outs[i] == w->op_host && nt <= HY_MAX_BATCH) continue;
+        const size_t nbytes = (size_t)w->mw.n * nt * sizeof(float);
+        HIPCHK(c, hipMemcpyAsync(outs[i], out + off, nbytes, hipMemcpyDeviceToHost, c->s));
+        off += (size_t)w->mw.n * nt;
+    }
+    HIPCHK(c, hipStreamSynchronize(c->s));
+    return true;
+}
+
 // Per-op path (src/device.h:37-39; reference cu_matmul src/cuda.c:258-280): the weights of one
 // group share the host's Q8_K activations; one synchronisation for the group. F16/F32 weights
 // are rejected: the reference multiplies them with fp32 activations (src/kernels.c:1279-1300),
@@ -406,38 +506,20 @@ static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, in
     }
     const size_t abytes = (size_t)nt * nb * sizeof(HyQ8K);
     if (!ensure_scratch(c, abytes, out_total * sizeof(float))) return false;
-    HIPCHK(c, hipMemcpyAsync(c->act, xq, abytes, hipMemcpyHostToDevice, c->s));
-    size_t off = 0;
-    for (int i = 0; i < cnt; i++) {
-        const DW* w = reinterpret_cast<const DW*>(ws[i]);
-        JobSpec j{w, c->out + off, w->mw.n, EPI_STORE};
-        MvOpts o;
-        o.act = static_cast<const HyQ8K*>(c->act);
-        if (!run_multi(c, &j, 1, false, nt, o)) {
-            c->broken = true;
-            return false;
-        }
-        off += (size_t)w->mw.n * nt;
-    }
-    off = 0;
-    for (int i = 0; i < cnt; i++) {
-        const DW* w = reinterpret_cast<const DW*>(ws[i]);
-        const size_t nbytes = (size_t)w->mw.n * nt * sizeof(float);
-        HIPCHK(c, hipMemcpyAsync(outs[i], c->out + off, nbytes, hipMemcpyDeviceToHost, c->s));
-        off += (size_t)w->mw.n * nt;
-    }
-    HIPCHK(c, hipStreamSynchronize(c->s));
-    return true;
+    return matmul_group(c, ws, outs, cnt, xq, nt, static_cast<HyQ8K*>(c->act), c->out);
 }
 
 // ----------------------------------------------------------------------------------- fused
 
+// Drops the captured graphs. A device loop in progress replays g_step, so it ends here too
+// (gen_steps then reports that no loop has begun).
 static void free_graphs(Fused* f) {
     if (f->g_fwd) (void)hipGraphExecDestroy(f->g_fwd);
     if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
     f->g_fwd = f->g_step = nullptr;
     f->sig_fwd.clear();
     f->sig_step.clear();
+    f->gen_total = 0;
 }
 
 static void free_fused(Fused* f) {
@@ -473,6 +555,7 @@ static bool copy_params(Ctx* c, const hymt2_fused_args* a) {
         HIPCHK(c, hipMemcpy(f->norm_ptr(li, 2), L.q_norm, (size_t)a->hdim * 4, hipMemcpyHostToDevice));
         HIPCHK(c, hipMemcpy(f->norm_ptr(li, 3), L.k_norm, (size_t)a->hdim * 4, hipMemcpyHostToDevice));
     }
+    if (f->eps != a->eps) free_graphs(f);  // captured kernels hold eps by value
     f->eps = a->eps;
     return true;
 }
@@ -717,7 +800,7 @@ static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax,
     }
     if (!ensure_logits(c, f, ow->mw.n)) return false;
     const float* hl = f->d_h + (size_t)(nt - 1) * f->hidden;
-    if (ow->mw.kind == KIND_F16 || ow->mw.kind == KIND_F32) {
+    if (ow->mw.kind == KIND_F16 || ow->mw.kind == KIND_F32 || ow->mw.kind == KIND_Q8_0) {
         HeadArgs h{};
         h.W = ow->mw;
         h.h = hl;
@@ -949,11 +1032,11 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     f->gen_total = 0;
     const DW* e = dw(embd);
     const DW* ow = dw(shape->outw);
-    if (!e || (e->mw.kind != KIND_F16 && e->mw.kind != KIND_F32) || e->mw.k != f->hidden || !ow) {
-        set_err(c, "gen_begin: embedding must be an uploaded F16/F32 [vocab][hidden] weight");
+    if (!e || !embed_kind(e->mw.kind) || e->mw.k != f->hidden || !ow) {
+        set_err(c, "gen_begin: embedding must be an uploaded F16/F32/Q8_0/Q4_K/Q6_K [vocab][hidden] weight");
         return -3;
     }
-    if (n_total > f->ctx || vocab_out < 1 || vocab_out > ow->mw.n) {
+    if (n_total > f->ctx || vocab_out < 1 || vocab_out > ow->mw.n || vocab_out > e->mw.n) {
         set_err(c, "gen_begin: %d positions exceed ctx %d (or bad vocab_out)", n_total, f->ctx);
         return -4;
     }
@@ -976,12 +1059,10 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     sig.push_back(reinterpret_cast<const void*>((intptr_t)vocab_out));
     sig.push_back(reinterpret_cast<const void*>((intptr_t)n_prompt));
     sig.push_back(reinterpret_cast<const void*>((intptr_t)n_total));
-    const uint16_t* e16 = e->mw.kind == KIND_F16 ? static_cast<const uint16_t*>(e->mem) : nullptr;
-    const float* e32 = e->mw.kind == KIND_F32 ? static_cast<const float*>(e->mem) : nullptr;
     if (!f->g_step || f->sig_step != sig) {
         if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
         f->g_step = nullptr;
-        FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e16, e32, f->d_h, f->hidden, n_total,
+        FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e->mw, f->d_h, f->hidden, n_total,
                       f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
         if (!capture(c, &f->g_step, [&] {
                 if (!enqueue_layers(c, shape, 1, 0, f->d_pos) || !enqueue_head(c, shape, 1, true, vocab_out))
@@ -997,7 +1078,7 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->in_dev, f->in_host, kInH, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->key, f->in_host, 8, hipMemcpyHostToDevice, c->s) != hipSuccess ||
-        launch_embed(f->ids, f->d_pos, e16, e32, f->d_h, f->hidden, c->s) != hipSuccess ||
+        launch_embed(f->ids, f->d_pos, e->mw, f->d_h, f->hidden, c->s) != hipSuccess ||
         hipStreamSynchronize(c->s) != hipSuccess) {
         set_err(c, "gen_begin: device setup failed");
         c->broken = true;
@@ -1007,8 +1088,7 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     f->gen_steps = 0;
     f->gen_prompt = n_prompt;
     f->gen_vocab = vocab_out;
-    f->gen_e16 = e16;
-    f->gen_e32 = e32;
+    f->gen_embd = e->mw;
     return 0;
 }
 
@@ -1028,7 +1108,7 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     const int np = f->gen_prompt;
     for (int i = 0; i < np; i += chunk) {
         const int nt = std::min(chunk, np - i);
-        if (launch_embed_rows(f->ids, i, nt, f->gen_e16, f->gen_e32, f->d_h, f->hidden, c->s) != hipSuccess ||
+        if (launch_embed_rows(f->ids, i, nt, f->gen_embd, f->d_h, f->hidden, c->s) != hipSuccess ||
             !enqueue_layers(c, shape, nt, i, nullptr) ||
             (i + nt == np && !enqueue_head(c, shape, nt, true, f->gen_vocab))) {
             c->broken = true;
@@ -1037,7 +1117,7 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     }
     // position np - 1 has been processed: the finishing kernel records the first generated id,
     // embeds it and advances the step counter to np, where the step graph continues
-    FinishArgs fa{f->key, f->ids, f->d_pos, np, f->gen_e16, f->gen_e32, f->d_h, f->hidden, f->gen_total,
+    FinishArgs fa{f->key, f->ids, f->d_pos, np, f->gen_embd, f->d_h, f->hidden, f->gen_total,
                   f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
     if (launch_set_int(f->d_pos, np - 1, c->s) != hipSuccess || launch_finish(fa, c->s) != hipSuccess) {
         set_err(c, "gen_prefill: launch failed");
@@ -1114,7 +1194,9 @@ int hymt2_hip_head(void* impl, hy_dweight* w, const float* h, const float* norm_
                    int n_arg, unsigned long long* key) {
     Ctx* c = static_cast<Ctx*>(impl);
     const DW* d = dw(w);
-    if (!c || c->broken || !d || (d->mw.kind != KIND_F16 && d->mw.kind != KIND_F32) || n_arg > d->mw.n) return -1;
+    if (!c || c->broken || !d || (d->mw.kind != KIND_F16 && d->mw.kind != KIND_F32 && d->mw.kind != KIND_Q8_0) ||
+        n_arg > d->mw.n)
+        return -1;
     HeadArgs a{};
     a.W = d->mw;
     a.h = h;

@@ -20,6 +20,12 @@
 // The table entries are 2^(i/32) correctly rounded to double, minus i<<47. The FMA placement
 // matches glibc's FMA build exactly: checked against the host libm on every float in
 // [-105, 90] (tests/test_expf.py), and on the device against libm in the GPU tests.
+//
+// Attribution: the method, the table layout and the polynomial coefficients below are those of
+// Arm's optimized-routines, math/expf.c and math/exp2f_data.c, Copyright (c) 2017-2018 Arm
+// Limited, SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception; the same routine
+// ships in glibc as sysdeps/ieee754/flt-32/e_expf.c and e_exp2f_data.c (LGPL-2.1-or-later,
+// contributed by Arm). The code here is written for this file; only the numbers must be equal.
 HY_HD inline float hy_expf(float x) {
     constexpr uint64_t T[32] = {
         0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,

@@ -8,7 +8,7 @@
 
 namespace hy {
 
-enum Kind : int { KIND_PANEL = 0, KIND_Q4K = 1, KIND_Q6K = 2, KIND_F16 = 3, KIND_F32 = 4, KIND_ANY = 7 };
+enum Kind : int { KIND_PANEL = 0, KIND_Q4K = 1, KIND_Q6K = 2, KIND_F16 = 3, KIND_F32 = 4, KIND_Q8_0 = 5, KIND_ANY = 7 };
 enum Epi : int { EPI_STORE = 0, EPI_ADD = 1 };
 enum Pro : int { PRO_NONE = 0, PRO_NORM = 1, PRO_QUANT = 2 };
 
@@ -20,6 +20,8 @@ enum Pro : int { PRO_NONE = 0, PRO_NORM = 1, PRO_QUANT = 2 };
 //   F16/F32: w = row tiles (hy_tile_offset): rows in groups of kRowTile, each group stored as
 //          its rows' 16-byte pieces, piece by piece, so that the LM head (one thread per row,
 //          all rows of a group stepping through their pieces together) reads contiguous memory
+//   Q8_0:  the 34-byte blocks (f16 d, int8 qs[32]) split into two row-tiled arrays:
+//          w = int8 weights [n][k], w2 = f16 scales [n][k / 32]
 struct MvWeight {
     int kind, n, k, nb;
     int pshift, poff;
@@ -190,7 +192,7 @@ struct Attn1Args {
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s);
 
 struct HeadArgs {
-    MvWeight W;            // F16 or F32 row tiles
+    MvWeight W;            // F16, F32 or Q8_0 row tiles
     const float* h;        // last token's hidden state [K]
     const float* norm_w;   // output norm
     float eps;
@@ -205,8 +207,7 @@ struct FinishArgs {
     int* ids;              // token ids [n_total]
     int* step;             // device step counter (position of the token just processed)
     int n_prompt;
-    const uint16_t* embd;  // F16 embedding rows [vocab][H], row-tiled (hy_tile_offset)
-    const float* embd32;   // or F32 rows
+    MvWeight E;            // token embedding [vocab][H]: F16 / F32 / Q8_0 / Q4_K / Q6_K
     float* h;              // next step's input [H]
     int H;
     int n_total;
@@ -216,11 +217,12 @@ struct FinishArgs {
     int rope_half, ctx;
 };
 hipError_t launch_finish(const FinishArgs& a, hipStream_t s);
-hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16, const float* embd32, float* h,
-                        int H, hipStream_t s);
-
-hipError_t launch_embed_rows(const int* ids, int first, int nt, const uint16_t* embd16, const float* embd32,
-                             float* h, int H, hipStream_t s);
+// True for the embedding kinds embed_row dequantizes (src/kernels.c:1304-1329).
+inline bool embed_kind(int kind) {
+    return kind == KIND_F16 || kind == KIND_F32 || kind == KIND_Q8_0 || kind == KIND_Q4K || kind == KIND_Q6K;
+}
+hipError_t launch_embed(const int* ids, const int* step, const MvWeight& E, float* h, int H, hipStream_t s);
+hipError_t launch_embed_rows(const int* ids, int first, int nt, const MvWeight& E, float* h, int H, hipStream_t s);
 hipError_t launch_set_int(int* p, int v, hipStream_t s);
 
 hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);

@@ -1026,10 +1026,13 @@ hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
 
 // =========================================================================== LM head
 
+// Key of logit v at row idx for the greedy argmax of src/model.c:945-948, which starts from
+// bv = logits[0] and takes row j only when logits[j] > bv: the first maximal row wins, a NaN at
+// row j > 0 never wins, and a NaN at row 0 wins outright (no comparison with it is true).
 __device__ inline unsigned long long argmax_key(float v, int idx) {
     uint32_t u = hy_fbits(v);
     if (u == 0x80000000u) u = 0;                       // -0 ties with +0 (first index wins)
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0;     // NaN never wins
+    if ((u & 0x7fffffffu) > 0x7f800000u) return idx == 0 ? ~0ull : 0ull;
     const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
 }
@@ -1042,23 +1045,28 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long v) {
     return v;
 }
 
-// One lane per vocabulary row: logits[r] = sum_j f16(W[r][j]) * xn[j] accumulated sequentially
-// (src/kernels.c:1279-1289), after the output RMSNorm (src/model.c:888-890). A workgroup owns
-// one row tile (kRowTile rows, one per thread). In the row-tiled layout piece q (16 bytes) of
-// the tile's rows is one contiguous 4 KB run, so every thread reads its own row straight into
-// registers with coalesced loads: a stage is 64 bytes of the row (four pieces), and four
-// register sets rotate, three stages in flight while one is summed. No LDS staging and no
-// barriers past the norm. Optionally folds the greedy argmax (first index on ties,
-// src/model.c:945-948) into a 64-bit atomicMax key.
-template <bool F16>
+// One lane per vocabulary row: logits[r] = sum_j w(r, j) * xn[j] accumulated sequentially in the
+// reference's order, after the output RMSNorm (src/model.c:888-890):
+//   F16 / F32: s += f16_to_f32(w) * x, one product and one add per weight (src/kernels.c:1279-1300)
+//   Q8_0: per 32-weight block s_b = sum_j (float)q_j * x_j, then sum += f16_to_f32(d_b) * s_b
+//         (dot_q8_0_f32, src/kernels.c:1099-1107)
+// A workgroup owns one row tile (kRowTile rows, one per thread). In the row-tiled layout piece q
+// (16 bytes) of the tile's rows is one contiguous 4 KB run, so every thread reads its own row
+// straight into registers with coalesced loads: a stage is 64 bytes of the row (four pieces),
+// and four register sets rotate, three stages in flight while one is summed. Q8_0 scales come
+// from their own row tiles, one 16-byte piece (8 blocks = 4 stages) at a time, a piece ahead.
+// No LDS staging and no barriers past the norm. Optionally folds the greedy argmax (first index
+// on ties, src/model.c:945-948) into a 64-bit atomicMax key.
+template <int KIND>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
     __shared__ float scale_slot;
     static_assert(kRowTile == 256, "one row per thread");
+    constexpr int WB = KIND == KIND_F16 ? 2 : KIND == KIND_F32 ? 4 : 1;  // bytes per weight
     const int tid = threadIdx.x;
     const int K = a.W.k, n = a.W.n;
     const int r0 = blockIdx.x * kRowTile;
-    const int rowb = F16 ? 2 * K : 4 * K;
+    const int rowb = WB * K;
     const int nstage = rowb / 64;
     // piece q of this thread's row
     const uint8_t* src = a.W.w + (size_t)blockIdx.x * kRowTile * rowb + (size_t)tid * 16;
@@ -1069,10 +1077,18 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) p[i] = *reinterpret_cast<const v4u*>(src + c + (size_t)i * (kRowTile * 16));
     };
+    // Q8_0 scales: piece g holds the f16 d of blocks 8 g .. 8 g + 7 (stages 4 g .. 4 g + 3)
+    const int dpieces = K / 256;
+    const uint8_t* dsrc = KIND == KIND_Q8_0 ? a.W.w2 + (size_t)blockIdx.x * kRowTile * (K / 16) + (size_t)tid * 16
+                                            : nullptr;
+    auto ld_d = [&](int g) __attribute__((always_inline)) {
+        return *reinterpret_cast<const v4u*>(dsrc + (size_t)min(g, dpieces - 1) * (kRowTile * 16));
+    };
+    v4u dcur = {0, 0, 0, 0}, dnext = {0, 0, 0, 0};
     float acc = 0.f;
     auto comp = [&](const v4u (&p)[4], int st) __attribute__((always_inline)) {
         if (st >= nstage) return;
-        if (F16) {
+        if (KIND == KIND_F16) {
             const float* xk = xs + st * 32;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -1083,7 +1099,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
                     acc += hy_f16((uint16_t)(w[e] >> 16)) * xk[8 * q + 2 * e + 1];
                 }
             }
-        } else {
+        } else if (KIND == KIND_F32) {
             const float* xk = xs + st * 16;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -1092,9 +1108,29 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
                 acc += hy_bitsf(p[q].z) * xk[4 * q + 2];
                 acc += hy_bitsf(p[q].w) * xk[4 * q + 3];
             }
+        } else {  // Q8_0: blocks 2 st and 2 st + 1, scales at halves (2 st) % 8 and (2 st + 1) % 8
+            const float* xk = xs + st * 64;
+            const uint32_t dw = (st & 3) == 0 ? dcur.x : (st & 3) == 1 ? dcur.y : (st & 3) == 2 ? dcur.z : dcur.w;
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                float sb = 0.f;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const v4u& pc = p[2 * blk + q];
+                    const uint32_t w[4] = {pc.x, pc.y, pc.z, pc.w};
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        sb += (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * xk[32 * blk + 16 * q + e];
+                }
+                acc += hy_f16((uint16_t)(blk ? dw >> 16 : dw & 0xffffu)) * sb;
+            }
         }
     };
     load_vec_lds(xs, a.h, K);  // first: loads return in issue order
+    if (KIND == KIND_Q8_0) {
+        dcur = ld_d(0);
+        dnext = ld_d(1);
+    }
     ld(s0, 0);
     ld(s1, 1);
     ld(s2, 2);
@@ -1109,6 +1145,10 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
         ld(s2, st + 6);
         comp(s3, st + 3);
         ld(s3, st + 7);
+        if (KIND == KIND_Q8_0) {
+            dcur = dnext;
+            dnext = ld_d(st / 4 + 2);
+        }
     }
     const int r = r0 + tid;
     if (r < n) a.logits[r] = acc;
@@ -1124,10 +1164,13 @@ hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
     const size_t lds = (2 * (size_t)a.W.k) * sizeof(float);
     if (a.W.kind == KIND_F16) {
         if (a.W.k % 32) return hipErrorInvalidValue;
-        k_head<true><<<grid, 256, lds, s>>>(a);
+        k_head<KIND_F16><<<grid, 256, lds, s>>>(a);
     } else if (a.W.kind == KIND_F32) {
         if (a.W.k % 16) return hipErrorInvalidValue;
-        k_head<false><<<grid, 256, lds, s>>>(a);
+        k_head<KIND_F32><<<grid, 256, lds, s>>>(a);
+    } else if (a.W.kind == KIND_Q8_0) {
+        if (a.W.k % 256) return hipErrorInvalidValue;
+        k_head<KIND_Q8_0><<<grid, 256, lds, s>>>(a);
     } else {
         return hipErrorInvalidValue;
     }
@@ -1136,13 +1179,56 @@ hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
 
 // =========================================================================== step finish
 
-// Row tok of a row-tiled F16 or F32 embedding (hy_tile_offset) into h.
-__device__ void embed_row(const uint16_t* e16, const float* e32, int tok, float* h, int H) {
-    if (e16) {
-        for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = hy_f16(e16[hy_tile_offset(tok, 2 * (size_t)i, 2 * (size_t)H) / 2]);
-    } else {
-        for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = e32[hy_tile_offset(tok, 4 * (size_t)i, 4 * (size_t)H) / 4];
+// Element i of row tok of an uploaded embedding, as the reference's dequant_row computes it
+// (src/kernels.c:1304-1329): F16 / F32 / Q8_0 from their row tiles (hy_tile_offset); Q4_K from
+// the raw blocks (q4_k_dequant_row, :844-859: d1 * q - m1 with d1 = d * sc, m1 = dmin * m);
+// Q6_K from its planes (q6_k_dequant_row, :786-806: d * sc * (q - 32)).
+__device__ float embed_elem(const MvWeight& E, int tok, int i, int H) {
+    switch (E.kind) {
+    case KIND_F16:
+        return hy_f16(reinterpret_cast<const uint16_t*>(E.w)[hy_tile_offset(tok, 2 * (size_t)i, 2 * (size_t)H) / 2]);
+    case KIND_F32:
+        return reinterpret_cast<const float*>(E.w)[hy_tile_offset(tok, 4 * (size_t)i, 4 * (size_t)H) / 4];
+    case KIND_Q8_0: {
+        const float d = hy_f16(
+            reinterpret_cast<const uint16_t*>(E.w2)[hy_tile_offset(tok, 2 * (size_t)(i / 32), (size_t)H / 16) / 2]);
+        return d * (float)(int8_t)E.w[hy_tile_offset(tok, (size_t)i, (size_t)H)];
     }
+    case KIND_Q4K: {
+        const uint8_t* b = E.w + ((size_t)tok * E.nb + i / 256) * 144;
+        const int j = i % 256, g = j / 64, is = 2 * g + ((j % 64) >= 32);
+        const float d = hy_f16((uint16_t)(b[0] | (b[1] << 8))), dmin = hy_f16((uint16_t)(b[2] | (b[3] << 8)));
+        const uint8_t* sc = b + 4;
+        int scv, mv;
+        if (is < 4) {
+            scv = sc[is] & 63;
+            mv = sc[is + 4] & 63;
+        } else {
+            scv = (sc[is + 4] & 0xF) | ((sc[is - 4] >> 6) << 4);
+            mv = (sc[is + 4] >> 4) | ((sc[is] >> 6) << 4);
+        }
+        const uint8_t qb = b[16 + 32 * g + j % 32];
+        const int q = (j % 64) < 32 ? (qb & 0xF) : (qb >> 4);
+        const float d1 = d * (float)scv, m1 = dmin * (float)mv;
+        return d1 * (float)q - m1;
+    }
+    case KIND_Q6K: {
+        const size_t blk = (size_t)tok * E.nb + i / 256;
+        const int j = i % 256, half = j / 128, qd = (j % 128) / 32, l = j % 32;
+        const uint8_t ql = E.w[blk * 128 + half * 64 + (qd & 1) * 32 + l];
+        const uint8_t qh = E.w2[blk * 64 + half * 32 + l];
+        const int q = ((qd < 2) ? (ql & 0xF) : (ql >> 4)) | (((qh >> (2 * qd)) & 3) << 4);
+        const float d = hy_f16(E.dh[blk]);
+        return d * (float)E.sc[blk * 16 + half * 8 + l / 16 + 2 * qd] * (float)(q - 32);
+    }
+    default:
+        return 0.f;
+    }
+}
+
+// Row tok of an uploaded embedding into h (dequant_row, src/kernels.c:1304).
+__device__ void embed_row(const MvWeight& E, int tok, float* h, int H) {
+    for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = embed_elem(E, tok, i, H);
 }
 
 // Greedy step tail: token = argmax key; the next input is the next prompt id while the prompt
@@ -1166,7 +1252,7 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
         next_pos = nx;
     }
     __syncthreads();
-    embed_row(a.embd, a.embd32, next_tok, a.h, a.H);
+    embed_row(a.E, next_tok, a.h, a.H);
     if (a.rope_cur && next_pos < a.ctx) {
         for (int i = threadIdx.x; i < a.rope_half; i += blockDim.x) {
             a.rope_cur[i] = a.rope_cos[(size_t)next_pos * a.rope_half + i];
@@ -1184,26 +1270,24 @@ hipError_t launch_finish(const FinishArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-__global__ __launch_bounds__(256) void k_embed(const int* ids, const int* step, const uint16_t* e16,
-                                               const float* e32, float* h, int H) {
-    embed_row(e16, e32, ids[*step], h, H);
+__global__ __launch_bounds__(256) void k_embed(const int* ids, const int* step, MvWeight E, float* h, int H) {
+    embed_row(E, ids[*step], h, H);
 }
 
-hipError_t launch_embed(const int* ids, const int* step, const uint16_t* embd16, const float* embd32, float* h,
-                        int H, hipStream_t s) {
-    k_embed<<<1, 256, 0, s>>>(ids, step, embd16, embd32, h, H);
+hipError_t launch_embed(const int* ids, const int* step, const MvWeight& E, float* h, int H, hipStream_t s) {
+    if (!embed_kind(E.kind)) return hipErrorInvalidValue;
+    k_embed<<<1, 256, 0, s>>>(ids, step, E, h, H);
     return hipGetLastError();
 }
 
 // Embedding rows of nt consecutive ids (ids[first + t] -> h[t]), for a prefill chunk.
-__global__ __launch_bounds__(256) void k_embed_rows(const int* ids, int first, const uint16_t* e16, const float* e32,
-                                                    float* h, int H) {
-    embed_row(e16, e32, ids[first + blockIdx.x], h + (size_t)blockIdx.x * H, H);
+__global__ __launch_bounds__(256) void k_embed_rows(const int* ids, int first, MvWeight E, float* h, int H) {
+    embed_row(E, ids[first + blockIdx.x], h + (size_t)blockIdx.x * H, H);
 }
 
-hipError_t launch_embed_rows(const int* ids, int first, int nt, const uint16_t* embd16, const float* embd32,
-                             float* h, int H, hipStream_t s) {
-    k_embed_rows<<<nt, 256, 0, s>>>(ids, first, embd16, embd32, h, H);
+hipError_t launch_embed_rows(const int* ids, int first, int nt, const MvWeight& E, float* h, int H, hipStream_t s) {
+    if (!embed_kind(E.kind)) return hipErrorInvalidValue;
+    k_embed_rows<<<nt, 256, 0, s>>>(ids, first, E, h, H);
     return hipGetLastError();
 }
 

@@ -31,6 +31,9 @@ class GenStats(C.Structure):
 
 _lib = None
 
+# embedding types the device loop dequantizes on the GPU
+EMBED_TYPES = (abi.GT_F16, abi.GT_F32, abi.GT_Q8_0, abi.GT_Q4_K, abi.GT_Q6_K)
+
 
 def load():
     """Load libhymt2_hip.so (raises if it has not been built)."""
@@ -168,7 +171,7 @@ class FusedModel:
         self.handles.append(self.outw)
         if model["embd"] is model["outw"]:
             self.embd_dev = self.outw
-        elif model["embd"].type in (abi.GT_F16, abi.GT_F32):
+        elif model["embd"].type in EMBED_TYPES:
             self.embd_dev = backend.upload(model["embd"])
             self.handles.append(self.embd_dev)
         else:
@@ -187,13 +190,9 @@ class FusedModel:
         self.vocab_out = model["vocab_out"]
 
     def embed(self, toks) -> np.ndarray:
-        e = self.model["embd"]
-        rows = np.ascontiguousarray(e.data[np.asarray(toks)])
-        if e.type == abi.GT_F16:
-            return rows.view(np.float16).astype(np.float32)
-        if e.type == abi.GT_F32:
-            return rows.view(np.float32).copy()
-        raise ValueError("host embedding supports F16/F32 tables")
+        """The host embedding of forward_batch (dequant_row, src/model.c:802)."""
+        from .synth import dequant_rows
+        return dequant_rows(self.model["embd"], toks)
 
     def forward(self, toks, pos0: int, want_logits: bool = True):
         """One fused_forward of len(toks) <= MAX_CHUNK tokens; returns logits or None."""
@@ -231,7 +230,7 @@ class FusedModel:
         """Greedy loop entirely on the device; the prompt runs as single-token steps (chunk 1)
         or as chunks of up to `chunk` positions. Returns (ids, GenStats)."""
         if self.embd_dev is None:
-            raise ValueError("device generation needs an F16/F32 embedding table")
+            raise ValueError("device generation needs an F16/F32/Q8_0/Q4_K/Q6_K embedding table")
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
         st = GenStats()
@@ -244,7 +243,7 @@ class FusedModel:
 
     def gen_begin(self, prompt, n_total: int):
         if self.embd_dev is None:
-            raise ValueError("device generation needs an F16/F32 embedding table")
+            raise ValueError("device generation needs an F16/F32/Q8_0/Q4_K/Q6_K embedding table")
         self._prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         rc = self.b.L.hymt2_hip_gen_begin(self.b.impl, C.byref(self.args), self.embd_dev, self.vocab_out,
                                           self._prompt.ctypes.data, len(self._prompt), n_total)

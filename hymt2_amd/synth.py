@@ -207,6 +207,67 @@ def quantize_q6_k(x: np.ndarray) -> np.ndarray:
     return out.reshape(n, nb * 210)
 
 
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """fp32 [n, k] -> Q8_0 blocks [n, k/32*34]: f16 d = max|x| / 127 per 32 weights, int8 round to
+    nearest (src/internal.h:22 block_q8_0: f16 d, int8 qs[32])."""
+    n, k = x.shape
+    xb = x.reshape(n, k // 32, 32).astype(np.float32)
+    d = f16_value(f16_bits(np.abs(xb).max(axis=2) / 127.0))
+    q = np.clip(np.rint(xb / np.where(d > 0, d, 1)[..., None]), -127, 127).astype(np.int8)
+    out = np.zeros((n, k // 32, 34), dtype=np.uint8)
+    out[:, :, 0:2] = f16_bits(d).view(np.uint8).reshape(n, k // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(n, k // 32 * 34)
+
+
+def dequant_rows(w: "Weight", rows) -> np.ndarray:
+    """fp32 rows of an F16 / F32 / Q8_0 / Q4_K / Q6_K weight, with the reference's dequant_row
+    operations in its order (src/kernels.c:1304-1329; Q4_K :844-859, Q6_K :786-806), one float32
+    rounding per operation, so the values are bit-identical to the reference host's embedding."""
+    rows = np.asarray(rows)
+    raw = np.ascontiguousarray(w.data.reshape(w.n, w.row_bytes)[rows])
+    m, k, f32 = len(rows), w.k, np.float32
+    if w.type == abi.GT_F16:
+        return raw.view(np.float16).astype(np.float32)
+    if w.type == abi.GT_F32:
+        return raw.view(np.float32).copy()
+    if w.type == abi.GT_Q8_0:
+        b = raw.reshape(m, k // 32, 34)
+        d = f16_value(b[:, :, 0:2].copy().view(np.uint16)[..., 0])
+        return (d[..., None] * b[:, :, 2:].view(np.int8).astype(f32)).reshape(m, k)
+    if w.type == abi.GT_Q4_K:
+        b = raw.reshape(m, k // QK, 144)
+        d = f16_value(b[:, :, 0:2].copy().view(np.uint16)[..., 0])
+        dmin = f16_value(b[:, :, 2:4].copy().view(np.uint16)[..., 0])
+        s = b[:, :, 4:16].astype(np.int32)
+        sc = np.empty(b.shape[:2] + (8,), np.int32)
+        mn = np.empty_like(sc)
+        for j in range(4):
+            sc[..., j], mn[..., j] = s[..., j] & 63, s[..., j + 4] & 63
+            sc[..., j + 4] = (s[..., j + 8] & 0xF) | ((s[..., j] >> 6) << 4)
+            mn[..., j + 4] = (s[..., j + 8] >> 4) | ((s[..., j + 4] >> 6) << 4)
+        qs = b[:, :, 16:].reshape(m, k // QK, 4, 32)
+        q = np.stack([qs & 0xF, qs >> 4], axis=3).reshape(m, k // QK, 8, 32).astype(f32)  # sub-block is
+        d1 = (d[..., None] * sc.astype(f32)).astype(f32)
+        m1 = (dmin[..., None] * mn.astype(f32)).astype(f32)
+        return ((d1[..., None] * q).astype(f32) - m1[..., None]).reshape(m, k)
+    if w.type == abi.GT_Q6_K:
+        b = raw.reshape(m, k // QK, 210)
+        ql, qh = b[:, :, :128].reshape(m, -1, 2, 64), b[:, :, 128:192].reshape(m, -1, 2, 32)
+        sc = b[:, :, 192:208].view(np.int8).reshape(m, -1, 2, 8).astype(f32)
+        d = f16_value(b[:, :, 208:210].copy().view(np.uint16)[..., 0])
+        out = np.empty((m, k // QK, 2, 4, 32), f32)
+        l = np.arange(32)
+        for qd in range(4):
+            lo = ql[..., (qd & 1) * 32 + l]
+            nib = (lo & 0xF) if qd < 2 else (lo >> 4)
+            q = (nib | (((qh >> (2 * qd)) & 3) << 4)).astype(np.int32) - 32
+            scl = sc[..., l // 16 + 2 * qd]
+            out[:, :, :, qd, :] = ((d[..., None, None] * scl).astype(f32) * q.astype(f32)).astype(f32)
+        return out.reshape(m, k)
+    raise ValueError(f"no dequant for type {w.type}")
+
+
 def f16_matrix(g: np.random.Generator, n: int, k: int, sigma=0.02) -> np.ndarray:
     x = g.standard_normal(size=(n, k), dtype=np.float32)
     x *= np.float32(sigma)
@@ -252,6 +313,8 @@ def make_weight(g: np.random.Generator, gtype: int, n: int, k: int, **kw) -> Wei
         return Weight(gtype, k, n, quantize_q4_k(g.normal(0, kw.get("sigma", 0.02), size=(n, k))))
     if gtype == abi.GT_Q6_K:
         return Weight(gtype, k, n, quantize_q6_k(g.normal(0, kw.get("sigma", 0.02), size=(n, k))))
+    if gtype == abi.GT_Q8_0:
+        return Weight(gtype, k, n, quantize_q8_0(g.normal(0, kw.get("sigma", 0.02), size=(n, k))))
     if gtype == abi.GT_F16:
         return Weight(gtype, k, n, f16_matrix(g, n, k, kw.get("sigma", 0.02)))
     if gtype == abi.GT_F32:
@@ -324,6 +387,39 @@ def make_model(shape: ModelShape, mode: str = "stq", seed: int = 3, head_type: i
     cosv, sinv = rope_tables(s.ctx, s.rope_half, s.hdim, s.rope_base, s.rope_alpha)
     return dict(shape=s, mode=mode, layers=layers, embd=embd, outw=embd, out_norm=out_norm,
                 rope_cos=cosv, rope_sin=sinv, vocab_out=s.vocab)
+
+
+def damp_token_row(model: dict, tok: int, factor: float = 1e-3) -> None:
+    """Scale row `tok` of the tied F16 embedding / LM head by `factor`, so that its logit never
+    wins the greedy argmax. Used for the EOS row (id 2) of the benchmark models: the reference's
+    greedy loop stops at EOS (src/model.c:949), and the damped row keeps every run at its full
+    length on both the reference host and the device loop."""
+    e = model["embd"].data.view(np.float16)
+    e[tok] = (e[tok].astype(np.float32) * factor).astype(np.float16)
+
+
+# BASELINE configs 3 and 4: the 1.8B-shaped models and their prompts. The prompts are chat
+# prompts of the "words" vocabulary (hymt2_amd.gguf): [BOS, USER, words..., ASSISTANT], so the
+# reference host's text-driven greedy loop sees exactly these ids.
+CONFIG3 = dict(mode="stq", seed=3, prompt_seed=1234, n_prompt=64, n_gen=128)
+CONFIG4 = dict(mode="q2", seed=4, prompt_seed=4096, n_prompt=1024, n_gen=256, chunk=128)
+
+
+def baseline_model(cfg: dict, ctx: int) -> dict:
+    """The config's model (Hy-MT2-1.8B shapes, tied F16 head with a damped EOS row). The
+    weights do not depend on ctx, which only sizes the RoPE tables."""
+    model = make_model(ModelShape(ctx=ctx), mode=cfg["mode"], seed=cfg["seed"])
+    damp_token_row(model, 2)
+    model["vocab_style"] = "words"
+    return model
+
+
+def baseline_prompt(cfg: dict, vocab: int = HYMT2_1_8B.vocab):
+    """(ids, user text) of the config's prompt: n_prompt ids whose chat-templated text the
+    reference encodes to exactly these ids."""
+    from . import gguf
+    words = rng(cfg["prompt_seed"]).integers(gguf.FIRST_WORD, vocab, size=cfg["n_prompt"] - 3)
+    return np.array(gguf.chat_ids(words), dtype=np.int32), gguf.chat_text(words)
 
 
 def rope_tables(ctx: int, rope_half: int, hdim: int, base: float, alpha: float):

@@ -20,6 +20,10 @@ HOST_LIB = os.path.join(HERE, "_ref", "libhymt2_host.so")
 
 _libs = {}
 
+# The chat template of the reference's greedy loop (src/model.c:915-916).
+CHAT_PRE = "<\uff5chy_begin\u2581of\u2581sentence\uff5c><\uff5chy_User\uff5c>"
+CHAT_POST = "<\uff5chy_Assistant\uff5c>"
+
 
 def available(path: str = REF_LIB) -> bool:
     return os.path.exists(path)
@@ -151,6 +155,20 @@ class RefModel:
             out.append(best)
             ids.append(best)
         return np.array(out, dtype=np.int32)
+
+    def encode(self, text: str) -> np.ndarray:
+        """The reference tokenizer's ids of `text` (tok_encode via hymt2_debug_encode)."""
+        p = C.POINTER(C.c_int)()
+        n = self.L.hymt2_debug_encode(self.m, text.encode(), C.byref(p))
+        ids = np.array([p[i] for i in range(n)], dtype=np.int32)
+        libc = C.CDLL(None)
+        libc.free.argtypes = [C.c_void_p]
+        libc.free(C.cast(p, C.c_void_p))
+        return ids
+
+    def encode_chat(self, user: str) -> np.ndarray:
+        """Ids of the chat prompt gen_ids builds around `user` (src/model.c:915-921)."""
+        return self.encode(CHAT_PRE + user + CHAT_POST)
 
     def generate_text(self, text: str, max_tokens: int):
         """The reference's own greedy loop (gen_ids via hymt2_debug_generate_ids) and its

@@ -13,13 +13,26 @@ scalar ISA (the bit-exact contract of the HIP backend):
 * bf16.npz        dot_bf16 / axpy_bf16 (src/kernels.c:1111-1124) and f32_to_bf16 (:107-111)
 * model_<m>.npz   whole-model logits (hymt2_debug_logits) and 8 greedy ids of a tiny
                   synthetic model loaded from a GGUF by the reference host (src/model.c)
+* baseline_config3.npz / baseline_config4.npz (with --baseline): the BASELINE decode
+                  workloads on the Hy-MT2-1.8B-shaped models (hymt2_amd.synth.CONFIG3 / CONFIG4).
+                  The reference's own greedy loop (gen_ids, src/model.c:914-958, through
+                  hymt2_debug_generate_ids) runs the chat prompt whose encoding is the config's
+                  prompt ids: config 3 = 64 prompt ids then 128 greedy ids; config 4 = 1024 prompt
+                  ids then 32 greedy ids. Logits (hymt2_debug_logits) are stored as a sha256 of
+                  their bits plus the top 32 (index, value) pairs: at the end of the prompt and,
+                  for config 3, after the prompt and the first 127 generated ids (the input of
+                  the loop's last forward). A control run at the auto-detected ISA records how
+                  many leading greedy ids agree with the scalar run.
 
 Inputs are stored in the fixtures (or, for the models, regenerated from a seed and checked
 against a stored digest). Run from the repository root: python tests/golden/make_golden.py
+[--baseline]
 """
+import hashlib
 import os
 import sys
 import tempfile
+import time
 
 import numpy as np
 
@@ -53,7 +66,73 @@ def q8k_inputs() -> np.ndarray:
     return x
 
 
+def logits_summary(prefix: str, lg: np.ndarray, top: int = 32) -> dict:
+    lg = np.ascontiguousarray(lg, dtype=np.float32)
+    order = np.argsort(-lg, kind="stable")[:top]
+    s = np.sort(lg)[::-1]
+    return {f"{prefix}_sha256": hashlib.sha256(lg.view(np.uint32).tobytes()).hexdigest(),
+            f"{prefix}_top_idx": order.astype(np.int32), f"{prefix}_top_val": lg[order],
+            f"{prefix}_top2_gap": np.float32(s[0] - s[1])}
+
+
+# canonical context lengths of the fixtures' models (the weights do not depend on ctx)
+BASELINE_CTX = {"config3": 256, "config4": 1344}
+
+
+def baseline_fixture(name: str, cfg: dict, n_gen: int, last_logits: bool, threads: int = 8):
+    ctx = BASELINE_CTX[name]
+    t0 = time.time()
+    model = synth.baseline_model(cfg, ctx)
+    prompt, text = synth.baseline_prompt(cfg)
+    rec = dict(name=name, mode=cfg["mode"], seed=cfg["seed"], ctx=ctx, digest=synth.model_digest(model),
+               prompt=prompt, n_gen=n_gen, threads=threads)
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, f"{name}.gguf")
+        gguf.write_model(path, model)
+        del model
+        for isa in ("scalar", "auto"):
+            rec_isa = R.set_isa(isa)
+            if isa == "auto":
+                rec["auto_isa"] = rec_isa
+            rm = R.RefModel(path, threads=threads, ctx=ctx)
+            ids = ref_greedy(rm, text, n_gen)
+            if isa == "scalar":
+                got = rm.encode_chat(text)
+                assert np.array_equal(got, prompt), "chat text does not encode to the prompt ids"
+                rec["greedy"] = ids
+                rec["info"] = rm.info()
+                rec.update(logits_summary("prompt_logits", rm.logits(prompt)))
+                if last_logits:
+                    rec.update(logits_summary("last_logits", rm.logits(np.concatenate([prompt, ids[:-1]]))))
+            else:
+                agree = 0
+                while agree < min(len(ids), len(rec["greedy"])) and ids[agree] == rec["greedy"][agree]:
+                    agree += 1
+                rec["auto_agree"] = agree
+                rec["auto_greedy"] = ids
+            rm.close()
+    R.set_isa("scalar")
+    np.savez(os.path.join(OUT, f"baseline_{name}.npz"), **rec)
+    print(name, f"{time.time() - t0:.0f} s: greedy", rec["greedy"][:12], "... auto agrees on", rec["auto_agree"],
+          "of", n_gen, "ids", flush=True)
+
+
+def ref_greedy(rm, text: str, n_gen: int) -> np.ndarray:
+    ids, st = rm.generate_text(text, n_gen)
+    assert len(ids) == n_gen, f"reference generated {len(ids)} ids, expected {n_gen} ({st})"
+    return ids.astype(np.int32)
+
+
+def baseline_fixtures():
+    os.environ.update(HYMT2_DEVICE="cpu", HYMT2_ISA="scalar", HYMT2_REPACK="1", HYMT2_PREFAULT="0")
+    baseline_fixture("config3", synth.CONFIG3, synth.CONFIG3["n_gen"], last_logits=True)
+    baseline_fixture("config4", synth.CONFIG4, 32, last_logits=False)
+
+
 def main():
+    if "--baseline" in sys.argv:
+        baseline_fixtures()
+        return
     R.set_isa("scalar")
     L = R.load()
     g = synth.rng(202)
@@ -73,6 +152,17 @@ def main():
         if w.pk is not None:
             pk, ps = R.panel_repack(w)
             np.savez(os.path.join(OUT, f"panel_{name}.npz"), type=gt, n=n, k=k, data=w.data, pk=pk, ps=ps)
+
+    # Q8_0 (the fp32-activation LM head of src/kernels.c:1099-1107), from its own stream so the
+    # fixtures above keep their inputs
+    gq = synth.rng(203)
+    n, k, nt = 32, 512, 3
+    w = synth.make_weight(gq, abi.GT_Q8_0, n, k)
+    xf = synth.activations(gq, nt, k)
+    out = R.matvec(w, xf, R.quantize_q8k(xf), nt, use_panel=False)
+    deq = R.dequant(synth.Weight(w.type, w.k, 4, w.data[:4]))
+    np.savez(os.path.join(OUT, "matvec_q8_0.npz"), type=abi.GT_Q8_0, n=n, k=k, nt=nt, data=w.data, x=xf,
+             q8k=R.quantize_q8k(xf).view(np.uint8), out=out, dequant4=deq)
 
     n = 300
     q = synth.activations(g, 1, n)[0]

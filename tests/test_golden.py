@@ -10,7 +10,7 @@ from conftest import GOLDEN
 from hymt2_amd import synth
 from oracle import oracle as O
 
-TYPES = ("stq1_0", "q2_0c", "q4_k", "q6_k", "f16", "f32")
+TYPES = ("stq1_0", "q2_0c", "q4_k", "q6_k", "f16", "f32", "q8_0")
 
 
 def load(name):
@@ -87,3 +87,22 @@ def test_model_golden(mode):
     assert np.array_equal(bits(logits), bits(f["logits"]))
     ids = O.OracleModel(model, threads=4).generate(prompt, len(f["greedy"]), batch=8)
     assert np.array_equal(ids, f["greedy"])
+
+
+def test_baseline_config3_oracle():
+    """The oracle at full size against the reference's scalar-ISA greedy loop on BASELINE config
+    3 (tests/golden/baseline_config3.npz): the 1.8B-shaped STQ1_0 model, 64 chat-template prompt
+    ids; the logits at the end of the prompt (sha256 of the bits) and the first greedy ids."""
+    import hashlib
+    f = load("baseline_config3")
+    model = synth.baseline_model(synth.CONFIG3, int(f["ctx"]))
+    assert synth.model_digest(model) == str(f["digest"]), "the generator no longer reproduces the fixture's model"
+    prompt = f["prompt"]
+    om = O.OracleModel(model, threads=8)
+    logits = None
+    for i in range(0, len(prompt), 8):
+        nt = min(8, len(prompt) - i)
+        logits = om.forward(prompt[i:i + nt], i, want_logits=(i + nt == len(prompt)))
+    assert hashlib.sha256(bits(logits).tobytes()).hexdigest() == str(f["prompt_logits_sha256"])
+    ids = O.OracleModel(model, threads=8).generate(prompt, 4, batch=8)
+    assert np.array_equal(ids, f["greedy"][:4])

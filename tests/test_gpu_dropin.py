@@ -46,3 +46,28 @@ def test_reference_host_on_hip_backend(tmp_path, mode):
     for key in ("logits", "stepwise"):
         assert np.array_equal(gpu[key].view(np.uint32), cpu[key].view(np.uint32)), key
     assert len(cpu["ids"]) > 0 and np.array_equal(gpu["ids"], cpu["ids"])
+
+
+@pytest.mark.parametrize("mode", ["stq", "q4km"])
+def test_reference_host_per_op_path(tmp_path, mode):
+    """HYMT2_FUSED=0 (src/model.c:330-333): the host's per-op path. Every layer matvec group goes
+    through the backend's matmul with the weight_out buffers as outputs (gpu_out,
+    src/model.c:662-667); norms, RoPE and attention run on the host. The backend declines the F16
+    head at upload, so the host computes it on the CPU and keeps the device for the layers
+    (reported "gpu=hip", not "+fused"). Logits, stepwise logits and greedy ids equal the CPU's."""
+    if not (refbind.available(refbind.HOST_LIB) and refbind.available(refbind.REF_LIB)):
+        pytest.skip("oracle/_ref host libraries not built (needs the reference tree at build time)")
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=2, hdim=128, vocab=1000, ctx=128)
+    model = synth.make_model(shape, mode=mode, seed=57)
+    path = str(tmp_path / f"m_{mode}.gguf")
+    gguf.write_model(path, model)
+    prompt = synth.rand_prompt(synth.rng(58), 19, shape.vocab)
+    text = "t5 t17 t300 t42"
+    gpu, log = run_leg({"HYMT2_DEVICE": "cuda", "HYMT2_FUSED": "0"}, path, shape.ctx, str(tmp_path / "gpu.npz"),
+                       prompt, text, 12)
+    cpu, _ = run_leg({"HYMT2_DEVICE": "cpu-ref"}, path, shape.ctx, str(tmp_path / "cpu.npz"), prompt, text, 12)
+    info = str(gpu["info"])
+    assert "gpu=hip" in info and "+fused" not in info, info + log[-2000:]
+    for key in ("logits", "stepwise"):
+        assert np.array_equal(gpu[key].view(np.uint32), cpu[key].view(np.uint32)), key
+    assert len(cpu["ids"]) > 0 and np.array_equal(gpu["ids"], cpu["ids"])

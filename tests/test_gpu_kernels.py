@@ -395,9 +395,37 @@ def test_per_op_matmul_128_tokens(backend):
             backend.release(h)
 
 
+def test_per_op_weight_out(backend):
+    """weight_out (src/device.h:76): a pinned host buffer per weight; matmul writes it from the
+    kernels when the host passes it as the output (src/model.c:662-667), and still copies into any
+    other host buffer. Both against the oracle, for a q/k/v-like group at 1, 7 and 16 tokens."""
+    g = synth.rng(81)
+    ws = [synth.make_weight(g, abi.GT_STQ1_0, 512, 1024), synth.make_weight(g, abi.GT_Q4_K, 256, 1024),
+          synth.make_weight(g, abi.GT_Q6_K, 128, 1024)]
+    hs = [backend.upload(w) for w in ws]
+    try:
+        ops = [backend.ops.weight_out(h) for h in hs]
+        assert all(ops)
+        for nt in (1, 7, 16):
+            x = synth.activations(g, nt, 1024)
+            xq = O.quantize_q8k(x)
+            host = np.zeros((nt, 128), np.float32)  # the third weight's output in a host buffer
+            outs = (C.c_void_p * 3)(ops[0], ops[1], host.ctypes.data)
+            assert backend.ops.matmul(backend.impl, (C.c_void_p * 3)(*hs), outs, 3, xq.ctypes.data, nt)
+            for i, w in enumerate(ws):
+                got = host if i == 2 else np.ctypeslib.as_array(
+                    C.cast(ops[i], C.POINTER(C.c_float)), shape=(16 * w.n,))[:nt * w.n].reshape(nt, w.n)
+                assert np.array_equal(bits(got), bits(O.matvec(w, x, xq, nt))), (i, nt)
+        assert backend.ops.weight_out(hs[0]) == ops[0]  # one buffer per weight, kept
+    finally:
+        for h in hs:
+            backend.release(h)
+
+
 # ----------------------------------------------------------------------------- LM head
 
-@pytest.mark.parametrize("gt,n", [(abi.GT_F16, 120818), (abi.GT_F16, 1000), (abi.GT_F32, 777)])
+@pytest.mark.parametrize("gt,n", [(abi.GT_F16, 120818), (abi.GT_F16, 1000), (abi.GT_F32, 777), (abi.GT_Q8_0, 120818),
+                                  (abi.GT_Q8_0, 999)])
 def test_head_and_argmax(backend, gt, n):
     import torch
     g = synth.rng(n)
@@ -422,6 +450,39 @@ def test_head_and_argmax(backend, gt, n):
         assert tok == int(np.argmax(ref[:n_arg]))
     finally:
         backend.release(h)
+
+
+def test_argmax_nan_rules(backend):
+    """The greedy argmax follows src/model.c:945-948 (best = 0, bv = logits[0], take j only when
+    logits[j] > bv): a NaN logit at row 0 wins, a NaN elsewhere never does. Rows of an F32 head
+    weight set to NaN give NaN logits at exactly those rows."""
+    import torch
+    g = synth.rng(4242)
+    n, k = 600, 256
+    w = synth.make_weight(g, abi.GT_F32, n, k, sigma=0.02)
+    hvec = synth.activations(g, 1, k)[0]
+    nw = np.ones(k, np.float32)
+    for nan_rows, want in (([0], 0), ([5, 77], None)):
+        data = w.data.copy().view(np.float32).reshape(n, k)
+        data[nan_rows] = np.nan
+        wn = synth.Weight(abi.GT_F32, k, n, data.view(np.uint8).reshape(n, 4 * k))
+        h = backend.upload(wn)
+        try:
+            logits = empty_f32(n)
+            key = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+            assert backend.L.hymt2_hip_head(backend.impl, h, dev(hvec).data_ptr(), dev(nw).data_ptr(),
+                                            C.c_float(1e-5), logits.data_ptr(), n, key.data_ptr()) == 0
+            sync()
+            ref = logits.cpu().numpy()
+            assert np.isnan(ref[nan_rows]).all()
+            best, bv = 0, ref[0]  # the reference's loop, literally
+            for j in range(1, n):
+                if ref[j] > bv:
+                    best, bv = j, ref[j]
+            tok = 0xFFFFFFFF - (int(key.cpu().numpy()[0]) & 0xFFFFFFFF)
+            assert tok == best and (want is None or tok == want)
+        finally:
+            backend.release(h)
 
 
 # ----------------------------------------------------------------------------- FFN input step
@@ -468,10 +529,18 @@ def test_entry_points_reject_bad_arguments(backend):
         ws = (C.c_void_p * 1)(h)
         outs = (C.c_void_p * 1)(np.zeros(64, np.float32).ctypes.data)
         assert not backend.ops.matmul(backend.impl, ws, outs, 1, xq.ctypes.data, 129)
-        # an unsupported tensor type is refused at upload (NULL), as the reference backend does
-        bad = abi.WeightT(w.data.ctypes.data, abi.GT_Q8_0, 512, 64, abi.row_bytes(abi.GT_Q8_0, 512), None, None, 0, 0,
-                          None)
+        # an unsupported tensor type (Q4_0, ggml type 2) is refused at upload (NULL), as the
+        # reference backend does
+        bad = abi.WeightT(w.data.ctypes.data, 2, 512, 64, 512 // 32 * 18, None, None, 0, 0, None)
         assert not backend.ops.upload(backend.impl, C.byref(bad))
+        # F16 / Q8_0 weights take fp32 activations in the reference (src/kernels.c:1099-1107,
+        # :1279-1289), which the per-op path does not receive: matmul refuses them
+        for gt in (abi.GT_F16, abi.GT_Q8_0):
+            hw = backend.upload(synth.make_weight(g, gt, 64, 512))
+            try:
+                assert not backend.ops.matmul(backend.impl, (C.c_void_p * 1)(hw), outs, 1, xq.ctypes.data, 1)
+            finally:
+                backend.release(hw)
         # the context is still usable afterwards
         backend.matvec(h, act.data_ptr(), out.data_ptr(), 1)
         sync()

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN
-from hymt2_amd import lib, synth
+from hymt2_amd import abi, lib, synth
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -188,6 +188,54 @@ def test_hidden2048_long_context_decode(backend):
     try:
         assert np.array_equal(bits(fm.prefill(list(prompt), batch=1)), bits(ref))
         ids, _ = fm.generate_device(prompt, 40)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
+@pytest.mark.parametrize("head", [abi.GT_Q6_K, abi.GT_Q4_K, abi.GT_Q8_0, abi.GT_F32])
+def test_tied_head_types(backend, head):
+    """Tied embedding / LM head of the other types the reference reads: Q6_K is the head of its own
+    bench and test models (tools/make_bench_gguf.c:30, tests/test_model.py:216-222) and the only
+    head its CUDA backend uploads (src/cuda.c:209-212). Q6_K / Q4_K heads run on the quantized
+    matvec with the RMSNorm + Q8_K prologue and a separate argmax; Q8_0 / F32 on the fp32-activation
+    LM head kernel. The device loop dequantizes the embedding rows itself (dequant_row,
+    src/kernels.c:1304-1329). Two layers at the 1.8B layer shapes; logits after a chunked prefill
+    and after a single-token step, and 20 greedy ids of the device loop (single-token and
+    chunked prompt), against the oracle."""
+    shape = synth.ModelShape(n_layer=2, vocab=1000, ctx=96)
+    model = synth.make_model(shape, mode="stq", seed=61 + head, head_type=head)
+    prompt = synth.rand_prompt(synth.rng(62), 21, shape.vocab)
+    om = O.OracleModel(model, threads=8)
+    om.forward(prompt[:16], 0, False)
+    ref = om.forward(prompt[16:20], 16, True)
+    ref1 = om.forward(prompt[20:], 20, True)
+    want = O.OracleModel(model, threads=8).generate(prompt, 20, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt[:20]), batch=16)), bits(ref))
+        assert np.array_equal(bits(fm.forward([int(prompt[20])], 20, True)), bits(ref1))
+        for chunk in (1, 8):
+            ids, _ = fm.generate_device(prompt, 20, chunk=chunk)
+            assert np.array_equal(ids, want), f"chunk={chunk}"
+        assert np.array_equal(fm.generate_host(prompt, 6, batch=16), want[:6])
+    finally:
+        fm.close()
+
+
+def test_full_vocab_q6k_head(backend):
+    """A Q6_K tied embedding / head at the full vocabulary (120818 x 2048, 203 MB), one layer:
+    logits of a prefill and 6 greedy ids of the device loop against the oracle."""
+    shape = synth.ModelShape(n_layer=1, ctx=64)
+    model = synth.make_model(shape, mode="stq", seed=65, head_type=abi.GT_Q6_K)
+    prompt = synth.rand_prompt(synth.rng(66), 10, shape.vocab)
+    om = O.OracleModel(model, threads=16)
+    ref = om.forward(prompt, 0, True)
+    want = O.OracleModel(model, threads=16).generate(prompt, 6, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.forward(list(prompt), 0, True)), bits(ref))
+        ids, _ = fm.generate_device(prompt, 6)
         assert np.array_equal(ids, want)
     finally:
         fm.close()

@@ -12,7 +12,7 @@ from conftest import ROOT
 from hymt2_amd import abi, gguf, synth
 from oracle import oracle as O
 
-KINDS = [abi.GT_STQ1_0, abi.GT_Q2_0C, abi.GT_Q4_K, abi.GT_Q6_K, abi.GT_F16, abi.GT_F32]
+KINDS = [abi.GT_STQ1_0, abi.GT_Q2_0C, abi.GT_Q4_K, abi.GT_Q6_K, abi.GT_F16, abi.GT_F32, abi.GT_Q8_0]
 
 
 def bits(a):
