@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <unistd.h>
 #include <vector>
@@ -102,7 +103,32 @@ struct Ctx {
     size_t out_cap = 0;
     Fused* f = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    uint8_t* scratch = nullptr;  // this device's address of `scratch` (hymt2_hip_matmul_static), or null
 };
+
+// Device staging of hymt2_hip_matmul_static, the per-op entry point that allocates nothing: the
+// Q8_K activation blocks, then the outputs that go back by copy. Every GPU the library runs on
+// holds one copy of it until the process ends; all calls on one GPU share that copy (calls that
+// overlap on one GPU race on it). In host code the name is a host-side stand-in: kernels and
+// copies use the device address hipGetSymbolAddress returns, kept per device in
+// g_scratch_addr and per context in Ctx::scratch.
+constexpr size_t kScratchBytes = 16u << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static uint8_t* g_scratch_addr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// This device's address of `scratch`, looked up once per device with that device current.
+static uint8_t* scratch_address(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        g_scratch_addr[dev] = static_cast<uint8_t*>(p);
+    }
+    return g_scratch_addr[dev];
+}
 
 static void set_err(Ctx* c, const char* fmt, ...) {
     char buf[512];
@@ -489,23 +515,33 @@ static bool matmul_group(Ctx* c, hy_dweight* const* ws, float* const* outs, int 
 // group share the host's Q8_K activations; one synchronisation for the group. F16/F32 weights
 // are rejected: the reference multiplies them with fp32 activations (src/kernels.c:1279-1300),
 // which this entry point does not receive.
-static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, int cnt, const hymt2_q8k_block* xq,
-                       int nt) {
-    Ctx* c = static_cast<Ctx*>(impl);
-    if (!c || c->broken || cnt < 1 || nt < 1 || nt > HY_MAX_CHUNK || !xq) return false;
+// Checks one per-op group; returns the bytes of its device staging (activations, then the
+// outputs that are not written to weight_out buffers), or 0 when the group is refused.
+static size_t matmul_staging(Ctx* c, hy_dweight* const* ws, float* const* outs, int cnt, const hymt2_q8k_block* xq,
+                             int nt, size_t* act_bytes) {
+    if (!c || c->broken || !ws || !outs || cnt < 1 || nt < 1 || nt > HY_MAX_CHUNK || !xq) return 0;
     const DW* w0 = reinterpret_cast<const DW*>(ws[0]);
+    if (!w0) return 0;
     const int nb = w0->mw.nb;
     size_t out_total = 0;
     for (int i = 0; i < cnt; i++) {
         const DW* w = reinterpret_cast<const DW*>(ws[i]);
-        if (!w || w->mw.nb != nb || w->mw.k != w0->mw.k || !quant_kind(w->mw.kind)) {
+        if (!w || !outs[i] || w->mw.nb != nb || w->mw.k != w0->mw.k || !quant_kind(w->mw.kind)) {
             set_err(c, "matmul: weight %d unsupported for the per-op path", i);
-            return false;
+            return 0;
         }
-        out_total += (size_t)w->mw.n * nt;
+        if (!(w->op_host && outs[i] == w->op_host && nt <= HY_MAX_BATCH)) out_total += (size_t)w->mw.n * nt;
     }
-    const size_t abytes = (size_t)nt * nb * sizeof(HyQ8K);
-    if (!ensure_scratch(c, abytes, out_total * sizeof(float))) return false;
+    *act_bytes = ((size_t)nt * nb * sizeof(HyQ8K) + 255) / 256 * 256;
+    return *act_bytes + out_total * sizeof(float);
+}
+
+static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, int cnt, const hymt2_q8k_block* xq,
+                       int nt) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    size_t abytes = 0;
+    const size_t total = matmul_staging(c, ws, outs, cnt, xq, nt, &abytes);
+    if (!total || !ensure_scratch(c, abytes, total - abytes)) return false;
     return matmul_group(c, ws, outs, cnt, xq, nt, static_cast<HyQ8K*>(c->act), c->out);
 }
 
@@ -949,6 +985,7 @@ void* hymt2_hip_open(char* info, size_t cap) {
         return nullptr;
     }
     for (hipEvent_t& e : c->ev) (void)hipEventCreate(&e);
+    c->scratch = scratch_address(c->dev);  // device 0 is current
     if (info && cap) snprintf(info, cap, "%s (%s, %d CUs)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName,
                               prop.multiProcessorCount);
     return c;
@@ -1188,6 +1225,25 @@ int hymt2_hip_generate_chunked(void* impl, const hymt2_fused_args* shape, hy_dwe
 int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
                        int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
     return hymt2_hip_generate_chunked(impl, shape, embd, vocab_out, prompt, n_prompt, n_gen, 1, out_ids, stats);
+}
+
+bool hymt2_hip_matmul_static(void* impl, hy_dweight* const* ws, float* const* outs, int cnt,
+                             const hymt2_q8k_block* xq, int nt) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    size_t abytes = 0;
+    const size_t total = matmul_staging(c, ws, outs, cnt, xq, nt, &abytes);
+    if (!total) return false;
+    if (!c->scratch) {
+        set_err(c, "matmul_static: the device address of the static scratch is unavailable");
+        return false;
+    }
+    if (total > kScratchBytes) {
+        set_err(c, "matmul_static: the group needs %zu bytes of staging, more than the %zu-byte static scratch", total,
+                kScratchBytes);
+        return false;
+    }
+    return matmul_group(c, ws, outs, cnt, xq, nt, reinterpret_cast<HyQ8K*>(c->scratch),
+                        reinterpret_cast<float*>(c->scratch + abytes));
 }
 
 int hymt2_hip_head(void* impl, hy_dweight* w, const float* h, const float* norm_w, float eps, float* logits,

@@ -131,6 +131,17 @@ HYMT2_HIP_API void *hymt2_hip_stream(void *impl);
 HYMT2_HIP_API int hymt2_hip_quantize_q8k(void *impl, const float *x_dev, void *act_dev, int k, int nt);
 HYMT2_HIP_API int hymt2_hip_matvec(void *impl, hy_dweight *w, const void *act_dev, float *out_dev, int nt);
 
+/* The per-op matmul of the vtable (hy_device_ops.matmul, same arguments and results) with no
+ * allocation: no counterpart in the reference interface. It is for callers that cannot
+ * allocate device memory (hipMalloc) while they run: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation. Its device staging (the Q8_K activations copied from
+ * xq, then the outputs that go back by copy rather than into weight_out buffers) lives in one
+ * static 16 MiB array per GPU, held until the process ends; a group that needs more staging is
+ * refused (false, with a message). All calls on one GPU share that array, so calls that overlap
+ * on one GPU race. It calls no hipMalloc / hipFree. */
+HYMT2_HIP_API bool hymt2_hip_matmul_static(void *impl, hy_dweight *const *ws, float *const *outs, int cnt,
+                                           const hymt2_q8k_block *xq, int nt);
+
 /* Device self-checks of the scalar conversions the kernels use (same device functions):
  * f16 -> f32 and expf over n inputs. */
 HYMT2_HIP_API int hymt2_hip_selftest_f16(void *impl, const uint16_t *src_dev, float *dst_dev, int n);
