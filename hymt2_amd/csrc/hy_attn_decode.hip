@@ -3,15 +3,15 @@
 // per-token RoPE, q/k RMSNorm and bf16 KV store (src/model.c:836-847).
 //
 // Scores: one key per thread per pass of 512 positions, dot_bf16's four interleaved partial
-// sums in order (src/kernels.c:1111-1121); the first pass's key rows load at kernel entry. Softmax (src/model.c:781-789): max (order-free), expf, the sum in
-// position order by the 8-wavefront exact segmented sum (hy_block_exact_sum8), p_j =
-// e_j * (1 / sum). Output (axpy_bf16, src/kernels.c:1122-1124): o[d] += p_j * V_j[d] in
-// position order, as a pipeline over tiles of 96 positions: wavefronts 2-7 form the products
-// p_j * V_j[d] (each rounded to fp32, as the reference rounds them) of tile t + 1 into one half
-// of a double-buffered [j][d] LDS tile while wavefronts 0-1 (one lane per dimension) add tile t
-// from the other half in position order, two products per LDS read; one LDS-only barrier per
-// tile, V rows loaded three tiles ahead. The fp32 output row goes to `ao`; the o-projection
-// quantizes it.
+// sums in order (src/kernels.c:1111-1121); the first pass's key rows load at kernel entry. Softmax
+// (src/model.c:781-789): max (order-free), expf, the sum in position order by the 8-wavefront
+// exact segmented sum (hy_block_exact_sum8), p_j = e_j * (1 / sum) formed once per position.
+// Output (axpy_bf16, src/kernels.c:1122-1124): o[d] += p_j * V_j[d] in position order, as a
+// pipeline over tiles of 96 positions: wavefronts 2-7 convert the V rows of tile t + 1 to fp32
+// into one half of a double-buffered [j][d] LDS tile while wavefronts 0-1 (one lane per
+// dimension) walk tile t in position order, each step one multiply p_j * V_j[d] (rounded to fp32,
+// as the reference rounds it) and one add; one LDS-only barrier per tile, V rows loaded three
+// tiles ahead. The fp32 output row goes to `ao`; the o-projection quantizes it.
 #include "hy_kernels.h"
 
 namespace hy {
@@ -51,22 +51,28 @@ __device__ __forceinline__ void rope_norm_wave(const float (&x)[HD / 64], float*
                                                const float (&sn)[HD / 64], int half, const float (&nw)[HD / 64],
                                                float eps, int lane, float (&out)[HD / 64]) {
     constexpr int RPL = HD / 64;
-#pragma unroll
-    for (int i = 0; i < RPL; i++) scr[lane + 64 * i] = x[i];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float r[RPL];
+    if (RPL == 2 && half == 64) {
+        // the rotation pairs elements lane and lane + 64, both held by this lane
+        r[0] = x[0] * c[0] - x[RPL - 1] * sn[0];
+        r[RPL - 1] = x[0] * sn[0] + x[RPL - 1] * c[0];
+    } else {
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
-        const int d = lane + 64 * i;
-        r[i] = x[i];
-        if (d < half) r[i] = x[i] * c[i] - scr[d + half] * sn[i];
-        else if (d < 2 * half) r[i] = scr[d - half] * sn[i] + x[i] * c[i];
+        for (int i = 0; i < RPL; i++) scr[lane + 64 * i] = x[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int d = lane + 64 * i;
+            r[i] = x[i];
+            if (d < half) r[i] = x[i] * c[i] - scr[d + half] * sn[i];
+            else if (d < 2 * half) r[i] = scr[d - half] * sn[i] + x[i] * c[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int i = 0; i < RPL; i++) scr[lane + 64 * i] = r[i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -159,54 +165,51 @@ __device__ __forceinline__ void a1_load_v(uint2 (&v)[A1Split<HD>::IPT], const ui
         v[k] = *reinterpret_cast<const uint2*>(V + (size_t)min(r0 + P::RSTEP * k, last) * HD + 4 * q);
 }
 
-// e_j of this producer thread's rows of the tile at t0
+// o += p_j * V_j[d] in position order over the first nch chunks of 32 positions of a tile
+// ([j][d] fp32 layout: lane d reads col = tile + d, two positions per LDS read; pj = the tile's
+// p_j, the same for every lane). Positions past the row have V = +0 and p_j = +0, so they add
+// +0, which leaves o unchanged (o is never -0: it starts at +0, and a sum of nonzero addends that
+// cancels rounds to +0). The reads of the next chunk are issued before a chunk is added, and
+// scheduling barriers keep them there: left to itself the compiler moves each read next to its
+// use, and the chain then waits out the LDS latency at every position.
 template <int HD>
-__device__ __forceinline__ void a1_load_e(float (&e)[A1Split<HD>::IPT], const float* ex, int t0, int p, int n) {
-    using P = A1Split<HD>;
-    const int r0 = t0 + p / P::QPR;
-#pragma unroll
-    for (int k = 0; k < P::IPT; k++) e[k] = ex[min(r0 + P::RSTEP * k, n - 1)];
-}
-
-// o += col[0] + col[HD] + col[2 HD] + ... in position order over the first nch chunks of 32
-// positions of a tile column ([j][d] layout: lane d reads col = tile + d, two positions per LDS
-// read); the producers zero the products past the row's end, and o + 0 == o exactly (o is never
-// -0: it starts at +0, and a sum of nonzero addends that cancels rounds to +0). The reads of the
-// next chunk are in flight while a chunk is added.
-template <int HD>
-__device__ __forceinline__ void a1_chain(const float* col, int nch, float& o) {
+__device__ __forceinline__ void a1_chain(const float* col, const float* pj, int nch, float& o) {
     static_assert(kA1Tile == 3 * kA1Chunk, "three chunks per tile");
-    float w0[kA1Chunk], w1[kA1Chunk];
+    constexpr int C = kA1Chunk / 2;  // positions per step
+    float va[C], pa[C], vb[C], pb[C];
+    auto ld = [&](float (&v)[C], float (&p)[C], int j0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kA1Chunk; i++) w0[i] = col[i * HD];
-    if (nch > 1) {
-#pragma unroll
-        for (int i = 0; i < kA1Chunk; i++) w1[i] = col[(kA1Chunk + i) * HD];
-    }
-#pragma unroll
-    for (int i = 0; i < kA1Chunk; i++) o += w0[i];
-    if (nch > 1) {
-        if (nch > 2) {
-#pragma unroll
-            for (int i = 0; i < kA1Chunk; i++) w0[i] = col[(2 * kA1Chunk + i) * HD];
+        for (int i = 0; i < C; i += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(pj + j0 + i);
+            p[i] = q.x, p[i + 1] = q.y, p[i + 2] = q.z, p[i + 3] = q.w;
         }
 #pragma unroll
-        for (int i = 0; i < kA1Chunk; i++) o += w1[i];
-        if (nch > 2) {
+        for (int i = 0; i < C; i++) v[i] = col[(j0 + i) * HD];
+    };
+    auto add = [&](const float (&v)[C], const float (&p)[C]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < kA1Chunk; i++) o += w0[i];
-        }
+        for (int i = 0; i < C; i++) o += p[i] * v[i];
+    };
+    const int steps = 2 * nch;
+    ld(va, pa, 0);
+    for (int c = 0; c < steps; c += 2) {  // no exit inside the body: the prefetches stay where written
+        ld(vb, pb, (c + 1) * C);
+        __builtin_amdgcn_sched_barrier(0);
+        add(va, pa);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(va, pa, min(c + 2, 2 * (kA1Tile / kA1Chunk) - 1) * C);
+        __builtin_amdgcn_sched_barrier(0);
+        add(vb, pb);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// The products p_j * V_j[d] of one tile (p_j = e_j * inv, formed once per position as the
-// reference forms it) for producer thread p's quads, into buf[j][d] (16-byte stores). EDGE (the
-// tile reaches the row's end): position `pos` takes this token's V row from LDS (vb, all read
-// before any product is stored) and positions past the row are +0.
+// V rows of one tile as fp32 into buf[j][d] (16-byte stores) for producer thread p's quads.
+// EDGE (the tile reaches the row's end): position `pos` takes this token's V row from LDS (vb,
+// all read before any value is stored) and positions past the row are +0.
 template <int HD, bool EDGE>
-__device__ __forceinline__ void a1_products(const uint2 (&v)[A1Split<HD>::IPT], float* buf,
-                                            const float (&e)[A1Split<HD>::IPT], const uint16_t* vb, float inv, int t0,
-                                            int p, int pos, int n) {
+__device__ __forceinline__ void a1_stage_tile(const uint2 (&v)[A1Split<HD>::IPT], float* buf, const uint16_t* vb,
+                                              int t0, int p, int pos, int n) {
     using P = A1Split<HD>;
     const int r0 = p / P::QPR, q = p % P::QPR;
     uint2 w[P::IPT];
@@ -223,9 +226,8 @@ __device__ __forceinline__ void a1_products(const uint2 (&v)[A1Split<HD>::IPT], 
 #pragma unroll
     for (int k = 0; k < P::IPT; k++) {
         const int r = r0 + P::RSTEP * k;
-        const float pj = e[k] * inv;
-        float4 x = {pj * hy_bitsf(w[k].x << 16), pj * hy_bitsf(w[k].x & 0xffff0000u), pj * hy_bitsf(w[k].y << 16),
-                    pj * hy_bitsf(w[k].y & 0xffff0000u)};
+        float4 x = make_float4(hy_bitsf(w[k].x << 16), hy_bitsf(w[k].x & 0xffff0000u), hy_bitsf(w[k].y << 16),
+                               hy_bitsf(w[k].y & 0xffff0000u));
         if (EDGE && t0 + r >= n) x = {0.f, 0.f, 0.f, 0.f};
         *reinterpret_cast<float4*>(buf + r * HD + 4 * q) = x;
     }
@@ -285,15 +287,22 @@ __device__ __forceinline__ float a1_short_chain(const float* col, const float* p
     const int nfull = n / C;
     ld(ea, va, 0);
     int c = 0;
+    // scheduling barriers keep each chunk's reads ahead of the previous chunk's adds
     for (; c + 2 <= nfull; c += 2) {  // no exit inside the body: the prefetches stay where written
         ld(eb, vb, (c + 1) * C);
+        __builtin_amdgcn_sched_barrier(0);
         add(ea, va);
+        __builtin_amdgcn_sched_barrier(0);
         ld(ea, va, min((c + 2) * C, LIM));
+        __builtin_amdgcn_sched_barrier(0);
         add(eb, vb);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (c < nfull) {
         ld(eb, vb, min((c + 1) * C, LIM));
+        __builtin_amdgcn_sched_barrier(0);
         add(ea, va);
+        __builtin_amdgcn_sched_barrier(0);
         add_tail(eb, vb, (c + 1) * C);
     } else {
         add_tail(ea, va, c * C);
@@ -301,28 +310,26 @@ __device__ __forceinline__ float a1_short_chain(const float* col, const float* p
     return o;
 }
 
-// One producer step: when the tile at t0 exists (a uniform branch), its products (the edge form
-// when it reaches the row's end) and its barrier; then, on every path, v refilled with the rows
-// three tiles on and e with the next tile's e_j. The loads are unconditional so that every path
-// through a group of three steps leaves the same loads in flight, and the compiler's wait before
-// a tile's products leaves the later tiles' loads outstanding.
+// One producer step: when the tile at t0 exists (a uniform branch), its V rows as fp32 (the edge
+// form when it reaches the row's end) and its barrier; then, on every path, v refilled with the
+// rows three tiles on. The loads are unconditional so that every path through a group of three
+// steps leaves the same loads in flight, and the compiler's wait before a tile's stores leaves
+// the later tiles' loads outstanding.
 template <int HD>
-__device__ __forceinline__ void a1_produce(uint2 (&v)[A1Split<HD>::IPT], float* buf, float (&e)[A1Split<HD>::IPT],
-                                           const float* ex, const uint16_t* vb, const uint16_t* V, float inv, int t0,
-                                           int p, int pos, int n, int last) {
+__device__ __forceinline__ void a1_produce(uint2 (&v)[A1Split<HD>::IPT], float* buf, const uint16_t* vb,
+                                           const uint16_t* V, int t0, int p, int pos, int n, int last) {
     if (t0 < n) {
-        if (t0 + kA1Tile < n) a1_products<HD, false>(v, buf, e, vb, inv, t0, p, pos, n);
-        else a1_products<HD, true>(v, buf, e, vb, inv, t0, p, pos, n);
+        if (t0 + kA1Tile < n) a1_stage_tile<HD, false>(v, buf, vb, t0, p, pos, n);
+        else a1_stage_tile<HD, true>(v, buf, vb, t0, p, pos, n);
     }
     a1_load_v<HD>(v, V, t0 + 3 * kA1Tile, p, last);
-    a1_load_e<HD>(e, ex, t0 + kA1Tile, p, n);
     if (t0 < n) hy_lds_barrier();
 }
 
 // LDS of one head's attention.
 template <int HD>
 struct A1Smem {
-    alignas(16) float ex[kA1MaxCtx];  // e_j = expf(s_j - max)
+    alignas(16) float ex[(kA1MaxCtx + kA1Tile - 1) / kA1Tile * kA1Tile];  // e_j = expf(s_j - max), then p_j
     union {
         HyExactLdsT<kA1Waves> exs;            // the softmax sum of long rows
         alignas(16) float prod[2][kA1Tile * HD];  // then the products of two tiles, [j][d]
@@ -343,7 +350,7 @@ template <int HD>
 __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const float (&x)[HD / 64],
                                         const float (&rc)[HD / 64], const float (&rs)[HD / 64],
                                         const float (&nw)[HD / 64], uint4 (&kA)[HD / 8], uint2 (&v0)[A1Split<HD>::IPT],
-                                        int pos) {
+                                        uint2 (&v1)[A1Split<HD>::IPT], int pos) {
     constexpr int KV4 = HD / 8;                 // 16-byte pieces of one K / V row
     constexpr int RPL = HD / 64;                // row elements per lane
     constexpr int PASSES = kA1MaxCtx / kA1Threads;
@@ -367,7 +374,7 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     const int pp = prd ? tid - 128 : lane;  // producer index (other wavefronts: any valid one)
     const int n = pos + 1;
     uint4 kB[KV4];
-    uint2 v1[A1Split<HD>::IPT], v2[A1Split<HD>::IPT];
+    uint2 v2[A1Split<HD>::IPT];
 
     // 1. RoPE + RMSNorm of q (wavefront 0) and k (1), bf16 of k and v
     if (wave < 2) {
@@ -382,7 +389,8 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
 #pragma unroll
         for (int i = 0; i < RPL; i++) vb[lane + 64 * i] = hy_to_bf16(x[i]);
     }
-    __syncthreads();
+    // LDS only: a full __syncthreads would also wait for every key and V row in flight
+    hy_lds_barrier();
     // the bf16 k, v of this position (src/model.c:842-847), stored once per KV head
     if (h % group == 0 && tid < HD) {
         const size_t off = ((size_t)g * a.ctx + pos) * HD + tid;
@@ -423,19 +431,13 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
             lmax = fmaxf(lmax, sv[p + 1]);
         }
     }
-    // V tiles 1 and 2 (rows clamped below the position), by the producer wavefronts only: the
-    // chain wavefronts never use them (loads left in flight there would hold registers that the
-    // short rows' chains reuse, and make them wait). Long rows: both, so that the same loads
-    // follow tile 0's on every path and the producers' waits leave them out; short rows: tile 1
-    // when the row reaches it.
+    // V tiles 1 and 2 of long rows (rows clamped below the position), by the producer
+    // wavefronts only: both, so that the same loads follow tile 0's on every path and the
+    // producers' waits leave them out (short rows loaded tile 1 at entry).
     const int last = max(pos - 1, 0);
-    if (prd) {
-        if (n > kA1ShortRow) {
-            a1_load_v<HD>(v1, V, kA1Tile, pp, last);
-            a1_load_v<HD>(v2, V, 2 * kA1Tile, pp, last);
-        } else if (n > kA1Tile) {
-            a1_load_v<HD>(v1, V, kA1Tile, pp, last);
-        }
+    if (prd && n > kA1ShortRow) {
+        a1_load_v<HD>(v1, V, kA1Tile, pp, last);
+        a1_load_v<HD>(v2, V, 2 * kA1Tile, pp, last);
     }
     a1_fence();  // issued here, not next to their first use
     lmax = hy_wave_max(lmax);
@@ -488,14 +490,19 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
                 for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? ev[i] : 0.f;
             }
             inv = 1.0f / hy_block_exact_sum8<kA1Waves, false>(e, S.exs, wave, lane);
-            hy_lds_barrier();  // the product tiles reuse the sum's LDS
+        }
+        if (n > kA1ShortRow) {
+            // p_j = e_j * (1 / sum), once per position; +0 past the row to the end of its last tile
+            const int end = (n + kA1Tile - 1) / kA1Tile * kA1Tile;
+            for (int j = tid; j < end; j += kA1Threads) ex[j] = j < n ? ex[j] * inv : 0.f;
+            hy_lds_barrier();  // and the tiles reuse the sum's LDS
         }
     }
 
     // 4. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16). Barrier t: tile t is in
-    //    buffer t % 2, and tile t - 1's buffer has been read. Wavefronts 0 .. HD/64 - 1 add tile t
-    //    after barrier t; the producers form tile t before it, with V three tiles ahead, in
-    //    groups of three steps (one loop exit; steps past the row only load).
+    //    buffer t % 2, and tile t - 1's buffer has been read. Wavefronts 0 .. HD/64 - 1 walk tile
+    //    t after barrier t; the producers convert tile t's V rows before it, with V three tiles
+    //    ahead, in groups of three steps (one loop exit; steps past the row only load).
     // Short rows: every lane of wavefronts 0 .. HD/64 - 1 walks its dimension over the staged V.
     if (n <= kA1ShortRow) {
         static_assert(kA1ShortRow <= kA1SerialSum && kA1ShortRow * HD <= 2 * kA1Tile * HD, "staged V fits");
@@ -509,17 +516,15 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
         for (int t = 0; t < tiles; t++) {
             hy_lds_barrier();
             const int cnt = min(kA1Tile, n - t * kA1Tile);
-            a1_chain<HD>(S.prod[t & 1] + tid, (cnt + kA1Chunk - 1) / kA1Chunk, o);
+            a1_chain<HD>(S.prod[t & 1] + tid, ex + t * kA1Tile, (cnt + kA1Chunk - 1) / kA1Chunk, o);
         }
         a.ao[(size_t)h * HD + tid] = o;
     } else if (prd) {
-        float e[A1Split<HD>::IPT];
-        a1_load_e<HD>(e, ex, 0, pp, n);
         for (int t = 0; t < tiles; t += 3) {
             const int t0 = t * kA1Tile;
-            a1_produce<HD>(v0, S.prod[t & 1], e, ex, vb, V, inv, t0, pp, pos, n, last);
-            a1_produce<HD>(v1, S.prod[(t + 1) & 1], e, ex, vb, V, inv, t0 + kA1Tile, pp, pos, n, last);
-            a1_produce<HD>(v2, S.prod[t & 1], e, ex, vb, V, inv, t0 + 2 * kA1Tile, pp, pos, n, last);
+            a1_produce<HD>(v0, S.prod[t & 1], vb, V, t0, pp, pos, n, last);
+            a1_produce<HD>(v1, S.prod[(t + 1) & 1], vb, V, t0 + kA1Tile, pp, pos, n, last);
+            a1_produce<HD>(v2, S.prod[t & 1], vb, V, t0 + 2 * kA1Tile, pp, pos, n, last);
         }
     } else {
         for (int t = 0; t < tiles; t++) hy_lds_barrier();
@@ -579,10 +584,12 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     } else if (tid < pos) {
         a1_load_key<HD>(kA, K, tid);
     }
-    uint2 v0[A1Split<HD>::IPT];
+    uint2 v0[A1Split<HD>::IPT], v1[A1Split<HD>::IPT];
     a1_load_v<HD>(v0, V, 0, pp, max(pos - 1, 0));
+    // short rows past one tile: the producers' second tile too, staged during the softmax sum
+    if (prd && pos >= kA1Tile && pos < kA1ShortRow) a1_load_v<HD>(v1, V, kA1Tile, pp, pos - 1);
     a1_fence();
-    a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, pos);
+    a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, v1, pos);
 }
 
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {

@@ -135,24 +135,37 @@ __device__ inline int hy_dot4(int a, int b, int c) { return __builtin_amdgcn_sdo
 // from registers at the add latency. Elements past n are read as +0.0f, which leaves the sum
 // unchanged bit for bit because every sum taken here (squares, exponentials) is non-negative,
 // so the running sum is never -0.
+// Lane L's 32 values x[e0 .. e0 + 32) of a row of n (+0 past n): whole groups with 16-byte
+// loads; the one lane that straddles n reads each element at an index clamped below n and
+// selects +0 past it (no per-element branch: with branches the wavefront would run 32
+// exec-masked loads, each waited for, whenever any lane straddles or passes the end).
+__device__ inline void hy_lane_load32(const float* p, int e0, int n, float (&v)[32]) {
+    if (e0 + 32 <= n) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(p + e0 + i);
+            v[i] = q.x;
+            v[i + 1] = q.y;
+            v[i + 2] = q.z;
+            v[i + 3] = q.w;
+        }
+    } else if (e0 < n) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = p[min(e0 + i, n - 1)];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? v[i] : 0.f;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = 0.f;
+    }
+}
+
 __device__ inline float hy_wave_seq_sum(const float* p, int n, int lane) {
     float s = 0.f;
     for (int base = 0; base < n; base += 64 * 32) {
         float v[32];
         const int e0 = base + 32 * lane;
-        if (e0 + 32 <= n) {
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                const float4 q = *reinterpret_cast<const float4*>(p + e0 + i);
-                v[i] = q.x;
-                v[i + 1] = q.y;
-                v[i + 2] = q.z;
-                v[i + 3] = q.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? p[e0 + i] : 0.f;
-        }
+        hy_lane_load32(p, e0, n, v);
         const int nl = min(64, (n - base + 31) / 32);
         for (int L = 0; L < nl; L++) {
             float t = s;
@@ -172,19 +185,9 @@ __device__ inline float hy_wave_seq_sq_sum(const float* x, int n, int lane) {
     for (int base = 0; base < n; base += 64 * 32) {
         float v[32];
         const int e0 = base + 32 * lane;
-        if (e0 + 32 <= n) {
+        hy_lane_load32(x, e0, n, v);
 #pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                const float4 q = *reinterpret_cast<const float4*>(x + e0 + i);
-                v[i] = q.x * q.x;
-                v[i + 1] = q.y * q.y;
-                v[i + 2] = q.z * q.z;
-                v[i + 3] = q.w * q.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? x[e0 + i] * x[e0 + i] : 0.f;
-        }
+        for (int i = 0; i < 32; i++) v[i] = v[i] * v[i];  // +0 past n stays +0
         const int nl = min(64, (n - base + 31) / 32);
         for (int L = 0; L < nl; L++) {
             float t = s;
@@ -266,20 +269,7 @@ __device__ inline double hy_readlane_d(double x, int l) {
 // hy_wave_load32 fetches lane L's values x[32L .. 32L+32) (zero past n); hy_wave_exact_sq_sum_v
 // takes them, so a caller can issue the loads early.
 __device__ inline void hy_wave_load32(const float* x, int n, int lane, float (&v)[32]) {
-    const int e0 = 32 * lane;
-    if (e0 + 32 <= n) {
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            const float4 q = *reinterpret_cast<const float4*>(x + e0 + i);
-            v[i] = q.x;
-            v[i + 1] = q.y;
-            v[i + 2] = q.z;
-            v[i + 3] = q.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = e0 + i < n ? x[e0 + i] : 0.f;
-    }
+    hy_lane_load32(x, 32 * lane, n, v);
 }
 
 __device__ inline float hy_wave_exact_sq_sum_v(const float (&xv)[32], int lane) {

@@ -26,6 +26,21 @@ constexpr int kMv1MaxWgs = 192;
 
 }  // namespace
 
+// Forces a kernel-argument value into SGPRs at this point (see k_mv1).
+template <typename T>
+__device__ __forceinline__ void hy_sgpr_pin(const T& v) {
+    asm volatile("" ::"s"(v));
+}
+
+// The fields of a job the kernel reads, for the weight kinds it may hold.
+template <int KIND>
+__device__ __forceinline__ void mv1_pin_job(const Mv1Job& J) {
+    hy_sgpr_pin(J.W.w), hy_sgpr_pin(J.W.n), hy_sgpr_pin(J.out), hy_sgpr_pin(J.epi), hy_sgpr_pin(J.wg_begin);
+    if (KIND == KIND_PANEL) hy_sgpr_pin(J.W.ps), hy_sgpr_pin(J.W.pshift), hy_sgpr_pin(J.W.poff);
+    if (KIND == KIND_Q6K || KIND == KIND_ANY) hy_sgpr_pin(J.W.w2), hy_sgpr_pin(J.W.sc), hy_sgpr_pin(J.W.dh);
+    if (KIND == KIND_ANY) hy_sgpr_pin(J.W.kind);
+}
+
 // KIND: PANEL, Q4K, Q6K, or ANY (Q4K and Q6K jobs mixed; the kind is read per workgroup).
 // SPL: 16-byte segments per lane per row (the row has 32 * SPL segments).
 template <int KIND, int SPL, int ITERS, int PRO>
@@ -43,24 +58,35 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hh = lane >> 5, j = lane & 31;
     const int wg = blockIdx.x;
+    // Every kernel argument this workgroup may use, loaded in one round of scalar loads and
+    // pinned in SGPRs before any selection: selecting the job by its index first makes the
+    // compiler load the chosen job's fields only once the index is known, several dependent
+    // round trips to memory before the first vector load can issue.
+    const Mv1Job j0 = L.job[0], j1 = L.job[1], j2 = L.job[2];
+    const int pair = L.pair, njobs = L.njobs, rows_per_wg = L.rows_per_wg;
+    const float* const lx = L.x;
+    const float* const lnorm = L.norm_w;
+    const HyQ8K* const lact = L.act;
+    hy_sgpr_pin(pair), hy_sgpr_pin(njobs), hy_sgpr_pin(rows_per_wg), hy_sgpr_pin(lx), hy_sgpr_pin(lnorm),
+        hy_sgpr_pin(lact);
+    mv1_pin_job<KIND>(j0), mv1_pin_job<KIND>(j1), mv1_pin_job<KIND>(j2);
     int jsel = 0;
-    if (!L.pair) {
-        if (L.njobs > 1 && wg >= L.job[1].wg_begin) jsel = 1;
-        if (L.njobs > 2 && wg >= L.job[2].wg_begin) jsel = 2;
+    if (!pair) {
+        if (njobs > 1 && wg >= j1.wg_begin) jsel = 1;
+        if (njobs > 2 && wg >= j2.wg_begin) jsel = 2;
     }
-    // constant-index selection only (a runtime index into the argument would spill it)
-    const Mv1Job J = jsel == 0 ? L.job[0] : (jsel == 1 ? L.job[1] : L.job[2]);
-    const bool up = L.pair && hh;  // pair mode: half-wave 1 streams the up rows
+    const Mv1Job J = jsel == 0 ? j0 : (jsel == 1 ? j1 : j2);
+    const bool up = pair && hh;  // pair mode: half-wave 1 streams the up rows
     const int kind = KIND == KIND_ANY ? J.W.kind : KIND;
-    const uint8_t* w = up ? L.job[1].W.w : J.W.w;
-    const uint8_t* w2 = up ? L.job[1].W.w2 : J.W.w2;
-    const int8_t* wsc = up ? L.job[1].W.sc : J.W.sc;
-    const uint16_t* wdh = up ? L.job[1].W.dh : J.W.dh;
-    const float* wps = up ? L.job[1].W.ps : J.W.ps;
-    const int pshift = up ? L.job[1].W.pshift : J.W.pshift;
-    const int poff = up ? L.job[1].W.poff : J.W.poff;
+    const uint8_t* w = up ? j1.W.w : J.W.w;
+    const uint8_t* w2 = up ? j1.W.w2 : J.W.w2;
+    const int8_t* wsc = up ? j1.W.sc : J.W.sc;
+    const uint16_t* wdh = up ? j1.W.dh : J.W.dh;
+    const float* wps = up ? j1.W.ps : J.W.ps;
+    const int pshift = up ? j1.W.pshift : J.W.pshift;
+    const int poff = up ? j1.W.poff : J.W.poff;
     const int n = J.W.n;
-    const int row0 = (wg - J.wg_begin) * L.rows_per_wg;
+    const int row0 = (wg - J.wg_begin) * rows_per_wg;
 
     // 1. the prologue's inputs first (vector loads complete in issue order, so anything issued
     //    before the weights can be consumed without waiting for them); the residual of this
@@ -70,23 +96,23 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     float e[R][8], nw[R][8];
     float resid = 0.f;
     const int rrow = min(row0 + wave * RPW + lane, n - 1);  // the row this lane sums (lane < RPW)
-    if (!L.pair && J.epi == EPI_ADD) resid = J.out[rrow];
+    if (!pair && J.epi == EPI_ADD) resid = J.out[rrow];
     ActSeg A[SPL];
     if (PRO == PRO_NONE) {
 #pragma unroll
-        for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(L.act, kind, j + 32 * s);
+        for (int s = 0; s < SPL; s++) A[s] = gather_act<SPB>(lact, kind, j + 32 * s);
     }
     if (PRO != PRO_NONE) {
 #pragma unroll
         for (int k = 0; k < R; k++) {
             const int off = (2 * (wave * R + k)) * HY_QK + 8 * lane;
-            const float4 v0 = *reinterpret_cast<const float4*>(L.x + off);
-            const float4 v1 = *reinterpret_cast<const float4*>(L.x + off + 4);
+            const float4 v0 = *reinterpret_cast<const float4*>(lx + off);
+            const float4 v1 = *reinterpret_cast<const float4*>(lx + off + 4);
             e[k][0] = v0.x, e[k][1] = v0.y, e[k][2] = v0.z, e[k][3] = v0.w;
             e[k][4] = v1.x, e[k][5] = v1.y, e[k][6] = v1.z, e[k][7] = v1.w;
             if (PRO == PRO_NORM) {
-                const float4 u0 = *reinterpret_cast<const float4*>(L.norm_w + off);
-                const float4 u1 = *reinterpret_cast<const float4*>(L.norm_w + off + 4);
+                const float4 u0 = *reinterpret_cast<const float4*>(lnorm + off);
+                const float4 u1 = *reinterpret_cast<const float4*>(lnorm + off + 4);
                 nw[k][0] = u0.x, nw[k][1] = u0.y, nw[k][2] = u0.z, nw[k][3] = u0.w;
                 nw[k][4] = u1.x, nw[k][5] = u1.y, nw[k][6] = u1.z, nw[k][7] = u1.w;
             }
@@ -100,7 +126,7 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     WSeg ws[ITERS][SPL];
 #pragma unroll
     for (int i = 0; i < ITERS; i++) {
-        const int r = L.pair ? row0 + wave * ITERS + i : row0 + wave * RPW + 2 * i + hh;
+        const int r = pair ? row0 + wave * ITERS + i : row0 + wave * RPW + 2 * i + hh;
         const int rl = min(r, n - 1);
 #pragma unroll
         for (int s = 0; s < SPL; s++) ws[i][s] = load_wseg<SPB>(kind, w, w2, wsc, wdh, wps, NB, rl, j + 32 * s);
@@ -144,7 +170,7 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     __syncthreads();
 
     // 5. per-row sums in block order and the epilogue
-    if (!L.pair) {
+    if (!pair) {
         if (lane < RPW) {
             const int r = row0 + wave * RPW + lane;
             if (r < n) {
