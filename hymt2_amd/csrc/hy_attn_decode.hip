@@ -535,6 +535,12 @@ template <int HD>
 __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     constexpr int RPL = HD / 64;
     __shared__ A1Smem<HD> S;
+    // Every kernel argument in one round of scalar loads, pinned in SGPRs before use: the
+    // per-wavefront selections below would otherwise chain dependent loads of the arguments.
+    hy_sgpr_pin(a.q), hy_sgpr_pin(a.k), hy_sgpr_pin(a.v), hy_sgpr_pin(a.kc), hy_sgpr_pin(a.vc),
+        hy_sgpr_pin(a.q_norm), hy_sgpr_pin(a.k_norm), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin),
+        hy_sgpr_pin(a.pos_dev), hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.pos0), hy_sgpr_pin(a.ao), hy_sgpr_pin(a.heads),
+        hy_sgpr_pin(a.kv_heads), hy_sgpr_pin(a.rope_half), hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.eps);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = blockIdx.x;
     const int g = h / (a.heads / a.kv_heads);

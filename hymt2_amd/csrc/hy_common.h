@@ -60,6 +60,15 @@ __device__ inline uint16_t hy_to_bf16(float f) {
 
 // Workgroup barrier for LDS only: waits for this wave's LDS operations, not for its global
 // loads, so prefetches stay in flight across it (a __syncthreads fence would drain them).
+// Forces a (kernel-argument) value into SGPRs at this point. Pinning every argument a kernel
+// uses at its entry makes the compiler issue all their scalar loads in one round: argument
+// fields chosen by a runtime index or read after a branch otherwise become dependent round
+// trips to memory (about 0.15-0.25 us each at kernel start) before the first vector load.
+template <typename T>
+__device__ __forceinline__ void hy_sgpr_pin(const T& v) {
+    asm volatile("" ::"s"(v));
+}
+
 __device__ __forceinline__ void hy_lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }

@@ -26,12 +26,6 @@ constexpr int kMv1MaxWgs = 192;
 
 }  // namespace
 
-// Forces a kernel-argument value into SGPRs at this point (see k_mv1).
-template <typename T>
-__device__ __forceinline__ void hy_sgpr_pin(const T& v) {
-    asm volatile("" ::"s"(v));
-}
-
 // The fields of a job the kernel reads, for the weight kinds it may hold.
 template <int KIND>
 __device__ __forceinline__ void mv1_pin_job(const Mv1Job& J) {

@@ -1061,6 +1061,9 @@ template <int KIND>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
     __shared__ float scale_slot;
+    hy_sgpr_pin(a.W.w), hy_sgpr_pin(a.W.w2), hy_sgpr_pin(a.W.k), hy_sgpr_pin(a.W.n), hy_sgpr_pin(a.h),
+        hy_sgpr_pin(a.norm_w), hy_sgpr_pin(a.eps), hy_sgpr_pin(a.logits), hy_sgpr_pin(a.argmax_key),
+        hy_sgpr_pin(a.n_arg), hy_sgpr_pin(blockDim.x);
     static_assert(kRowTile == 256, "one row per thread");
     constexpr int WB = KIND == KIND_F16 ? 2 : KIND == KIND_F32 ? 4 : 1;  // bytes per weight
     const int tid = threadIdx.x;
@@ -1226,41 +1229,56 @@ __device__ float embed_elem(const MvWeight& E, int tok, int i, int H) {
     }
 }
 
-// Row tok of an uploaded embedding into h (dequant_row, src/kernels.c:1304).
+// Row tok of an uploaded embedding into h (dequant_row, src/kernels.c:1304). F16 / F32 rows are
+// read as whole 16-byte pieces of the row-tiled layout (piece p holds the row's bytes
+// 16p .. 16p + 15); the block formats element by element.
 __device__ void embed_row(const MvWeight& E, int tok, float* h, int H) {
+    if (E.kind == KIND_F16 || E.kind == KIND_F32) {
+        const int wb = E.kind == KIND_F16 ? 2 : 4, rowb = wb * H;
+        for (int p = threadIdx.x; p < rowb / 16; p += blockDim.x) {
+            const v4u q = *reinterpret_cast<const v4u*>(E.w + hy_tile_offset(tok, 16 * (size_t)p, rowb));
+            float4* dst = reinterpret_cast<float4*>(h + p * (16 / wb));
+            if (wb == 2) {
+                dst[0] = make_float4(hy_f16((uint16_t)(q.x & 0xffffu)), hy_f16((uint16_t)(q.x >> 16)),
+                                     hy_f16((uint16_t)(q.y & 0xffffu)), hy_f16((uint16_t)(q.y >> 16)));
+                dst[1] = make_float4(hy_f16((uint16_t)(q.z & 0xffffu)), hy_f16((uint16_t)(q.z >> 16)),
+                                     hy_f16((uint16_t)(q.w & 0xffffu)), hy_f16((uint16_t)(q.w >> 16)));
+            } else {
+                dst[0] = make_float4(hy_bitsf(q.x), hy_bitsf(q.y), hy_bitsf(q.z), hy_bitsf(q.w));
+            }
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = embed_elem(E, tok, i, H);
 }
 
 // Greedy step tail: token = argmax key; the next input is the next prompt id while the prompt
 // lasts, else the argmax (recorded in ids). Embeds the next token's row into h, copies the next
-// position's RoPE row, advances the device step counter and clears the key.
+// position's RoPE row, advances the device step counter and clears the key. The key, the step
+// and the prompt id are read by every thread (uniform scalar loads, one round each), so no
+// broadcast is needed before the embedding; the writes wait for every wavefront's reads.
 __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
-    __shared__ int next_tok, next_pos;
-    if (threadIdx.x == 0) {
-        const unsigned long long key = *a.argmax_key;
-        const int best = key ? (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull)) : 0;
-        const int step = *a.step;
-        const int nx = step + 1;
-        int tok;
-        if (nx < a.n_prompt) {
-            tok = a.ids[nx];
-        } else {
-            tok = best;
-            if (nx < a.n_total) a.ids[nx] = best;
-        }
-        next_tok = tok;
-        next_pos = nx;
-    }
-    __syncthreads();
-    embed_row(a.E, next_tok, a.h, a.H);
-    if (a.rope_cur && next_pos < a.ctx) {
+    hy_sgpr_pin(a.argmax_key), hy_sgpr_pin(a.ids), hy_sgpr_pin(a.step), hy_sgpr_pin(a.n_prompt),
+        hy_sgpr_pin(a.E.w), hy_sgpr_pin(a.E.kind), hy_sgpr_pin(a.h), hy_sgpr_pin(a.H), hy_sgpr_pin(a.n_total),
+        hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin), hy_sgpr_pin(a.rope_half),
+        hy_sgpr_pin(a.ctx), hy_sgpr_pin(blockDim.x);
+    const unsigned long long key = *a.argmax_key;
+    const int step = *a.step;
+    const int nx = step + 1;
+    const int pid = a.ids[min(nx, a.n_total - 1)];  // the next prompt id, if the prompt lasts
+    const int best = key ? (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull)) : 0;
+    const int next_tok = nx < a.n_prompt ? pid : best;
+    if (a.rope_cur && nx < a.ctx) {
         for (int i = threadIdx.x; i < a.rope_half; i += blockDim.x) {
-            a.rope_cur[i] = a.rope_cos[(size_t)next_pos * a.rope_half + i];
-            a.rope_cur[a.rope_half + i] = a.rope_sin[(size_t)next_pos * a.rope_half + i];
+            a.rope_cur[i] = a.rope_cos[(size_t)nx * a.rope_half + i];
+            a.rope_cur[a.rope_half + i] = a.rope_sin[(size_t)nx * a.rope_half + i];
         }
     }
+    embed_row(a.E, next_tok, a.h, a.H);
+    __syncthreads();
     if (threadIdx.x == 0) {
-        *a.step = next_pos;
+        if (nx >= a.n_prompt && nx < a.n_total) a.ids[nx] = best;
+        *a.step = nx;
         *a.argmax_key = 0ull;
     }
 }
