@@ -340,6 +340,7 @@ struct A1Smem {
     alignas(16) uint16_t vb[HD];
     float red[kA1Waves];
     float stat;
+    uint64_t etab[32];  // expf table
 };
 
 // Phases 1-4 of one head's attention, every thread of the workgroup: this token's rows (x:
@@ -350,7 +351,7 @@ template <int HD>
 __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const float (&x)[HD / 64],
                                         const float (&rc)[HD / 64], const float (&rs)[HD / 64],
                                         const float (&nw)[HD / 64], uint4 (&kA)[HD / 8], uint2 (&v0)[A1Split<HD>::IPT],
-                                        uint2 (&v1)[A1Split<HD>::IPT], int pos) {
+                                        uint2 (&v1)[A1Split<HD>::IPT], int pos, uint64_t etv) {
     constexpr int KV4 = HD / 8;                 // 16-byte pieces of one K / V row
     constexpr int RPL = HD / 64;                // row elements per lane
     constexpr int PASSES = kA1MaxCtx / kA1Threads;
@@ -442,6 +443,7 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     a1_fence();  // issued here, not next to their first use
     lmax = hy_wave_max(lmax);
     if (lane == 0) red[wave] = lmax;
+    if (tid < 32) S.etab[tid] = etv;
     hy_lds_barrier();
 
     // 3. softmax (src/model.c:781-789): max (order-free), e_j = expf(s_j - max), their sum in
@@ -456,11 +458,11 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
         for (int p = 0; p < PASSES; p++) {
             const int j = p * kA1Threads + tid;
             if (pair) {
-                if ((tid & 1) == 0 && (tid >> 1) < n) ex[tid >> 1] = hy_expf(sv[0] - mx);
+                if ((tid & 1) == 0 && (tid >> 1) < n) ex[tid >> 1] = hy_expf_tab(sv[0] - mx, S.etab);
                 break;
             }
             if (j - tid >= n) break;
-            if (j < n) ex[j] = hy_expf(sv[p] - mx);
+            if (j < n) ex[j] = hy_expf_tab(sv[p] - mx, S.etab);
         }
         hy_lds_barrier();
         if (n <= kA1SerialSum) {
@@ -559,6 +561,7 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     // The rows and norm weights first, before the position is read: scalar loads are waited
     // for all together, so a row load issued after the position's load would wait for it.
     float x[RPL], rc[RPL], rs[RPL], nw[RPL];
+    const uint64_t etv = tid < 32 ? hy_exp_tab_entry(tid) : 0;  // expf table entry, into LDS before the max
     {
         const float* src = wave == 0 ? a.q + (size_t)h * HD : (wave == 1 ? a.k + (size_t)g * HD : a.v + (size_t)g * HD);
         const float* nsrc = wave == 0 ? a.q_norm : a.k_norm;
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     // short rows past one tile: the producers' second tile too, staged during the softmax sum
     if (prd && pos >= kA1Tile && pos < kA1ShortRow) a1_load_v<HD>(v1, V, kA1Tile, pp, pos - 1);
     a1_fence();
-    a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, v1, pos);
+    a1_core<HD>(a, S, x, rc, rs, nw, kA, v0, v1, pos, etv);
 }
 
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {
@@ -603,6 +606,408 @@ hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {
     switch (a.hdim) {
     case 64: k_attn1<64><<<a.heads, kA1Threads, 0, s>>>(a); break;
     case 128: k_attn1<128><<<a.heads, kA1Threads, 0, s>>>(a); break;
+    default: return hipErrorNotSupported;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ split form for long rows
+//
+// The same attention as k_attn1 in two kernels, so that long rows use many CUs:
+//   k_attn_scores, one 256-thread workgroup per (KV head, segment of kSplitSeg positions):
+//     RoPE + RMSNorm of the group's q heads (each wavefront its heads, recomputed by every
+//     workgroup) and, in the workgroup whose segment holds the position, of this token's k, with
+//     the bf16 KV store at the position; then one key per lane, scored for each q head of the
+//     wavefront in dot_bf16's order; the scores and each segment's maximum go to global memory.
+//   k_attn_out, one 512-thread workgroup per (query head, 64 output dimensions): the maximum of
+//     the segment maxima (order-free), e_j = expf(s_j - max), their sum in position order by the
+//     8-wavefront exact segmented sum (rows longer than kSplitWin in chunks, each later chunk
+//     taking the running sum as its first addend, which continues the same sequential sum),
+//     p_j = e_j * (1 / sum), then o[d] += p_j * V_j[d] in position order: wavefronts 1-7 form the
+//     products p_j * V_j[d] (rounded to fp32, as the reference's multiply) into [d][j] tiles of
+//     128 positions, and wavefront 0 (one lane per dimension) adds them in position order, four
+//     per LDS read, with only the dependent adds on its critical path.
+
+namespace {
+
+constexpr int kSpThreads = 512;                // k_attn_scores: eight wavefronts
+constexpr int kSpGridX = 128;                  // score workgroups per KV head (more segments loop)
+constexpr int kSoThreads = 512;                // k_attn_out
+constexpr int kSoTile = 256;                   // positions per product tile
+constexpr int kSoPad = kSoTile + 4;            // [d][j] row length (16-byte rows, no bank conflicts)
+constexpr int kSoPieces = kSoTile * 8;         // (position, 8 dimensions) pieces of a tile
+constexpr int kSoProd = kSoThreads - 64;       // producer threads (wavefronts 1-7)
+constexpr int kSoPPT = (kSoPieces + kSoProd - 1) / kSoProd;  // pieces per producer thread
+static_assert(kSplitWin % kSoTile == 0 && kSplitWin == 8 * kSoThreads, "windows of whole tiles, 8 per thread");
+static_assert(kSoProd % 64 == 0 && kSoTile % 32 == 0, "whole rows per wavefront load; swizzle within 32 positions");
+
+struct SoSmem {
+    alignas(16) float pj[kSplitWin];  // p_j of the current window
+    union {
+        HyExactLdsT<kA1Waves> exs;                    // the softmax sum
+        alignas(16) float prod[2][64][kSoPad];        // then two product tiles [d][j]
+    };
+    float red[kSoThreads / 64];
+    uint64_t etab[32];  // expf table
+};
+
+}  // namespace
+
+template <int HD>
+__global__ __launch_bounds__(kSpThreads) void k_attn_scores(Attn1Args a) {
+    constexpr int RPL = HD / 64;
+    constexpr int HW = kSpThreads / 128;  // wavefronts per half of the workgroup (head slots)
+    __shared__ alignas(16) float qn[kSplitMaxGroup][HD];
+    __shared__ alignas(16) float scr[kSpThreads / 64][HD];
+    __shared__ alignas(16) uint16_t kb[HD];
+    hy_sgpr_pin(a.q), hy_sgpr_pin(a.k), hy_sgpr_pin(a.v), hy_sgpr_pin(a.kc), hy_sgpr_pin(a.vc),
+        hy_sgpr_pin(a.q_norm), hy_sgpr_pin(a.k_norm), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin),
+        hy_sgpr_pin(a.pos_dev), hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.pos0), hy_sgpr_pin(a.heads),
+        hy_sgpr_pin(a.kv_heads), hy_sgpr_pin(a.rope_half), hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.eps), hy_sgpr_pin(a.sc),
+        hy_sgpr_pin(a.segmax), hy_sgpr_pin(a.sc_stride), hy_sgpr_pin(a.seg_stride);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = blockIdx.y, group = a.heads / a.kv_heads;
+    const int half = a.rope_half;
+    const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
+    // wavefront w scores the group's q heads w % HW, w % HW + HW, ... for the half w / HW of the
+    // segment's positions, one key per pair of lanes; the first half's wavefronts RoPE and norm
+    // those heads' q rows, the last wavefront this token's k (in the position's workgroup)
+    const int slot = wave % HW, sh = wave / HW;
+    const bool hasq = slot < group;
+    const bool qw = hasq && sh == 0;
+    const bool kw = wave == kSpThreads / 64 - 1;
+    const int par = lane & 1;
+
+    // 0. q rows and norm weights, this token's k and v rows, then the position (scalar), its RoPE
+    //    row and the first segment's key rows
+    float x[RPL], nw[RPL], kx[RPL], knw[RPL], vx[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+        const int d = lane + 64 * i;
+        if (qw) x[i] = a.q[(size_t)(g * group + slot) * HD + d], nw[i] = a.q_norm[d];
+        if (kw) kx[i] = a.k[(size_t)g * HD + d], knw[i] = a.k_norm[d], vx[i] = a.v[(size_t)g * HD + d];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    const int n = pos + 1, nseg = (n + kSplitSeg - 1) / kSplitSeg;
+    if ((int)blockIdx.x >= nseg) return;  // uniform: no work for this workgroup at this position
+    const bool own = (nseg - 1) % (int)gridDim.x == (int)blockIdx.x;  // it scores the segment holding pos
+    float rc[RPL], rs[RPL];
+    {
+        const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
+        const float* sn = a.rope_cur ? a.rope_cur + half : a.rope_sin + (size_t)pos * half;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int d = lane + 64 * i, t = d < half ? d : (d < 2 * half ? d - half : 0);
+            rc[i] = cs[t];
+            rs[i] = sn[t];
+        }
+    }
+    a1_fence();
+    const int koff = sh * (kSplitSeg / 2) + (lane >> 1);  // this lane's key within a segment
+    uint4 kr[HD / 8];
+    {
+        const int r = blockIdx.x * kSplitSeg + koff;
+        if (hasq && r < pos) a1_load_key<HD>(kr, K, r);
+    }
+    a1_fence();
+
+    // 1. RoPE + RMSNorm (src/model.c:836-841): this token's k (bf16, stored at the position with
+    //    its v, src/model.c:842-847) and the group's q heads
+    if (own && kw) {
+        float y[RPL];
+        rope_norm_wave<HD>(kx, scr[wave], rc, rs, half, knw, a.eps, lane, y);
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const int d = lane + 64 * i;
+            const uint16_t kq = hy_to_bf16(y[i]);
+            kb[d] = kq;
+            const size_t off = ((size_t)g * a.ctx + pos) * HD + d;
+            a.kc[off] = kq;
+            a.vc[off] = hy_to_bf16(vx[i]);
+        }
+    }
+    if (qw) {
+        for (int hq = slot; hq < group; hq += HW) {
+            if (hq != slot) {
+#pragma unroll
+                for (int i = 0; i < RPL; i++) x[i] = a.q[(size_t)(g * group + hq) * HD + lane + 64 * i];
+            }
+            float y[RPL];
+            rope_norm_wave<HD>(x, scr[wave], rc, rs, half, nw, a.eps, lane, y);
+#pragma unroll
+            for (int i = 0; i < RPL; i++) qn[hq][lane + 64 * i] = y[i];
+        }
+    }
+    hy_lds_barrier();  // LDS only: the key rows stay in flight
+
+    // 2. scores s_j = dot_bf16(q, K_j) * (1/sqrtf(hd)) (src/model.c:778-782) of this workgroup's
+    //    segments, key pos from this token's bf16 k; the maximum of each kSplitMaxSeg positions
+    //    (order-free)
+    if (!hasq) return;
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int sgm = blockIdx.x; sgm < nseg; sgm += gridDim.x) {
+        const int r = sgm * kSplitSeg + koff;
+        if (sgm != (int)blockIdx.x && r < pos) a1_load_key<HD>(kr, K, r);
+        if (r == pos) a1_load_key<HD>(kr, kb, 0);
+        for (int hq = slot; hq < group; hq += HW) {
+            const float s = a1_score_pair<HD>(kr, qn[hq], par, scale);
+            const int hh = g * group + hq;
+            if (r < n && par == 0) a.sc[(size_t)hh * a.sc_stride + r] = s;
+            const float m = hy_wave_max(r < n ? s : -__builtin_inff());
+            if (lane == 0) a.segmax[(size_t)hh * a.seg_stride + sgm * 2 + sh] = m;
+        }
+    }
+}
+
+namespace {
+
+// Product tile layout: buf[d][c], d the dimension (of this workgroup's 64), c a swizzled position:
+// position j of the tile sits at column j ^ (4 * (d / 8)). The XOR moves whole groups of four
+// positions within aligned groups of 32, so the chain's 16-byte reads of four consecutive
+// positions stay contiguous, and the producers' stores of one instruction (eight positions times
+// eight 8-dimension groups) spread over all LDS banks.
+
+// V pieces of the tile at t0 for producer thread pt: piece q = pt + kSoProd k is position
+// t0 + q / 8, dimensions 8 (q % 8) .. + 8 of this workgroup's 64 (V is offset to them), so that
+// eight lanes read one row's 128 contiguous bytes; rows clamped inside the cache (pieces past the
+// row are never added). Every load is issued, also for pieces past the tile's (q clamped, the
+// value unused): with a conditional load the compiler cannot count the loads in flight and waits
+// for all of them.
+template <int HD>
+__device__ __forceinline__ void so_load_v(uint4 (&v)[kSoPPT], const uint16_t* V, int t0, int pt, int cap) {
+#pragma unroll
+    for (int k = 0; k < kSoPPT; k++) {
+        const int q = min(pt + kSoProd * k, kSoPieces - 1);
+        v[k] = *reinterpret_cast<const uint4*>(V + (size_t)min(t0 + q / 8, cap) * HD + 8 * (q % 8));
+    }
+}
+
+// The products p_j * V_j[d] of a tile (rounded to fp32, axpy_bf16's multiply) into buf.
+__device__ __forceinline__ void so_products(const uint4 (&v)[kSoPPT], float (*buf)[kSoPad], const float* pj, int pt) {
+#pragma unroll
+    for (int k = 0; k < kSoPPT; k++) {
+        const int q = pt + kSoProd * k;
+        if (q < kSoPieces) {
+            const int j = q / 8, dg = q % 8;
+            const float p = pj[j];
+            float f[8];
+            bf16x8f(v[k], f);
+            const int c = j ^ (4 * dg);  // the column of position j in rows 8 dg .. 8 dg + 7
+#pragma unroll
+            for (int i = 0; i < 8; i++) buf[8 * dg + i][c] = p * f[i];
+        }
+    }
+}
+
+// o += the products of positions 0 .. cnt - 1 of lane d's row, one add at a time in position
+// order. Reads run 16 positions ahead of the adds; scheduling barriers keep them there. A partial
+// tile adds +0 past cnt, which leaves o unchanged (o is never -0: it starts at +0, and a sum of
+// nonzero addends that cancels rounds to +0).
+__device__ __forceinline__ void so_chain(const float* row, int d, int cnt, float& o) {
+    const int sw = 4 * (d >> 3);
+    auto ld = [&](float4 (&x)[4], int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) x[k] = *reinterpret_cast<const float4*>(row + ((16 * c + 4 * k) ^ sw));
+    };
+    auto add = [&](const float4 (&x)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            o += x[k].x;
+            o += x[k].y;
+            o += x[k].z;
+            o += x[k].w;
+        }
+    };
+    constexpr int C = kSoTile / 16;
+    if (cnt == kSoTile) {
+        float4 A[4], B[4];
+        ld(A, 0);
+        for (int c = 0; c < C; c += 2) {  // no exit inside the body: the reads stay ahead
+            ld(B, c + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            add(A);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(A, min(c + 2, C - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            add(B);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        for (int c = 0; 16 * c < cnt; c++) {
+            float4 A[4];
+            ld(A, c);
+            const float f[16] = {A[0].x, A[0].y, A[0].z, A[0].w, A[1].x, A[1].y, A[1].z, A[1].w,
+                                 A[2].x, A[2].y, A[2].z, A[2].w, A[3].x, A[3].y, A[3].z, A[3].w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) o += 16 * c + i < cnt ? f[i] : 0.f;
+        }
+    }
+}
+
+}  // namespace
+
+template <int HD>
+__global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
+    constexpr int PARTS = HD / 64;
+    constexpr int NW = kSoThreads / 64;
+    __shared__ SoSmem S;
+    hy_sgpr_pin(a.vc), hy_sgpr_pin(a.pos_dev), hy_sgpr_pin(a.pos0), hy_sgpr_pin(a.ao), hy_sgpr_pin(a.heads),
+        hy_sgpr_pin(a.kv_heads), hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.sc), hy_sgpr_pin(a.segmax),
+        hy_sgpr_pin(a.sc_stride), hy_sgpr_pin(a.seg_stride);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = blockIdx.x / PARTS, part = blockIdx.x % PARTS;
+    const int g = h / (a.heads / a.kv_heads);
+    const uint16_t* V = a.vc + (size_t)g * a.ctx * HD + 64 * part;
+    const bool prd = wave >= 1;
+    const int pt = tid - 64;  // producer index
+    const int cap = a.ctx - 1;
+    float* sc = a.sc + (size_t)h * a.sc_stride;
+
+    // 0. loads that do not wait for the position, oldest first (their waits then leave the
+    //    younger ones in flight): this thread's eight scores and one segment maximum (masked by
+    //    the position below), then the producers' V pieces of the first three tiles
+    const int e0 = 8 * tid;
+    const uint64_t etv = tid < 32 ? hy_exp_tab_entry(tid) : 0;  // expf table entry, into LDS before the max
+    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
+    if (e0 < a.sc_stride) {
+        s0 = *reinterpret_cast<const float4*>(sc + e0);
+        s1 = *reinterpret_cast<const float4*>(sc + e0 + 4);
+    }
+    const float m0 = tid < a.seg_stride ? a.segmax[(size_t)h * a.seg_stride + tid] : -__builtin_inff();
+    uint4 va[kSoPPT], vb[kSoPPT], vc[kSoPPT];
+    if (prd) {
+        so_load_v<HD>(va, V, 0, pt, cap);
+        so_load_v<HD>(vb, V, kSoTile, pt, cap);
+        so_load_v<HD>(vc, V, 2 * kSoTile, pt, cap);
+    }
+    a1_fence();
+    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    const int n = pos + 1, nseg = (n + kSplitMaxSeg - 1) / kSplitMaxSeg;  // segment maxima in use
+
+    // 1. max over the segment maxima (src/model.c:781-782; order-free)
+    float m = tid < nseg ? m0 : -__builtin_inff();
+    for (int i = tid + kSoThreads; i < nseg; i += kSoThreads) m = fmaxf(m, a.segmax[(size_t)h * a.seg_stride + i]);
+    m = hy_wave_max(m);
+    if (lane == 0) S.red[wave] = m;
+    if (tid < 32) S.etab[tid] = etv;
+    hy_lds_barrier();
+    float mx = S.red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) mx = fmaxf(mx, S.red[w]);
+
+    // 2. e_j = expf(s_j - max) and their sum in position order (src/model.c:784-785); thread t
+    //    holds positions 8t .. 8t + 7 of a chunk
+    const bool one = n <= kSplitWin;
+    float e[8];
+    float sum;
+    if (one) {
+        if (e0 < n) {
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? hy_expf_tab(sv[i] - mx, S.etab) : 0.f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) e[i] = 0.f;
+        }
+        sum = hy_block_exact_sum8<NW, false>(e, S.exs, wave, lane);
+    } else {
+        // chunks of kSplitWin addends; a later chunk's first addend is the running sum, so the
+        // chunk continues the one sequential sum. e_j goes back over s_j for the windows below.
+        float carry = 0.f;
+        for (int base = 0, c = 0; base < n; c++) {
+            const int off = c ? 1 : 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int idx = 8 * tid + i, j = base + idx - off;
+                if (off && idx == 0) {
+                    e[i] = carry;
+                } else if (j < n) {
+                    e[i] = hy_expf_tab(sc[j] - mx, S.etab);
+                    sc[j] = e[i];
+                } else {
+                    e[i] = 0.f;
+                }
+            }
+            carry = hy_block_exact_sum8<NW, false>(e, S.exs, wave, lane);
+            __syncthreads();  // the sum's LDS is written again; the e_j stores are seen below
+            base += kSplitWin - off;
+        }
+        sum = carry;
+    }
+    const float inv = 1.0f / sum;
+
+    // 3. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16), p_j = e_j * inv. p_j goes
+    //    to LDS a window of kSplitWin positions at a time (a barrier after each fill), then one
+    //    barrier per tile: before barrier t the producers have formed tile t into buffer t % 2,
+    //    after it the chain adds tile t (tile t - 1's buffer was read before barrier t, when the
+    //    producers fill it with tile t + 1).
+    constexpr int WT = kSplitWin / kSoTile;  // tiles per window
+    const int tiles = (n + kSoTile - 1) / kSoTile;
+    if (one) {
+        if (e0 < n) {
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) p[i] = e[i] * inv;
+            *reinterpret_cast<float4*>(S.pj + e0) = make_float4(p[0], p[1], p[2], p[3]);
+            *reinterpret_cast<float4*>(S.pj + e0 + 4) = make_float4(p[4], p[5], p[6], p[7]);
+        }
+    }
+    float o = 0.f;
+    if (!prd) {
+        __builtin_amdgcn_s_setprio(3);  // the chain is the critical path: its adds issue first
+        const float* row = &S.prod[0][lane][0];
+        for (int t = 0; t < tiles; t++) {
+            if (t % WT == 0) hy_lds_barrier();  // the window's p_j
+            hy_lds_barrier();
+            so_chain(row + (t & 1) * 64 * kSoPad, lane, min(kSoTile, n - t * kSoTile), o);
+        }
+        a.ao[(size_t)h * HD + 64 * part + lane] = o;
+    } else {
+        // one step per tile, unrolled by three over three register sets of V pieces, each
+        // refilled three tiles ahead: every load is issued a full three tiles before its use and
+        // no register copy waits on a recent load. Loads past the row read clamped rows.
+        auto step = [&](uint4 (&v)[kSoPPT], int t) __attribute__((always_inline)) {
+            if (t < tiles) {
+                if (t % WT == 0) {
+                    if (!one) {
+                        const int w0 = t * kSoTile, wn = min(kSplitWin, n - w0);
+                        for (int j = pt; j < wn; j += kSoProd) S.pj[j] = sc[w0 + j] * inv;
+                    }
+                    hy_lds_barrier();
+                }
+                so_products(v, S.prod[t & 1], S.pj + (t % WT) * kSoTile, pt);
+                hy_lds_barrier();
+            }
+            so_load_v<HD>(v, V, (t + 3) * kSoTile, pt, cap);
+        };
+        for (int t = 0; t < tiles; t += 3) {
+            step(va, t);
+            step(vb, t + 1);
+            step(vc, t + 2);
+        }
+    }
+}
+
+hipError_t launch_attn_split(const Attn1Args& a, hipStream_t s) {
+    if (a.heads % a.kv_heads || a.heads / a.kv_heads > kSplitMaxGroup || 2 * a.rope_half > a.hdim || !a.sc ||
+        !a.segmax || a.sc_stride < split_sc_stride(a.ctx) || a.seg_stride < split_seg_stride(a.ctx))
+        return hipErrorNotSupported;
+    const dim3 g1(min(split_seg_stride(a.ctx), kSpGridX), a.kv_heads);
+    const int g2 = a.heads * (a.hdim / 64);
+    switch (a.hdim) {
+    case 64:
+        k_attn_scores<64><<<g1, kSpThreads, 0, s>>>(a);
+        k_attn_out<64><<<g2, kSoThreads, 0, s>>>(a);
+        break;
+    case 128:
+        k_attn_scores<128><<<g1, kSpThreads, 0, s>>>(a);
+        k_attn_out<128><<<g2, kSoThreads, 0, s>>>(a);
+        break;
+    case 256:
+        k_attn_scores<256><<<g1, kSpThreads, 0, s>>>(a);
+        k_attn_out<256><<<g2, kSoThreads, 0, s>>>(a);
+        break;
     default: return hipErrorNotSupported;
     }
     return hipGetLastError();

@@ -60,6 +60,9 @@ struct DW {  // hy_dweight
 // hidden rows of the chunk at kInH.
 constexpr size_t kInH = 2048;
 
+// Single-token forwards at positions from here on use the split attention (launch_attn_split).
+constexpr int kSplitFromDefault = 448;
+
 struct Fused {
     int n_layer = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, hdim = 0, qdim = 0, kvdim = 0, ctx = 0,
         rope_half = 0;
@@ -83,8 +86,13 @@ struct Fused {
     int gen_steps = 0;   // steps enqueued so far
     int gen_prompt = 0, gen_vocab = 0;
     MvWeight gen_embd{};  // embedding of the current device loop
-    hipGraphExec_t g_fwd = nullptr, g_step = nullptr;
-    std::vector<const void*> sig_fwd, sig_step;
+    // attention scratch of the split form (launch_attn_split): scores [heads][sc_stride] and
+    // segment maxima [heads][seg_stride]
+    float *sc = nullptr, *segmax = nullptr;
+    // captured single-token graphs, [0] with the one-kernel attention (k_attn1), [1] with the
+    // split form; a forward at position p replays [split_at(p)]
+    hipGraphExec_t g_fwd[2] = {nullptr, nullptr}, g_step[2] = {nullptr, nullptr};
+    std::vector<const void*> sig_fwd[2], sig_step;
     float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
         const size_t per = 2 * (size_t)hidden + 2 * (size_t)hdim;
         float* base = norms + per * li;
@@ -104,7 +112,14 @@ struct Ctx {
     Fused* f = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     uint8_t* scratch = nullptr;  // this device's address of `scratch` (hymt2_hip_matmul_static), or null
+    int split_from = kSplitFromDefault;  // single-token attention at positions >= this: split form
 };
+
+// Whether the single-token forward at position pos uses the split attention: long rows, and
+// every shape the one-kernel form (k_attn1: head dim 64 or 128, ctx <= kA1MaxCtx) does not take.
+static bool split_at(const Ctx* c, const Fused* f, int pos) {
+    return pos >= c->split_from || (f->hdim != 64 && f->hdim != 128) || f->ctx > kA1MaxCtx;
+}
 
 // Device staging of hymt2_hip_matmul_static, the per-op entry point that allocates nothing: the
 // Q8_K activation blocks, then the outputs that go back by copy. Every GPU the library runs on
@@ -550,10 +565,12 @@ static bool hip_matmul(void* impl, hy_dweight* const* ws, float* const* outs, in
 // Drops the captured graphs. A device loop in progress replays g_step, so it ends here too
 // (gen_steps then reports that no loop has begun).
 static void free_graphs(Fused* f) {
-    if (f->g_fwd) (void)hipGraphExecDestroy(f->g_fwd);
-    if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
-    f->g_fwd = f->g_step = nullptr;
-    f->sig_fwd.clear();
+    for (int v = 0; v < 2; v++) {
+        if (f->g_fwd[v]) (void)hipGraphExecDestroy(f->g_fwd[v]);
+        if (f->g_step[v]) (void)hipGraphExecDestroy(f->g_step[v]);
+        f->g_fwd[v] = f->g_step[v] = nullptr;
+        f->sig_fwd[v].clear();
+    }
     f->sig_step.clear();
     f->gen_total = 0;
 }
@@ -562,7 +579,7 @@ static void free_fused(Fused* f) {
     if (!f) return;
     free_graphs(f);
     void* dev[] = {f->in_dev, f->q, f->k, f->v, f->ao, f->g, f->u, f->logits, f->act_h, f->act_q, f->act_f,
-                   f->rope_c, f->rope_s, f->out_norm, f->norms, f->kc, f->vc, f->key, f->ids};
+                   f->rope_c, f->rope_s, f->out_norm, f->norms, f->kc, f->vc, f->key, f->ids, f->sc, f->segmax};
     for (void* p : dev)
         if (p) (void)hipFree(p);
     if (f->in_host) (void)hipHostFree(f->in_host);
@@ -633,7 +650,9 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
          dalloc(c, &f->rope_s, (size_t)a->ctx * a->rope_half * 4 + 4) && dalloc(c, &f->out_norm, H * 4) &&
          dalloc(c, &f->norms, (size_t)a->n_layer * (2 * H + 2 * a->hdim) * 4) &&
          dalloc(c, &f->kc, (size_t)a->n_layer * a->ctx * KV * 2) &&
-         dalloc(c, &f->vc, (size_t)a->n_layer * a->ctx * KV * 2) && dalloc(c, &f->key, 64);
+         dalloc(c, &f->vc, (size_t)a->n_layer * a->ctx * KV * 2) && dalloc(c, &f->key, 64) &&
+         dalloc(c, &f->sc, (size_t)a->heads * split_sc_stride(a->ctx) * 4) &&
+         dalloc(c, &f->segmax, (size_t)a->heads * split_seg_stride(a->ctx) * 4);
     if (!ok) {
         free_fused(f);
         return false;
@@ -677,7 +696,7 @@ static const DW* dw(hy_dweight* p) { return reinterpret_cast<const DW*>(p); }
 // matvec with the RMSNorm prologue, SwiGLU and Q8_K epilogue] -> [down matvec + residual].
 // nt > 1 quantizes each token's activations once into global memory and runs the general
 // RoPE / attention kernels and the same matvec kernels over all tokens.
-static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, const int* pos_dev) {
+static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, const int* pos_dev, bool split) {
     Fused* f = c->f;
     const int H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
     for (int li = 0; li < f->n_layer; li++) {
@@ -705,9 +724,10 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             HIPCHK(c, launch_rmsnorm_q8k(f->d_h, attn_norm, f->eps, H, nt, nullptr, f->act_h, c->s));
             o1.act = f->act_h;
         }
-        // single token: one workgroup per head (k_attn1), fp32 output quantized by the o matvec;
-        // else the 256-output-block attention kernel, else the general path
-        const bool head_attn = nt == 1 && (f->hdim == 64 || f->hdim == 128) && f->ctx <= kA1MaxCtx;
+        // single token: one workgroup per head (k_attn1) or, for long rows, the split form
+        // (split_at), both with an fp32 output row that the o matvec quantizes; chunks: the
+        // RoPE / KV-store kernel, then the chunk attention
+        const bool head_attn = nt == 1;
         Attn1Args aa{};
         if (head_attn) {
             aa.q = f->q;
@@ -729,34 +749,14 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
             aa.rope_half = f->rope_half;
             aa.ctx = f->ctx;
             aa.eps = f->eps;
+            aa.sc = f->sc;
+            aa.segmax = f->segmax;
+            aa.sc_stride = split_sc_stride(f->ctx);
+            aa.seg_stride = split_seg_stride(f->ctx);
         }
         if (!(nt == 1 ? run_mv1(c, qkv, 3, false, o1) : run_multi(c, qkv, 3, false, nt, o1))) return false;
-        const bool fused_attn = nt == 1 && 256 % f->hdim == 0 && (f->heads / f->kv_heads) % (256 / f->hdim) == 0 &&
-                                attn_decode_lds(f->hdim, f->ctx) <= 96 * 1024;
         if (head_attn) {
-            HIPCHK(c, launch_attn1(aa, c->s));
-        } else if (fused_attn) {
-            AttnDecodeArgs ad{};
-            ad.q = f->q;
-            ad.k = f->k;
-            ad.v = f->v;
-            ad.kc = kc;
-            ad.vc = vc;
-            ad.q_norm = f->norm_ptr(li, 2);
-            ad.k_norm = f->norm_ptr(li, 3);
-            ad.rope_cos = f->rope_c;
-            ad.rope_sin = f->rope_s;
-            ad.pos_dev = pos_dev;
-            ad.pos0 = pos0;
-            ad.act_out = f->act_q;
-            ad.ao_out = nullptr;
-            ad.heads = f->heads;
-            ad.kv_heads = f->kv_heads;
-            ad.hdim = f->hdim;
-            ad.rope_half = f->rope_half;
-            ad.ctx = f->ctx;
-            ad.eps = f->eps;
-            HIPCHK(c, launch_attn_decode(ad, c->s));
+            HIPCHK(c, split ? launch_attn_split(aa, c->s) : launch_attn1(aa, c->s));
         } else {
             AttnArgs at{};
             at.q = f->q;
@@ -909,21 +909,22 @@ static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
         if (logits && !ensure_logits(c, f, dw(a->outw)->mw.n)) return false;
         std::vector<const void*> sig = weight_sig(a);
         sig.push_back(reinterpret_cast<const void*>((uintptr_t)logits));
-        if (!f->g_fwd || f->sig_fwd != sig) {
-            if (f->g_fwd) (void)hipGraphExecDestroy(f->g_fwd);
-            f->g_fwd = nullptr;
-            if (!capture(c, &f->g_fwd, [&] {
-                    return enqueue_layers(c, a, 1, 0, f->d_pos) && (!logits || enqueue_head(c, a, 1, false, 0));
+        const int v = split_at(c, f, a->pos0) ? 1 : 0;
+        if (!f->g_fwd[v] || f->sig_fwd[v] != sig) {
+            if (f->g_fwd[v]) (void)hipGraphExecDestroy(f->g_fwd[v]);
+            f->g_fwd[v] = nullptr;
+            if (!capture(c, &f->g_fwd[v], [&] {
+                    return enqueue_layers(c, a, 1, 0, f->d_pos, v == 1) && (!logits || enqueue_head(c, a, 1, false, 0));
                 })) {
                 c->broken = true;
                 return false;
             }
-            f->sig_fwd = sig;
+            f->sig_fwd[v] = sig;
         }
-        HIPCHK(c, hipGraphLaunch(f->g_fwd, c->s));
+        HIPCHK(c, hipGraphLaunch(f->g_fwd[v], c->s));
     } else {
         HIPCHK(c, hipMemcpyAsync(f->d_h, f->in_host + kInH, hbytes, hipMemcpyHostToDevice, c->s));
-        if (!enqueue_layers(c, a, nt, a->pos0, nullptr) || (logits && !enqueue_head(c, a, nt, false, 0))) {
+        if (!enqueue_layers(c, a, nt, a->pos0, nullptr, false) || (logits && !enqueue_head(c, a, nt, false, 0))) {
             c->broken = true;
             return false;
         }
@@ -1060,6 +1061,14 @@ int hymt2_hip_selftest_expf(void* impl, const float* src, float* dst, int n) {
     return launch_selftest(src, dst, n, 1, c->s) == hipSuccess ? 0 : -2;
 }
 
+int hymt2_hip_attn_split_from(void* impl, int from) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c) return -1;
+    c->split_from = from < 0 ? kSplitFromDefault : from;
+    if (c->f) free_graphs(c->f);
+    return 0;
+}
+
 int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out,
                         const int* prompt, int n_prompt, int n_total) {
     Ctx* c = static_cast<Ctx*>(impl);
@@ -1096,17 +1105,26 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     sig.push_back(reinterpret_cast<const void*>((intptr_t)vocab_out));
     sig.push_back(reinterpret_cast<const void*>((intptr_t)n_prompt));
     sig.push_back(reinterpret_cast<const void*>((intptr_t)n_total));
-    if (!f->g_step || f->sig_step != sig) {
-        if (f->g_step) (void)hipGraphExecDestroy(f->g_step);
-        f->g_step = nullptr;
+    // the step graphs this loop's positions 0 .. n_total - 2 need (a step at position p replays
+    // g_step[split_at(p)])
+    const bool need[2] = {!split_at(c, f, 0), split_at(c, f, n_total - 2)};
+    if (f->sig_step != sig || (need[0] && !f->g_step[0]) || (need[1] && !f->g_step[1])) {
+        for (int v = 0; v < 2; v++) {
+            if (f->g_step[v]) (void)hipGraphExecDestroy(f->g_step[v]);
+            f->g_step[v] = nullptr;
+        }
+        f->sig_step.clear();
         FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e->mw, f->d_h, f->hidden, n_total,
                       f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
-        if (!capture(c, &f->g_step, [&] {
-                if (!enqueue_layers(c, shape, 1, 0, f->d_pos) || !enqueue_head(c, shape, 1, true, vocab_out))
-                    return false;
-                return launch_finish(fa, c->s) == hipSuccess;
-            }))
-            return -7;
+        for (int v = 0; v < 2; v++) {
+            if (!need[v]) continue;
+            if (!capture(c, &f->g_step[v], [&] {
+                    if (!enqueue_layers(c, shape, 1, 0, f->d_pos, v == 1) || !enqueue_head(c, shape, 1, true, vocab_out))
+                        return false;
+                    return launch_finish(fa, c->s) == hipSuccess;
+                }))
+                return -7;
+        }
         f->sig_step = sig;
     }
     // start state: ids[0..n_prompt) = prompt, pos = 0, key = 0, h = embedding of ids[0]
@@ -1146,7 +1164,7 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     for (int i = 0; i < np; i += chunk) {
         const int nt = std::min(chunk, np - i);
         if (launch_embed_rows(f->ids, i, nt, f->gen_embd, f->d_h, f->hidden, c->s) != hipSuccess ||
-            !enqueue_layers(c, shape, nt, i, nullptr) ||
+            !enqueue_layers(c, shape, nt, i, nullptr, nt == 1 && split_at(c, f, i)) ||
             (i + nt == np && !enqueue_head(c, shape, nt, true, f->gen_vocab))) {
             c->broken = true;
             return -3;
@@ -1174,7 +1192,7 @@ int hymt2_hip_gen_steps(void* impl, int n) {
         return -2;
     }
     for (int i = 0; i < n; i++)
-        if (hipGraphLaunch(f->g_step, c->s) != hipSuccess) {
+        if (hipGraphLaunch(f->g_step[split_at(c, f, f->gen_steps + i) ? 1 : 0], c->s) != hipSuccess) {
             set_err(c, "gen_steps: hipGraphLaunch failed");
             c->broken = true;
             return -3;

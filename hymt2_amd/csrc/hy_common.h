@@ -69,6 +69,14 @@ __device__ __forceinline__ void hy_sgpr_pin(const T& v) {
     asm volatile("" ::"s"(v));
 }
 
+// Entry i (i < 32) of hy_expf's table, for a kernel that keeps a copy in LDS (hy_expf_tab): the
+// load is issued at kernel entry and the value stored to LDS before a barrier that precedes the
+// first expf, so no lookup waits on global memory.
+__device__ __forceinline__ uint64_t hy_exp_tab_entry(int i) {
+    constexpr uint64_t T[32] = {HY_EXP2F_TABLE};
+    return T[i & 31];
+}
+
 __device__ __forceinline__ void hy_lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }

@@ -26,16 +26,20 @@
 // Limited, SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception; the same routine
 // ships in glibc as sysdeps/ieee754/flt-32/e_expf.c and e_exp2f_data.c (LGPL-2.1-or-later,
 // contributed by Arm). The code here is written for this file; only the numbers must be equal.
-HY_HD inline float hy_expf(float x) {
-    constexpr uint64_t T[32] = {
-        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+// The 32 table entries (2^(i/32) correctly rounded to double, minus i << 47).
+#define HY_EXP2F_TABLE \
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull, \
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, \
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull, \
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull, \
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull, \
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull, \
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull
+
+// expf with the table T[32] supplied by the caller (GPU kernels pass a copy in LDS, so that a
+// lookup is an LDS read rather than a load from global memory on the critical path).
+HY_HD inline float hy_expf_tab(float x, const uint64_t* T) {
     constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
     constexpr double kShift = 0x1.8p+52;
     constexpr double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -62,5 +66,10 @@ HY_HD inline float hy_expf(float x) {
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+HY_HD inline float hy_expf(float x) {
+    constexpr uint64_t T[32] = {HY_EXP2F_TABLE};
+    return hy_expf_tab(x, T);
 }
 

@@ -147,25 +147,6 @@ hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s);
 // Q8_K blocks); otherwise the caller quantizes ao itself.
 bool attention_quantizes(const AttnArgs& a);
 
-struct AttnDecodeArgs {
-    const float* q;        // [qdim] fp32 (before RoPE)
-    const float* k;        // [kvdim]
-    const float* v;        // [kvdim]
-    uint16_t* kc;          // layer base of K cache [kv_heads][ctx][hdim]
-    uint16_t* vc;
-    const float* q_norm;
-    const float* k_norm;
-    const float* rope_cos;
-    const float* rope_sin;
-    const int* pos_dev;    // optional: position read from device memory (graph replay)
-    int pos0;
-    HyQ8K* act_out;        // [qdim / 256] Q8_K blocks of the attention output
-    float* ao_out;         // optional fp32 copy of the attention output [qdim]
-    int heads, kv_heads, hdim, rope_half, ctx;
-    float eps;
-};
-hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s);
-size_t attn_decode_lds(int hdim, int ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 // Single-token attention, one workgroup per query head (k_attn1, hy_attn_decode.hip): RoPE
@@ -188,8 +169,24 @@ struct Attn1Args {
     float* ao;             // [qdim] attention output
     int heads, kv_heads, hdim, rope_half, ctx;
     float eps;
+    // split form only (launch_attn_split): scores and per-segment maxima of each query head
+    float* sc;             // [heads][sc_stride] fp32 scores, then expf(s - max) for rows > kSplitWin
+    float* segmax;         // [heads][seg_stride] maximum score of each kSplitMaxSeg positions
+    int sc_stride, seg_stride;
 };
 hipError_t launch_attn1(const Attn1Args& a, hipStream_t s);
+
+// Split single-token attention for long rows (hy_attn_decode.hip): k_attn_scores spreads the
+// scores of each KV head's query heads over workgroups of kSplitSeg positions (with RoPE, the
+// q/k norms and the KV store), then k_attn_out (one workgroup per query head and 64 output
+// dimensions) forms the softmax and the output. Any context length; bit-identical to k_attn1.
+constexpr int kSplitSeg = 64;     // positions per score workgroup segment (a key per pair of lanes)
+constexpr int kSplitMaxSeg = 32;  // positions per segment maximum (one wavefront's keys)
+constexpr int kSplitWin = 4096;   // positions of p_j held in LDS at a time
+constexpr int kSplitMaxGroup = 16;
+inline int split_sc_stride(int ctx) { return (ctx + kSplitSeg - 1) / kSplitSeg * kSplitSeg; }
+inline int split_seg_stride(int ctx) { return (ctx + kSplitSeg - 1) / kSplitSeg * (kSplitSeg / kSplitMaxSeg); }
+hipError_t launch_attn_split(const Attn1Args& a, hipStream_t s);
 
 struct HeadArgs {
     MvWeight W;            // F16, F32 or Q8_0 row tiles

@@ -823,207 +823,6 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Single-token attention block: one workgroup per 256 query dims (256/HD heads sharing one KV
-// head). Does RoPE + per-head RMSNorm of its q heads and of the KV head's k, the bf16 rounding
-// of k and v (stored at `pos` by the group's first workgroup; the others use the same bits from
-// LDS for that position), causal attention over positions 0..pos with the reference's exact
-// operation order, and quantizes its 256 outputs to one Q8_K block for the o-projection.
-constexpr int kAttnThreads = 512;
-constexpr int kVTile = 64;
-
-template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnDecodeArgs a) {
-    constexpr int HPW = 256 / HD;     // heads per workgroup
-    constexpr int DPL = HD / 64;      // output dims per lane
-    constexpr int NW = kAttnThreads / 64;
-    extern __shared__ __align__(16) float sm[];
-    __shared__ __align__(16) float rows[HPW + 2][HD];   // q heads, k, v
-    __shared__ __align__(16) float sq[(HPW + 1) * HD];
-    __shared__ __align__(16) uint16_t kb[HD];
-    __shared__ __align__(16) uint16_t vb[HD];
-    __shared__ __align__(16) float ao[256];
-    __shared__ float scal[HPW + 1];
-    __shared__ float red[HPW][NW];
-    __shared__ float stat[HPW];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h0 = blockIdx.x * HPW;
-    const int group = a.heads / a.kv_heads;
-    const int kvh = h0 / group;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos0;
-    const int n = pos + 1;
-    const int half = a.rope_half;
-    const int npad = ((a.ctx + 3) & ~3);
-    float* sc = sm;                                                   // [HPW][npad]
-    uint16_t* vt = reinterpret_cast<uint16_t*>(sm + HPW * npad);      // [2][kVTile][HD]
-
-    // 1. q heads, k and v rows of this token
-    for (int i = tid; i < (HPW + 2) * HD; i += kAttnThreads) {
-        const int r = i / HD, d = i % HD;
-        rows[r][d] = r < HPW ? a.q[(size_t)(h0 + r) * HD + d]
-                             : (r == HPW ? a.k[(size_t)kvh * HD + d] : a.v[(size_t)kvh * HD + d]);
-    }
-    __syncthreads();
-    // 2. NeoX RoPE of q heads and k (src/model.c:754-765)
-    const float* cs = a.rope_cos + (size_t)pos * half;
-    const float* sn = a.rope_sin + (size_t)pos * half;
-    for (int i = tid; i < (HPW + 1) * half; i += kAttnThreads) {
-        const int r = i / half, jx = i % half;
-        const float x0 = rows[r][jx], x1 = rows[r][jx + half];
-        rows[r][jx] = x0 * cs[jx] - x1 * sn[jx];
-        rows[r][jx + half] = x0 * sn[jx] + x1 * cs[jx];
-    }
-    __syncthreads();
-    // 3. per-head RMSNorm (src/model.c:840-841): squares in parallel, one sequential sum per row
-    for (int i = tid; i < (HPW + 1) * HD; i += kAttnThreads) sq[i] = rows[i / HD][i % HD] * rows[i / HD][i % HD];
-    __syncthreads();
-    if (wave <= HPW) {
-        const float sum = hy_wave_seq_sum(sq + wave * HD, HD, lane);
-        if (lane == 0) scal[wave] = 1.0f / sqrtf(sum / (float)HD + a.eps);
-    }
-    __syncthreads();
-    for (int i = tid; i < (HPW + 1) * HD; i += kAttnThreads) {
-        const int r = i / HD, d = i % HD;
-        rows[r][d] = rows[r][d] * scal[r] * (r < HPW ? a.q_norm[d] : a.k_norm[d]);
-    }
-    __syncthreads();
-    // 4. bf16 k, v of this position (src/model.c:842-847)
-    for (int d = tid; d < HD; d += kAttnThreads) {
-        kb[d] = hy_to_bf16(rows[HPW][d]);
-        vb[d] = hy_to_bf16(rows[HPW + 1][d]);
-    }
-    __syncthreads();
-    if (h0 % group == 0) {
-        const size_t off = ((size_t)kvh * a.ctx + pos) * HD;
-        for (int d = tid; d < HD; d += kAttnThreads) {
-            a.kc[off + d] = kb[d];
-            a.vc[off + d] = vb[d];
-        }
-    }
-    // 5. scores s[r][j] = dot_bf16(q_r, K_j) * (1/sqrtf(hd)), four interleaved partial sums
-    const float scale = 1.0f / sqrtf((float)HD);
-    const uint16_t* K = a.kc + (size_t)kvh * a.ctx * HD;
-    const uint16_t* V = a.vc + (size_t)kvh * a.ctx * HD;
-    float lmax[HPW];
-#pragma unroll
-    for (int r = 0; r < HPW; r++) lmax[r] = -__builtin_inff();
-    for (int jx = tid; jx < n; jx += kAttnThreads) {
-        const uint16_t* kr = jx == pos ? kb : K + (size_t)jx * HD;
-        float acc[HPW][4];
-#pragma unroll
-        for (int r = 0; r < HPW; r++) acc[r][0] = acc[r][1] = acc[r][2] = acc[r][3] = 0.f;
-        // q stays in LDS (read next to its use): hoisting all HPW*HD values would overflow VGPRs
-#pragma unroll 2
-        for (int d = 0; d < HD; d += 8) {
-            float kf[8];
-            bf16x8(*reinterpret_cast<const uint4*>(kr + d), kf);
-#pragma unroll
-            for (int r = 0; r < HPW; r++) {
-                const float* q = rows[r] + d;
-                acc[r][0] += q[0] * kf[0];
-                acc[r][1] += q[1] * kf[1];
-                acc[r][2] += q[2] * kf[2];
-                acc[r][3] += q[3] * kf[3];
-                acc[r][0] += q[4] * kf[4];
-                acc[r][1] += q[5] * kf[5];
-                acc[r][2] += q[6] * kf[6];
-                acc[r][3] += q[7] * kf[7];
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < HPW; r++) {
-            const float s = ((acc[r][0] + acc[r][1]) + (acc[r][2] + acc[r][3])) * scale;
-            sc[r * npad + jx] = s;
-            lmax[r] = fmaxf(lmax[r], s);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < HPW; r++) {
-        const float m = hy_wave_max(lmax[r]);
-        if (lane == 0) red[r][wave] = m;
-    }
-    __syncthreads();
-    if (tid < HPW) {
-        float m = red[tid][0];
-        for (int w = 1; w < NW; w++) m = fmaxf(m, red[tid][w]);
-        stat[tid] = m;
-    }
-    __syncthreads();
-    // 6. softmax: exp (parallel), sum (sequential per head, src/model.c:785-789), normalise
-    for (int i = tid; i < HPW * n; i += kAttnThreads) {
-        const int r = i / n, jx = i % n;
-        sc[r * npad + jx] = hy_expf(sc[r * npad + jx] - stat[r]);
-    }
-    __syncthreads();
-    if (wave < HPW) {
-        const float sum = hy_wave_seq_sum(sc + wave * npad, n, lane);
-        if (lane == 0) stat[wave] = 1.0f / sum;
-    }
-    __syncthreads();
-    for (int i = tid; i < HPW * n; i += kAttnThreads) {
-        const int r = i / n, jx = i % n;
-        sc[r * npad + jx] = sc[r * npad + jx] * stat[r];
-    }
-    // 7. o[r][d] = sum_j p[r][j] * V[j][d] in position order: waves < HPW accumulate while the
-    // other waves stage the next tile of V rows into LDS
-    const int ntile = (n + kVTile - 1) / kVTile;
-    auto stage = [&](int tile, int buf) {
-        const int st = tid - HPW * 64, nst = kAttnThreads - HPW * 64;
-        uint16_t* dst = vt + (size_t)buf * kVTile * HD;
-        constexpr int per_row = HD / 8;
-        for (int i = st; i < kVTile * per_row; i += nst) {
-            const int jj = i / per_row, part = i % per_row, jx = tile * kVTile + jj;
-            uint4 val = make_uint4(0, 0, 0, 0);
-            if (jx < pos) val = *reinterpret_cast<const uint4*>(V + (size_t)jx * HD + part * 8);
-            else if (jx == pos) val = *reinterpret_cast<const uint4*>(vb + part * 8);
-            *reinterpret_cast<uint4*>(dst + jj * HD + part * 8) = val;
-        }
-    };
-    if (wave >= HPW) stage(0, 0);
-    __syncthreads();
-    float o[DPL];
-#pragma unroll
-    for (int i = 0; i < DPL; i++) o[i] = 0.f;
-    for (int tl = 0; tl < ntile; tl++) {
-        if (wave >= HPW) {
-            if (tl + 1 < ntile) stage(tl + 1, (tl + 1) & 1);
-        } else {
-            const int cnt = min(kVTile, n - tl * kVTile);
-            v_accumulate<DPL>(o, sc + wave * npad + tl * kVTile, vt + (size_t)(tl & 1) * kVTile * HD, HD,
-                              lane * DPL, cnt);
-        }
-        __syncthreads();
-    }
-    if (wave < HPW) {
-#pragma unroll
-        for (int i = 0; i < DPL; i++) ao[wave * HD + lane * DPL + i] = o[i];
-    }
-    __syncthreads();
-    if (a.ao_out)
-        for (int i = tid; i < 256; i += kAttnThreads) a.ao_out[(size_t)h0 * HD + i] = ao[i];
-    // 8. Q8_K block of this workgroup's 256 outputs (quantize_q8k, src/kernels.c:128-165)
-    if (tid < 64) q8k_quantize_wave(ao, a.act_out + blockIdx.x, tid);
-}
-
-size_t attn_decode_lds(int hdim, int ctx) {
-    const int hpw = 256 / hdim;
-    return (size_t)hpw * (((ctx + 3) & ~3)) * sizeof(float) + 2 * (size_t)kVTile * hdim * sizeof(uint16_t);
-}
-
-hipError_t launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
-    const int hpw = 256 / a.hdim;
-    if (256 % a.hdim || (a.heads / a.kv_heads) % hpw || a.heads % hpw) return hipErrorInvalidValue;
-    const size_t lds = attn_decode_lds(a.hdim, a.ctx);
-    if (lds > 96 * 1024) return hipErrorInvalidValue;
-    const int grid = a.heads / hpw;
-    switch (a.hdim) {
-    case 64: k_attn_decode<64><<<grid, kAttnThreads, lds, s>>>(a); break;
-    case 128: k_attn_decode<128><<<grid, kAttnThreads, lds, s>>>(a); break;
-    case 256: k_attn_decode<256><<<grid, kAttnThreads, lds, s>>>(a); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 // =========================================================================== LM head
 
 // Key of logit v at row idx for the greedy argmax of src/model.c:945-948, which starts from

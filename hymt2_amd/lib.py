@@ -68,6 +68,7 @@ def load():
         "hymt2_hip_head": (i, [vp, vp, vp, vp, C.c_float, vp, i, vp]),
         "hymt2_hip_ffn_in": (i, [vp, vp, vp, vp, vp, C.c_float, vp]),
         "hymt2_hip_matmul_static": (C.c_bool, [vp, C.POINTER(vp), C.POINTER(vp), i, vp, i]),
+        "hymt2_hip_attn_split_from": (i, [vp, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -80,7 +81,8 @@ EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops",
            "hymt2_hip_abi_layout", "hymt2_hip_stream", "hymt2_hip_quantize_q8k", "hymt2_hip_matvec",
            "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_selftest_sqsum", "hymt2_hip_generate", "hymt2_hip_gen_begin",
            "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in",
-           "hymt2_hip_gen_prefill", "hymt2_hip_generate_chunked", "hymt2_hip_matmul_static"]
+           "hymt2_hip_gen_prefill", "hymt2_hip_generate_chunked", "hymt2_hip_matmul_static",
+           "hymt2_hip_attn_split_from"]
 
 
 def abi_layout() -> dict:
@@ -105,6 +107,11 @@ class Backend:
             raise RuntimeError(f"hymt2_hip_open failed: {self.info}")
         self.ops = L.hymt2_hip_ops().contents
         self.L = L
+
+    def attn_split_from(self, pos: int):
+        """Single-token forwards at positions >= pos use the split attention (-1: default)."""
+        if self.L.hymt2_hip_attn_split_from(self.impl, pos) != 0:
+            raise RuntimeError("hymt2_hip_attn_split_from failed")
 
     def last_error(self) -> str:
         buf = C.create_string_buffer(512)

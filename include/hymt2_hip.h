@@ -192,6 +192,14 @@ HYMT2_HIP_API int hymt2_hip_generate_chunked(void *impl, const hymt2_fused_args 
                                              int vocab_out, const int *prompt, int n_prompt, int n_gen, int chunk,
                                              int *out_ids, hymt2_gen_stats *stats);
 
+/* Single-token attention form by position (no counterpart in the reference interface): a forward
+ * at position >= from (fused_forward with nt == 1, and the device loop's steps) runs the split
+ * attention, whose scores use many CUs (k_attn_scores, then k_attn_out); positions below run
+ * the one-workgroup-per-head kernel (k_attn1). Both give the same bits. from < 0 restores the
+ * default. Shapes k_attn1 does not take (head dim other than 64/128, ctx > 4096) always split.
+ * Drops the captured graphs (and ends a device loop in progress). 0 on success. */
+HYMT2_HIP_API int hymt2_hip_attn_split_from(void *impl, int from);
+
 /* LM head on device pointers (enqueued on the context stream): logits[r] = row r of an
  * uploaded F16/F32 weight . rmsnorm(h; norm_w, eps), each row summed sequentially in the
  * reference's order (src/model.c:887-900, src/kernels.c:1279-1300). With key != NULL also

@@ -304,3 +304,84 @@ def test_full_size_chunked_prefill_config4(backend):
         assert a[0] == int(np.argmax(stepwise[:fm.vocab_out]))
     finally:
         fm.close()
+
+
+def _stepwise_logits(om, prompt):
+    """The oracle's logits after the prompt, fed 16 positions at a time."""
+    ref = None
+    for i in range(0, len(prompt), 16):
+        c = prompt[i:i + 16]
+        ref = om.forward(c, i, want_logits=(i + len(c) == len(prompt)))
+    return ref
+
+
+@pytest.mark.parametrize("hd", [128, 64])
+def test_split_attention_matches_one_kernel(backend, hd):
+    """The split single-token attention (scores over many workgroups, then softmax and output)
+    against the one-workgroup-per-head kernel and the oracle: two layers (the second layer's keys
+    and values depend on the first layer's attention at every position, so the last logits cover
+    all of them), a 600-token prompt fed one position at a time with the split form forced from
+    position 0, then from 10**9 (never), last logits bit for bit equal to the oracle's; then 30
+    device greedy ids (positions 600-629) under each form, equal to the oracle's."""
+    if hd == 128:
+        shape = synth.ModelShape(n_layer=2, vocab=1000, ctx=640)
+    else:
+        shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1536, heads=8, kv_heads=2, hdim=64, vocab=900, ctx=640)
+    model = synth.make_model(shape, mode="stq", seed=71 + hd)
+    prompt = synth.rand_prompt(synth.rng(72), 600, shape.vocab)
+    ref = _stepwise_logits(O.OracleModel(model, threads=16), prompt)
+    want = O.OracleModel(model, threads=16).generate(prompt, 30, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        for split_from in (0, 10 ** 9):
+            backend.attn_split_from(split_from)
+            assert np.array_equal(bits(fm.prefill(list(prompt), batch=1)), bits(ref)), f"split_from={split_from}"
+            ids, _ = fm.generate_device(prompt, 30)
+            assert np.array_equal(ids, want), f"split_from={split_from}"
+    finally:
+        backend.attn_split_from(-1)
+        fm.close()
+
+
+def test_split_attention_head_dim_256(backend):
+    """Head dim 256 (the one-kernel form takes 64 and 128 only, so every single-token step runs
+    the split form): a 150-token prompt one position at a time, logits and 20 greedy ids vs the
+    oracle."""
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=2, kv_heads=1, hdim=256, vocab=700, ctx=192)
+    model = synth.make_model(shape, mode="q4km", seed=77)
+    prompt = synth.rand_prompt(synth.rng(78), 150, shape.vocab)
+    ref = _stepwise_logits(O.OracleModel(model, threads=16), prompt)
+    want = O.OracleModel(model, threads=16).generate(prompt, 20, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt), batch=1)), bits(ref))
+        ids, _ = fm.generate_device(prompt, 20)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
+def test_long_context_beyond_4096(backend):
+    """Context 4400 (past the one-kernel form's 4096 and the chunk kernel's 2048): two layers, a
+    4150-token prompt in 128-token chunks (the general chunk attention, rows up to 4150), the last
+    logits vs the oracle bit for bit; then single-token forwards at positions 4150 and 4151 (the
+    split form's softmax sum in two chunks, the second continuing the first's running sum), logits
+    vs the oracle; then 40 device greedy ids after the chunked prompt vs the oracle."""
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=2, hdim=128, vocab=600, ctx=4400)
+    model = synth.make_model(shape, mode="stq", seed=79)
+    prompt = synth.rand_prompt(synth.rng(80), 4150, shape.vocab)
+    om = O.OracleModel(model, threads=16)
+    ref = _stepwise_logits(om, prompt)
+    extra = [int(t) for t in synth.rand_prompt(synth.rng(81), 2, shape.vocab)]
+    ref1 = om.forward(extra[:1], 4150, True)
+    ref2 = om.forward(extra[1:], 4151, True)
+    want = O.OracleModel(model, threads=16).generate(prompt, 40, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt), batch=128)), bits(ref))
+        assert np.array_equal(bits(fm.forward(extra[:1], 4150, True)), bits(ref1))
+        assert np.array_equal(bits(fm.forward(extra[1:], 4151, True)), bits(ref2))
+        ids, _ = fm.generate_device(prompt, 40, chunk=128)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
