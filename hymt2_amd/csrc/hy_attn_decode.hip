@@ -25,6 +25,7 @@ constexpr int kA1Prod = kA1Threads - 128;  // producer threads (wavefronts 2-7)
 constexpr int kA1Chunk = 32;           // positions per chain step (16 LDS reads of 2 products)
 constexpr int kA1SerialSum = 256;      // softmax rows up to this length: the lane-serial sum
 constexpr int kA1PairRow = kA1Threads / 2;  // rows up to this length: two lanes per key
+static_assert(kA1SerialSum <= kA1PairRow, "the serial sum reads the pair form's padded exponentials");
 constexpr int kA1ShortRow = 2 * kA1Tile;    // rows up to this length: V staged whole, direct chains
 
 __device__ __forceinline__ void bf16x8f(const uint4& v, float* f) {
@@ -458,7 +459,10 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
         for (int p = 0; p < PASSES; p++) {
             const int j = p * kA1Threads + tid;
             if (pair) {
-                if ((tid & 1) == 0 && (tid >> 1) < n) ex[tid >> 1] = hy_expf_tab(sv[0] - mx, S.etab);
+                // +0 past the row to the next multiple of 32: the lane-serial sum then reads whole
+                // 32-value groups (adding +0 leaves a sum of non-negative terms unchanged)
+                const int m = tid >> 1;
+                if ((tid & 1) == 0 && m < (n + 31) / 32 * 32) ex[m] = m < n ? hy_expf_tab(sv[0] - mx, S.etab) : 0.f;
                 break;
             }
             if (j - tid >= n) break;
@@ -467,7 +471,7 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
         hy_lds_barrier();
         if (n <= kA1SerialSum) {
             if (wave == 0) {
-                const float sum = hy_wave_seq_sum(ex, n, lane);  // the same value in every lane
+                const float sum = hy_wave_seq_sum(ex, (n + 31) / 32 * 32, lane);  // the same value in every lane
                 if (lane == 0) S.stat = 1.0f / sum;
                 if (n <= kA1ShortRow) {  // short rows: p_j = e_j * (1 / sum) in place, once per position
                     const float iv = 1.0f / sum;

@@ -62,6 +62,9 @@ constexpr size_t kInH = 2048;
 
 // Single-token forwards at positions from here on use the split attention (launch_attn_split).
 constexpr int kSplitFromDefault = 448;
+// Device-loop steps captured in one graph: each graph launch costs about 8.5 us of idle GPU
+// between the previous graph's last kernel and the next graph's first.
+constexpr int kStepsPerGraph = 8;
 
 struct Fused {
     int n_layer = 0, hidden = 0, ffn = 0, heads = 0, kv_heads = 0, hdim = 0, qdim = 0, kvdim = 0, ctx = 0,
@@ -92,6 +95,7 @@ struct Fused {
     // captured single-token graphs, [0] with the one-kernel attention (k_attn1), [1] with the
     // split form; a forward at position p replays [split_at(p)]
     hipGraphExec_t g_fwd[2] = {nullptr, nullptr}, g_step[2] = {nullptr, nullptr};
+    hipGraphExec_t g_steps[2] = {nullptr, nullptr};  // kStepsPerGraph steps of the device loop in one graph
     std::vector<const void*> sig_fwd[2], sig_step;
     float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
         const size_t per = 2 * (size_t)hidden + 2 * (size_t)hdim;
@@ -568,7 +572,8 @@ static void free_graphs(Fused* f) {
     for (int v = 0; v < 2; v++) {
         if (f->g_fwd[v]) (void)hipGraphExecDestroy(f->g_fwd[v]);
         if (f->g_step[v]) (void)hipGraphExecDestroy(f->g_step[v]);
-        f->g_fwd[v] = f->g_step[v] = nullptr;
+        if (f->g_steps[v]) (void)hipGraphExecDestroy(f->g_steps[v]);
+        f->g_fwd[v] = f->g_step[v] = f->g_steps[v] = nullptr;
         f->sig_fwd[v].clear();
     }
     f->sig_step.clear();
@@ -1111,17 +1116,24 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     if (f->sig_step != sig || (need[0] && !f->g_step[0]) || (need[1] && !f->g_step[1])) {
         for (int v = 0; v < 2; v++) {
             if (f->g_step[v]) (void)hipGraphExecDestroy(f->g_step[v]);
-            f->g_step[v] = nullptr;
+            if (f->g_steps[v]) (void)hipGraphExecDestroy(f->g_steps[v]);
+            f->g_step[v] = f->g_steps[v] = nullptr;
         }
         f->sig_step.clear();
         FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e->mw, f->d_h, f->hidden, n_total,
                       f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
+        auto one_step = [&](int v) {
+            if (!enqueue_layers(c, shape, 1, 0, f->d_pos, v == 1) || !enqueue_head(c, shape, 1, true, vocab_out))
+                return false;
+            return launch_finish(fa, c->s) == hipSuccess;
+        };
         for (int v = 0; v < 2; v++) {
             if (!need[v]) continue;
-            if (!capture(c, &f->g_step[v], [&] {
-                    if (!enqueue_layers(c, shape, 1, 0, f->d_pos, v == 1) || !enqueue_head(c, shape, 1, true, vocab_out))
-                        return false;
-                    return launch_finish(fa, c->s) == hipSuccess;
+            if (!capture(c, &f->g_step[v], [&] { return one_step(v); })) return -7;
+            if (!capture(c, &f->g_steps[v], [&] {
+                    for (int i = 0; i < kStepsPerGraph; i++)
+                        if (!one_step(v)) return false;
+                    return true;
                 }))
                 return -7;
         }
@@ -1191,12 +1203,18 @@ int hymt2_hip_gen_steps(void* impl, int n) {
         set_err(c, "gen_steps: %d + %d steps exceed the %d positions of this loop", f->gen_steps, n, f->gen_total);
         return -2;
     }
-    for (int i = 0; i < n; i++)
-        if (hipGraphLaunch(f->g_step[split_at(c, f, f->gen_steps + i) ? 1 : 0], c->s) != hipSuccess) {
+    // kStepsPerGraph steps per launch where their positions share one attention form, else one
+    for (int i = 0; i < n;) {
+        const int p = f->gen_steps + i;
+        const int v = split_at(c, f, p) ? 1 : 0;
+        const bool many = n - i >= kStepsPerGraph && (split_at(c, f, p + kStepsPerGraph - 1) ? 1 : 0) == v;
+        if (hipGraphLaunch(many ? f->g_steps[v] : f->g_step[v], c->s) != hipSuccess) {
             set_err(c, "gen_steps: hipGraphLaunch failed");
             c->broken = true;
             return -3;
         }
+        i += many ? kStepsPerGraph : 1;
+    }
     f->gen_steps += n;
     return 0;
 }
