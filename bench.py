@@ -301,6 +301,84 @@ def config4(b):
                 distinct_ids=len(set(ids.tolist())))
 
 
+def q6k_head_leg(b, n_gen: int = 64, reps: int = 10):
+    """The reference's own bench-model shape (tools/make_bench_gguf.c: the 1.8B shapes with
+    STQ1_0 layers and a Q6_K tied embedding / LM head, 203 MB): device-loop decode after a
+    64-token prompt, and the LM head matvec alone (Q6_K 120818 x 2048 through hymt2_hip_matvec on
+    a Q8_K activation; HIP events on the backend stream). Algorithmic head bytes = the Q6_K rows
+    + the activation blocks + the logits."""
+    import torch
+    from hymt2_amd import abi, lib, synth
+    shape = synth.ModelShape(ctx=64 + n_gen + 64)
+    model = synth.make_model(shape, mode="stq", seed=3, head_type=abi.GT_Q6_K)
+    prompt = synth.rand_prompt(synth.rng(1234), 64, shape.vocab)
+    fm = lib.FusedModel(b, model)
+    fm.generate_device(prompt[:8], 4)  # warm: kernels loaded, graphs captured
+    ids, st = fm.generate_device(prompt, n_gen)
+    w = model["outw"]
+    stream = torch.cuda.ExternalStream(b.stream)
+    act = torch.zeros((w.k // 256) * abi.Q8K_BYTES, dtype=torch.uint8, device="cuda")
+    x = torch.randn(w.k, device="cuda", dtype=torch.float32)
+    out = torch.empty(w.n, device="cuda", dtype=torch.float32)
+    b.quantize_q8k(x.data_ptr(), act.data_ptr(), w.k, 1)
+
+    def launch(_):
+        b.matvec(fm.outw, act.data_ptr(), out.data_ptr(), 1)
+
+    for i in range(3):
+        launch(i)
+    avg_s = _timed_launches(stream, launch, reps)
+    algo = w.n * w.row_bytes + (w.k // 256) * abi.Q8K_BYTES + w.n * 4
+    wb = synth.model_weight_bytes(model)
+    dec = st.decode_steps / (st.decode_ms / 1e3)
+    tok_bytes = wb["layers"] + wb["head"] + 2 * shape.n_layer * shape.kvdim * 2 * (64 + n_gen / 2.0)
+    fm.close()
+    return dict(workload="Hy-MT2-1.8B shapes, STQ1_0 layers, Q6_K tied embedding / LM head (the reference's "
+                         "make_bench_gguf shape), 64 random prompt ids, device-loop greedy decode",
+                decode_tok_s=round(dec, 2), decode_bytes_per_token=int(tok_bytes),
+                decode_effective_GBs=round(tok_bytes * dec / 1e9, 1), distinct_ids=len(set(ids.tolist())),
+                head_kernel="Q6_K LM head matvec 120818 x 2048 (hymt2_hip_matvec, one Q8_K token)",
+                head_bytes=int(algo), head_us=round(avg_s * 1e6, 2), head_GBs=round(algo / avg_s / 1e9, 1),
+                head_frac=round(algo / avg_s / 1e9 / HBM_PEAK_GBS, 4))
+
+
+def summarize_trace(d: str):
+    """Markdown table of a rocprofv3 --kernel-trace CSV (DIR/*kernel_trace.csv): per kernel the
+    dispatches, average / min / max duration and share of GPU time; then, for the decode step's
+    FFN-input kernel (the bench's roofline kernel), the average over the dispatches launched back
+    to back by the roofline leg (each preceded by another dispatch of the same kernel) apart from
+    the ones inside the decode graphs. No GPU needed."""
+    import csv
+    import glob
+    fs = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    if not fs:
+        raise SystemExit(f"no *kernel_trace.csv under {d}")
+    rows = []
+    for f in fs:
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    dur = {}
+    for r in rows:
+        dur.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    tot = sum(sum(v) for v in dur.values())
+    print("| kernel | calls | avg us | min us | max us | % of GPU time |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for k, v in sorted(dur.items(), key=lambda kv: -sum(kv[1]))[:24]:
+        print(f"| `{k[:96]}` | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | {100 * sum(v) / tot:.2f} |")
+    tgt = "k_mv1<0, 1, 8, 1>"
+    alone, graph = [], []
+    for i, r in enumerate(rows):
+        if tgt not in r["Kernel_Name"]:
+            continue
+        t = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        (alone if i and tgt in rows[i - 1]["Kernel_Name"] else graph).append(t)
+    if alone:
+        print()
+        print(f"`{tgt}`: {len(alone)} back-to-back dispatches (the roofline leg, hymt2_hip_ffn_in) average "
+              f"{sum(alone) / len(alone):.2f} us; {len(graph)} dispatches inside the decode graphs average "
+              f"{sum(graph) / len(graph):.2f} us.")
+
+
 def host_loop_rate(fm, prompt, n_tokens: int):
     """Decode rate of the reference host's own loop over the drop-in boundary: one
     fused_forward per token with the host embedding in (8 KB H2D), the 120818 logits out (483 KB
@@ -409,7 +487,14 @@ def main():
                     help="only the config 4 chunked-prefill run and the prefill GEMM timing (for profiling)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the standalone kernel launches used for rocprofv3 counter passes")
+    ap.add_argument("--no-q6k", action="store_true", help="skip the Q6_K-head model leg")
+    ap.add_argument("--q6k-only", action="store_true", help="only the Q6_K-head model leg (for profiling)")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print the kernel table of a rocprofv3 --kernel-trace output directory and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the Hy-MT2 token loop at batch 1 runs on a single MI355X "
               "(multi-GPU figures are not part of this build); run with --gpus 1", file=sys.stderr)
@@ -419,6 +504,11 @@ def main():
 
     if args.kernels_only:
         kernels_only(args)
+        return
+    if args.q6k_only:
+        b = lib.Backend()
+        print(json.dumps(q6k_head_leg(b)), flush=True)
+        b.close()
         return
     if args.config4_only:
         b = lib.Backend()
@@ -463,6 +553,10 @@ def main():
     if not args.no_layer_sets:
         sets = layer_sets(b)
         log(f"layer sets: {sets}")
+    q6 = None
+    if not args.no_q6k:
+        q6 = q6k_head_leg(b)
+        log(f"q6k head model: {q6}")
     c4 = None
     if not args.no_config4:
         c4 = config4(b)
@@ -492,6 +586,7 @@ def main():
         "head_roofline": head,
         "host_loop": host,
         "layer_sets": sets,
+        "q6k_head_model": q6,
         "config4_prefill": c4,
         "cpu_baseline": cpu,
     }

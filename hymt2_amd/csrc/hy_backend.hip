@@ -82,7 +82,8 @@ struct Fused {
     float *rope_c = nullptr, *rope_s = nullptr, *out_norm = nullptr, *norms = nullptr;
     uint16_t *kc = nullptr, *vc = nullptr;
     size_t logits_cap = 0;
-    unsigned long long* key = nullptr;
+    unsigned long long* slots = nullptr;  // argmax keys of the LM head, one per workgroup (kArgSlots)
+    int head_slots = 0;                   // the slots the last enqueued head with argmax writes
     int* ids = nullptr;
     int ids_cap = 0;
     int gen_total = 0;   // positions of the current device loop (0: no loop begun)
@@ -584,7 +585,7 @@ static void free_fused(Fused* f) {
     if (!f) return;
     free_graphs(f);
     void* dev[] = {f->in_dev, f->q, f->k, f->v, f->ao, f->g, f->u, f->logits, f->act_h, f->act_q, f->act_f,
-                   f->rope_c, f->rope_s, f->out_norm, f->norms, f->kc, f->vc, f->key, f->ids, f->sc, f->segmax};
+                   f->rope_c, f->rope_s, f->out_norm, f->norms, f->kc, f->vc, f->slots, f->ids, f->sc, f->segmax};
     for (void* p : dev)
         if (p) (void)hipFree(p);
     if (f->in_host) (void)hipHostFree(f->in_host);
@@ -655,7 +656,7 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
          dalloc(c, &f->rope_s, (size_t)a->ctx * a->rope_half * 4 + 4) && dalloc(c, &f->out_norm, H * 4) &&
          dalloc(c, &f->norms, (size_t)a->n_layer * (2 * H + 2 * a->hdim) * 4) &&
          dalloc(c, &f->kc, (size_t)a->n_layer * a->ctx * KV * 2) &&
-         dalloc(c, &f->vc, (size_t)a->n_layer * a->ctx * KV * 2) && dalloc(c, &f->key, 64) &&
+         dalloc(c, &f->vc, (size_t)a->n_layer * a->ctx * KV * 2) && dalloc(c, &f->slots, (size_t)kArgSlots * 8) &&
          dalloc(c, &f->sc, (size_t)a->heads * split_sc_stride(a->ctx) * 4) &&
          dalloc(c, &f->segmax, (size_t)a->heads * split_seg_stride(a->ctx) * 4);
     if (!ok) {
@@ -669,7 +670,7 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
     if (!copy_params(c, a)) return false;
     HIPCHK(c, hipMemset(f->kc, 0, (size_t)a->n_layer * a->ctx * KV * 2));
     HIPCHK(c, hipMemset(f->vc, 0, (size_t)a->n_layer * a->ctx * KV * 2));
-    HIPCHK(c, hipMemset(f->key, 0, 64));
+    HIPCHK(c, hipMemset(f->slots, 0, (size_t)kArgSlots * 8));
     HIPCHK(c, hipMemset(f->in_dev, 0, f->in_bytes));
     return true;
 }
@@ -831,7 +832,8 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
 }
 
 // Output RMSNorm + LM head on the last token (src/model.c:887-900), optionally folding the
-// greedy argmax into f->key.
+// greedy argmax into f->slots (one key per workgroup of the head kernel; f->head_slots of them).
+// Quantized heads run on the decode matvec with its RMSNorm + Q8_K prologue.
 static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax, int vocab_out) {
     Fused* f = c->f;
     const DW* ow = dw(a->outw);
@@ -848,18 +850,48 @@ static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax,
         h.norm_w = f->out_norm;
         h.eps = f->eps;
         h.logits = f->logits;
-        h.argmax_key = argmax ? f->key : nullptr;
+        h.slots = argmax ? f->slots : nullptr;
         h.n_arg = vocab_out;
+        if (argmax && head_grid(ow->mw.n) > kArgSlots) {
+            set_err(c, "fused_forward: %d head rows exceed the argmax slots", ow->mw.n);
+            return false;
+        }
         HIPCHK(c, launch_head(h, c->s));
+        f->head_slots = head_grid(ow->mw.n);
     } else {
-        JobSpec j{ow, f->logits, ow->mw.n, EPI_STORE};
-        MvOpts o;
-        o.pro = PRO_NORM;
-        o.x = hl;
-        o.norm_w = f->out_norm;
-        o.eps = f->eps;
-        if (!run_matvec(c, &j, 1, false, 1, o)) return false;
-        if (argmax) HIPCHK(c, launch_argmax(f->logits, vocab_out, f->key, c->s));
+        Mv1Launch L;
+        memset(&L, 0, sizeof L);
+        L.njobs = 1;
+        L.job[0].W = ow->mw;
+        L.job[0].out = f->logits;
+        L.job[0].epi = EPI_STORE;
+        L.x = hl;
+        L.norm_w = f->out_norm;
+        L.eps = f->eps;
+        L.slots = argmax ? f->slots : nullptr;
+        L.n_arg = vocab_out;
+        const hipError_t e = nt == 1 ? launch_mv1(L, PRO_NORM, c->s) : hipErrorNotSupported;
+        if (e == hipSuccess) {
+            f->head_slots = L.grid;
+        } else if (e != hipErrorNotSupported) {
+            HIPCHK(c, e);
+        } else {
+            JobSpec j{ow, f->logits, ow->mw.n, EPI_STORE};
+            MvOpts o;
+            o.pro = PRO_NORM;
+            o.x = hl;
+            o.norm_w = f->out_norm;
+            o.eps = f->eps;
+            if (!run_matvec(c, &j, 1, false, 1, o)) return false;
+            if (argmax) {
+                if (head_grid(vocab_out) > kArgSlots) {
+                    set_err(c, "fused_forward: vocab %d exceeds the argmax slots", vocab_out);
+                    return false;
+                }
+                HIPCHK(c, launch_argmax(f->logits, vocab_out, f->slots, c->s));
+                f->head_slots = head_grid(vocab_out);
+            }
+        }
     }
     return true;
 }
@@ -1120,11 +1152,11 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
             f->g_step[v] = f->g_steps[v] = nullptr;
         }
         f->sig_step.clear();
-        FinishArgs fa{f->key, f->ids, f->d_pos, n_prompt, e->mw, f->d_h, f->hidden, n_total,
-                      f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
         auto one_step = [&](int v) {
             if (!enqueue_layers(c, shape, 1, 0, f->d_pos, v == 1) || !enqueue_head(c, shape, 1, true, vocab_out))
                 return false;
+            const FinishArgs fa{f->slots, f->head_slots, f->ids, f->d_pos, n_prompt, e->mw, f->d_h, f->hidden,
+                                n_total, f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
             return launch_finish(fa, c->s) == hipSuccess;
         };
         for (int v = 0; v < 2; v++) {
@@ -1139,12 +1171,11 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
         }
         f->sig_step = sig;
     }
-    // start state: ids[0..n_prompt) = prompt, pos = 0, key = 0, h = embedding of ids[0]
+    // start state: ids[0..n_prompt) = prompt, pos = 0, h = embedding of ids[0]
     memset(f->in_host, 0, f->in_bytes);
     stage_pos(f, shape, 0);
     if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->in_dev, f->in_host, kInH, hipMemcpyHostToDevice, c->s) != hipSuccess ||
-        hipMemcpyAsync(f->key, f->in_host, 8, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         launch_embed(f->ids, f->d_pos, e->mw, f->d_h, f->hidden, c->s) != hipSuccess ||
         hipStreamSynchronize(c->s) != hipSuccess) {
         set_err(c, "gen_begin: device setup failed");
@@ -1184,8 +1215,8 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     }
     // position np - 1 has been processed: the finishing kernel records the first generated id,
     // embeds it and advances the step counter to np, where the step graph continues
-    FinishArgs fa{f->key, f->ids, f->d_pos, np, f->gen_embd, f->d_h, f->hidden, f->gen_total,
-                  f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
+    const FinishArgs fa{f->slots, f->head_slots, f->ids, f->d_pos, np, f->gen_embd, f->d_h, f->hidden, f->gen_total,
+                        f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
     if (launch_set_int(f->d_pos, np - 1, c->s) != hipSuccess || launch_finish(fa, c->s) != hipSuccess) {
         set_err(c, "gen_prefill: launch failed");
         c->broken = true;

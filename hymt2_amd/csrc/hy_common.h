@@ -77,6 +77,40 @@ __device__ __forceinline__ uint64_t hy_exp_tab_entry(int i) {
     return T[i & 31];
 }
 
+// Key of logit v at row idx for the greedy argmax of src/model.c:945-948, which starts from
+// bv = logits[0] and takes row j only when logits[j] > bv: the first maximal row wins, a NaN at
+// row j > 0 never wins, and a NaN at row 0 wins outright (no comparison with it is true).
+__device__ inline unsigned long long argmax_key(float v, int idx) {
+    uint32_t u = hy_fbits(v);
+    if (u == 0x80000000u) u = 0;                       // -0 ties with +0 (first index wins)
+    if ((u & 0x7fffffffu) > 0x7f800000u) return idx == 0 ? ~0ull : 0ull;
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+
+__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// The greedy argmax key of a workgroup (the maximum of every thread's key) into *slot, written by
+// thread 0: one slot per workgroup, reduced by the step's finishing kernel, so no two workgroups
+// write one address (same-address atomics from a whole grid serialize). Every thread calls it.
+__device__ inline void hy_wg_slot_max(unsigned long long key, unsigned long long* slot) {
+    __shared__ unsigned long long wk[16];
+    key = wave_max_u64(key);
+    const int nw = (blockDim.x + 63) >> 6;
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < nw; w++) key = wk[w] > key ? wk[w] : key;
+        *slot = key;
+    }
+}
+
 __device__ __forceinline__ void hy_lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }

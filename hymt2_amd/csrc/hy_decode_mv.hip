@@ -163,8 +163,10 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     }
     __syncthreads();
 
-    // 5. per-row sums in block order and the epilogue
+    // 5. per-row sums in block order and the epilogue (optionally the greedy argmax of the rows,
+    //    one key per workgroup)
     if (!pair) {
+        unsigned long long key = 0ull;
         if (lane < RPW) {
             const int r = row0 + wave * RPW + lane;
             if (r < n) {
@@ -172,8 +174,10 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
 #pragma unroll
                 for (int b = 0; b < NB; b++) acc += terms[wave][lane][b];
                 J.out[r] = J.epi == EPI_ADD ? resid + acc : acc;  // residual: h += tmp
+                if (r < L.n_arg) key = argmax_key(acc, r);
             }
         }
+        if (L.slots) hy_wg_slot_max(key, L.slots + wg);
     } else if (lane < ITERS) {
         const int p = row0 + wave * ITERS + lane;
         if (p < n) {
@@ -257,6 +261,8 @@ hipError_t launch_mv1(Mv1Launch& L, int pro, hipStream_t s) {
         L.rows_per_wg = per;
         if (g <= kMv1MaxWgs) break;
     }
+    if (L.slots && (L.pair || grid > kArgSlots)) return hipErrorNotSupported;
+    L.grid = grid;
     L.K = K;
     const int kind = panel ? KIND_PANEL : (q4 && q6 ? KIND_ANY : (q4 ? KIND_Q4K : KIND_Q6K));
     if (kind == KIND_PANEL) {

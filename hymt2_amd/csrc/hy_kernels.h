@@ -97,6 +97,9 @@ struct Mv1Launch {
     const float* norm_w;   // PRO_NORM weights [K]
     float eps;
     int K;
+    unsigned long long* slots;  // optional: the greedy argmax over rows < n_arg, one key per workgroup
+    int n_arg;
+    int grid;              // set by launch_mv1: its workgroups (argmax slots written)
 };
 
 // Builds and launches k_mv1 for jobs of one kind class with K = 2048 or 6144; returns
@@ -194,13 +197,18 @@ struct HeadArgs {
     const float* norm_w;   // output norm
     float eps;
     float* logits;         // [n]
-    unsigned long long* argmax_key;  // optional fused argmax over rows < n_arg
+    unsigned long long* argmax_key;  // optional fused argmax over rows < n_arg, by atomicMax into one key
     int n_arg;
+    unsigned long long* slots;       // or: one key per workgroup (slot = workgroup, head_grid of them)
 };
 hipError_t launch_head(const HeadArgs& a, hipStream_t s);
+inline int head_grid(int n) { return (n + 255) / 256; }
+// Argmax slots of the device loop: one per workgroup of the LM head kernel that writes them.
+constexpr int kArgSlots = 8192;
 
 struct FinishArgs {
-    unsigned long long* argmax_key;
+    const unsigned long long* slots;  // the head's per-workgroup argmax keys
+    int nslots;
     int* ids;              // token ids [n_total]
     int* step;             // device step counter (position of the token just processed)
     int n_prompt;
@@ -222,7 +230,8 @@ hipError_t launch_embed(const int* ids, const int* step, const MvWeight& E, floa
 hipError_t launch_embed_rows(const int* ids, int first, int nt, const MvWeight& E, float* h, int H, hipStream_t s);
 hipError_t launch_set_int(int* p, int v, hipStream_t s);
 
-hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s);
+// The greedy argmax of v[0 .. n) as one key per 256-element workgroup into slots (head_grid(n) slots).
+hipError_t launch_argmax(const float* v, int n, unsigned long long* slots, hipStream_t s);
 hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s);
 hipError_t launch_selftest_sqsum(const float* x, int n, int m, float* out, int method, hipStream_t s);

@@ -825,25 +825,6 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
 
 // =========================================================================== LM head
 
-// Key of logit v at row idx for the greedy argmax of src/model.c:945-948, which starts from
-// bv = logits[0] and takes row j only when logits[j] > bv: the first maximal row wins, a NaN at
-// row j > 0 never wins, and a NaN at row 0 wins outright (no comparison with it is true).
-__device__ inline unsigned long long argmax_key(float v, int idx) {
-    uint32_t u = hy_fbits(v);
-    if (u == 0x80000000u) u = 0;                       // -0 ties with +0 (first index wins)
-    if ((u & 0x7fffffffu) > 0x7f800000u) return idx == 0 ? ~0ull : 0ull;
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
-}
-
-__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
-    for (int o = 32; o >= 1; o >>= 1) {
-        const unsigned long long w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
-    return v;
-}
-
 // One lane per vocabulary row: logits[r] = sum_j w(r, j) * xn[j] accumulated sequentially in the
 // reference's order, after the output RMSNorm (src/model.c:888-890):
 //   F16 / F32: s += f16_to_f32(w) * x, one product and one add per weight (src/kernels.c:1279-1300)
@@ -954,7 +935,9 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     }
     const int r = r0 + tid;
     if (r < n) a.logits[r] = acc;
-    if (a.argmax_key) {
+    if (a.slots) {
+        hy_wg_slot_max(r < a.n_arg ? argmax_key(acc, r) : 0ull, a.slots + blockIdx.x);
+    } else if (a.argmax_key) {
         unsigned long long key = (r < a.n_arg) ? argmax_key(acc, r) : 0ull;
         key = wave_max_u64(key);
         if ((tid & 63) == 0 && key) atomicMax(a.argmax_key, key);
@@ -1051,17 +1034,24 @@ __device__ void embed_row(const MvWeight& E, int tok, float* h, int H) {
     for (int i = threadIdx.x; i < H; i += blockDim.x) h[i] = embed_elem(E, tok, i, H);
 }
 
-// Greedy step tail: token = argmax key; the next input is the next prompt id while the prompt
-// lasts, else the argmax (recorded in ids). Embeds the next token's row into h, copies the next
-// position's RoPE row, advances the device step counter and clears the key. The key, the step
-// and the prompt id are read by every thread (uniform scalar loads, one round each), so no
-// broadcast is needed before the embedding; the writes wait for every wavefront's reads.
+// Greedy step tail: token = the maximum of the head's per-workgroup argmax keys; the next input
+// is the next prompt id while the prompt lasts, else the argmax (recorded in ids). Embeds the
+// next token's row into h, copies the next position's RoPE row and advances the device step
+// counter. The step and the prompt id are read by every thread (uniform scalar loads); the slots
+// are reduced over the workgroup before the embedding.
 __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
-    hy_sgpr_pin(a.argmax_key), hy_sgpr_pin(a.ids), hy_sgpr_pin(a.step), hy_sgpr_pin(a.n_prompt),
+    hy_sgpr_pin(a.slots), hy_sgpr_pin(a.nslots), hy_sgpr_pin(a.ids), hy_sgpr_pin(a.step), hy_sgpr_pin(a.n_prompt),
         hy_sgpr_pin(a.E.w), hy_sgpr_pin(a.E.kind), hy_sgpr_pin(a.h), hy_sgpr_pin(a.H), hy_sgpr_pin(a.n_total),
         hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin), hy_sgpr_pin(a.rope_half),
         hy_sgpr_pin(a.ctx), hy_sgpr_pin(blockDim.x);
-    const unsigned long long key = *a.argmax_key;
+    __shared__ unsigned long long kw[4];
+    unsigned long long key = 0ull;
+    for (int i = threadIdx.x; i < a.nslots; i += 256) key = a.slots[i] > key ? a.slots[i] : key;
+    key = wave_max_u64(key);
+    if ((threadIdx.x & 63) == 0) kw[threadIdx.x >> 6] = key;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; w++) key = kw[w] > key ? kw[w] : key;
     const int step = *a.step;
     const int nx = step + 1;
     const int pid = a.ids[min(nx, a.n_total - 1)];  // the next prompt id, if the prompt lasts
@@ -1078,7 +1068,6 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
     if (threadIdx.x == 0) {
         if (nx >= a.n_prompt && nx < a.n_total) a.ids[nx] = best;
         *a.step = nx;
-        *a.argmax_key = 0ull;
     }
 }
 
@@ -1118,15 +1107,13 @@ hipError_t launch_set_int(int* p, int v, hipStream_t s) {
 // =========================================================================== small kernels
 
 // Greedy argmax over rows [0, n) of fp32 logits into a 64-bit key (first index on ties).
-__global__ __launch_bounds__(256) void k_argmax(const float* v, int n, unsigned long long* key) {
+__global__ __launch_bounds__(256) void k_argmax(const float* v, int n, unsigned long long* slots) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    unsigned long long k = i < n ? argmax_key(v[i], i) : 0ull;
-    k = wave_max_u64(k);
-    if ((threadIdx.x & 63) == 0 && k) atomicMax(key, k);
+    hy_wg_slot_max(i < n ? argmax_key(v[i], i) : 0ull, slots + blockIdx.x);
 }
 
-hipError_t launch_argmax(const float* v, int n, unsigned long long* key, hipStream_t s) {
-    k_argmax<<<(n + 255) / 256, 256, 0, s>>>(v, n, key);
+hipError_t launch_argmax(const float* v, int n, unsigned long long* slots, hipStream_t s) {
+    k_argmax<<<head_grid(n), 256, 0, s>>>(v, n, slots);
     return hipGetLastError();
 }
 
