@@ -833,7 +833,7 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
 
 // Output RMSNorm + LM head on the last token (src/model.c:887-900), optionally folding the
 // greedy argmax into f->slots (one key per workgroup of the head kernel; f->head_slots of them).
-// Quantized heads run on the decode matvec with its RMSNorm + Q8_K prologue.
+// Quantized heads run on the decode matvec over the Q8_K of the normalized last token.
 static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax, int vocab_out) {
     Fused* f = c->f;
     const DW* ow = dw(a->outw);
@@ -865,12 +865,12 @@ static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax,
         L.job[0].W = ow->mw;
         L.job[0].out = f->logits;
         L.job[0].epi = EPI_STORE;
-        L.x = hl;
-        L.norm_w = f->out_norm;
-        L.eps = f->eps;
+        L.act = f->act_h;
         L.slots = argmax ? f->slots : nullptr;
         L.n_arg = vocab_out;
-        const hipError_t e = nt == 1 ? launch_mv1(L, PRO_NORM, c->s) : hipErrorNotSupported;
+        // RMSNorm + Q8_K of the last token once, not in every workgroup of the wide head grid
+        HIPCHK(c, launch_rmsnorm_q8k(hl, f->out_norm, f->eps, f->hidden, 1, nullptr, f->act_h, c->s));
+        const hipError_t e = launch_mv1(L, PRO_NONE, c->s);
         if (e == hipSuccess) {
             f->head_slots = L.grid;
         } else if (e != hipErrorNotSupported) {

@@ -833,12 +833,15 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
 // A workgroup owns one row tile (kRowTile rows, one per thread). In the row-tiled layout piece q
 // (16 bytes) of the tile's rows is one contiguous 4 KB run, so every thread reads its own row
 // straight into registers with coalesced loads: a stage is 64 bytes of the row (four pieces),
-// and four register sets rotate, three stages in flight while one is summed. Q8_0 scales come
-// from their own row tiles, one 16-byte piece (8 blocks = 4 stages) at a time, a piece ahead.
-// No LDS staging and no barriers past the norm. Optionally folds the greedy argmax (first index
-// on ties, src/model.c:945-948) into a 64-bit atomicMax key.
+// and NS register sets rotate, NS - 1 stages in flight while one is summed (NS = 8 for F16 and
+// F32: 32 KB in flight per wavefront keeps HBM busy with one or two workgroups per CU; 4 for
+// Q8_0). Q8_0 scales come from their own row tiles, one 16-byte piece (8 blocks = 4 stages) at a
+// time, a piece ahead. No LDS staging and no barriers past the norm. Optionally folds the greedy
+// argmax (first index on ties, src/model.c:945-948) into one key per workgroup (slots) or a
+// 64-bit atomicMax key.
 template <int KIND>
 __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
+    constexpr int NS = KIND == KIND_Q8_0 ? 4 : 8;
     extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
     __shared__ float scale_slot;
     hy_sgpr_pin(a.W.w), hy_sgpr_pin(a.W.w2), hy_sgpr_pin(a.W.k), hy_sgpr_pin(a.W.n), hy_sgpr_pin(a.h),
@@ -853,7 +856,6 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     const int nstage = rowb / 64;
     // piece q of this thread's row
     const uint8_t* src = a.W.w + (size_t)blockIdx.x * kRowTile * rowb + (size_t)tid * 16;
-    v4u s0[4], s1[4], s2[4], s3[4];
     // stage st = pieces 4 st .. 4 st + 3; stages past the last repeat it, unused
     auto ld = [&](v4u (&p)[4], int st) __attribute__((always_inline)) {
         const size_t c = (size_t)min(st, nstage - 1) * 4 * (kRowTile * 16);
@@ -869,7 +871,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     };
     v4u dcur = {0, 0, 0, 0}, dnext = {0, 0, 0, 0};
     float acc = 0.f;
-    auto comp = [&](const v4u (&p)[4], int st) __attribute__((always_inline)) {
+    auto comp = [&](const v4u (&p)[4], int st, int q4) __attribute__((always_inline)) {  // q4 = st % 4 (Q8_0)
         if (st >= nstage) return;
         if (KIND == KIND_F16) {
             const float* xk = xs + st * 32;
@@ -893,7 +895,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
             }
         } else {  // Q8_0: blocks 2 st and 2 st + 1, scales at halves (2 st) % 8 and (2 st + 1) % 8
             const float* xk = xs + st * 64;
-            const uint32_t dw = (st & 3) == 0 ? dcur.x : (st & 3) == 1 ? dcur.y : (st & 3) == 2 ? dcur.z : dcur.w;
+            const uint32_t dw = q4 == 0 ? dcur.x : q4 == 1 ? dcur.y : q4 == 2 ? dcur.z : dcur.w;
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
                 float sb = 0.f;
@@ -914,23 +916,37 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
         dcur = ld_d(0);
         dnext = ld_d(1);
     }
-    ld(s0, 0);
-    ld(s1, 1);
-    ld(s2, 2);
-    ld(s3, 3);
-    rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);  // while the weights stream
-    for (int st = 0; st < nstage; st += 4) {
-        comp(s0, st);
-        ld(s0, st + 4);
-        comp(s1, st + 1);
-        ld(s1, st + 5);
-        comp(s2, st + 2);
-        ld(s2, st + 6);
-        comp(s3, st + 3);
-        ld(s3, st + 7);
-        if (KIND == KIND_Q8_0) {
+    if constexpr (KIND == KIND_Q8_0) {
+        // four named register sets: an array of them, or eight, spills with the scale logic
+        v4u s0[4], s1[4], s2[4], s3[4];
+        ld(s0, 0);
+        ld(s1, 1);
+        ld(s2, 2);
+        ld(s3, 3);
+        rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);  // while the weights stream
+        for (int st = 0; st < nstage; st += 4) {
+            comp(s0, st, 0);
+            ld(s0, st + 4);
+            comp(s1, st + 1, 1);
+            ld(s1, st + 5);
+            comp(s2, st + 2, 2);
+            ld(s2, st + 6);
+            comp(s3, st + 3, 3);
+            ld(s3, st + 7);
             dcur = dnext;
             dnext = ld_d(st / 4 + 2);
+        }
+    } else {
+        v4u sb[NS][4];
+#pragma unroll
+        for (int i = 0; i < NS; i++) ld(sb[i], i);
+        rmsnorm_lds(xs, xs + K, a.norm_w, K, a.eps, &scale_slot);  // while the weights stream
+        for (int st = 0; st < nstage; st += NS) {
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                comp(sb[i], st + i, 0);
+                ld(sb[i], st + NS + i);
+            }
         }
     }
     const int r = r0 + tid;
@@ -1045,8 +1061,17 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
         hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin), hy_sgpr_pin(a.rope_half),
         hy_sgpr_pin(a.ctx), hy_sgpr_pin(blockDim.x);
     __shared__ unsigned long long kw[4];
+    // the slot maxima, eight loads in flight per thread; indices past the end re-read the last
+    // slot (a maximum is unchanged by repeats), so every load is unconditional
     unsigned long long key = 0ull;
-    for (int i = threadIdx.x; i < a.nslots; i += 256) key = a.slots[i] > key ? a.slots[i] : key;
+    const int last = a.nslots - 1;
+    for (int base = threadIdx.x; base <= last; base += 8 * 256) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = a.slots[min(base + 256 * u, last)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) key = v[u] > key ? v[u] : key;
+    }
     key = wave_max_u64(key);
     if ((threadIdx.x & 63) == 0) kw[threadIdx.x >> 6] = key;
     __syncthreads();
