@@ -884,12 +884,12 @@ static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax,
             o.eps = f->eps;
             if (!run_matvec(c, &j, 1, false, 1, o)) return false;
             if (argmax) {
-                if (head_grid(vocab_out) > kArgSlots) {
+                if (argmax_grid(vocab_out) > kArgSlots) {
                     set_err(c, "fused_forward: vocab %d exceeds the argmax slots", vocab_out);
                     return false;
                 }
                 HIPCHK(c, launch_argmax(f->logits, vocab_out, f->slots, c->s));
-                f->head_slots = head_grid(vocab_out);
+                f->head_slots = argmax_grid(vocab_out);
             }
         }
     }

@@ -202,7 +202,8 @@ struct HeadArgs {
     unsigned long long* slots;       // or: one key per workgroup (slot = workgroup, head_grid of them)
 };
 hipError_t launch_head(const HeadArgs& a, hipStream_t s);
-inline int head_grid(int n) { return (n + 255) / 256; }
+constexpr int kHeadThreads = 256;  // LM head rows per workgroup (one per thread; 128 measured slower)
+inline int head_grid(int n) { return (n + kHeadThreads - 1) / kHeadThreads; }
 // Argmax slots of the device loop: one per workgroup of the LM head kernel that writes them.
 constexpr int kArgSlots = 8192;
 
@@ -230,7 +231,8 @@ hipError_t launch_embed(const int* ids, const int* step, const MvWeight& E, floa
 hipError_t launch_embed_rows(const int* ids, int first, int nt, const MvWeight& E, float* h, int H, hipStream_t s);
 hipError_t launch_set_int(int* p, int v, hipStream_t s);
 
-// The greedy argmax of v[0 .. n) as one key per 256-element workgroup into slots (head_grid(n) slots).
+// The greedy argmax of v[0 .. n) as one key per 256-element workgroup into slots (argmax_grid(n) slots).
+inline int argmax_grid(int n) { return (n + 255) / 256; }
 hipError_t launch_argmax(const float* v, int n, unsigned long long* slots, hipStream_t s);
 hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s);

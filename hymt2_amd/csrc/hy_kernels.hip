@@ -830,9 +830,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
 //   F16 / F32: s += f16_to_f32(w) * x, one product and one add per weight (src/kernels.c:1279-1300)
 //   Q8_0: per 32-weight block s_b = sum_j (float)q_j * x_j, then sum += f16_to_f32(d_b) * s_b
 //         (dot_q8_0_f32, src/kernels.c:1099-1107)
-// A workgroup owns one row tile (kRowTile rows, one per thread). In the row-tiled layout piece q
-// (16 bytes) of the tile's rows is one contiguous 4 KB run, so every thread reads its own row
-// straight into registers with coalesced loads: a stage is 64 bytes of the row (four pieces),
+// A workgroup owns kHeadThreads consecutive rows of one row tile (one per thread). In the
+// row-tiled layout piece q (16 bytes) of the tile's rows is one contiguous 4 KB run, so every
+// thread reads its own row straight into registers with coalesced loads: a stage is 64 bytes of the row (four pieces),
 // and NS register sets rotate, NS - 1 stages in flight while one is summed (NS = 8 for F16 and
 // F32: 32 KB in flight per wavefront keeps HBM busy with one or two workgroups per CU; 4 for
 // Q8_0). Q8_0 scales come from their own row tiles, one 16-byte piece (8 blocks = 4 stages) at a
@@ -840,22 +840,24 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
 // argmax (first index on ties, src/model.c:945-948) into one key per workgroup (slots) or a
 // 64-bit atomicMax key.
 template <int KIND>
-__global__ __launch_bounds__(256) void k_head(HeadArgs a) {
+__global__ __launch_bounds__(kHeadThreads) void k_head(HeadArgs a) {
     constexpr int NS = KIND == KIND_Q8_0 ? 4 : 8;
     extern __shared__ __align__(16) float xs[];    // [K] normalized input, [K] squares
     __shared__ float scale_slot;
     hy_sgpr_pin(a.W.w), hy_sgpr_pin(a.W.w2), hy_sgpr_pin(a.W.k), hy_sgpr_pin(a.W.n), hy_sgpr_pin(a.h),
         hy_sgpr_pin(a.norm_w), hy_sgpr_pin(a.eps), hy_sgpr_pin(a.logits), hy_sgpr_pin(a.argmax_key),
         hy_sgpr_pin(a.n_arg), hy_sgpr_pin(blockDim.x);
-    static_assert(kRowTile == 256, "one row per thread");
+    static_assert(kRowTile % kHeadThreads == 0, "a workgroup takes whole rows of one tile");
+    constexpr int SUB = kRowTile / kHeadThreads;  // workgroups per row tile
     constexpr int WB = KIND == KIND_F16 ? 2 : KIND == KIND_F32 ? 4 : 1;  // bytes per weight
     const int tid = threadIdx.x;
     const int K = a.W.k, n = a.W.n;
-    const int r0 = blockIdx.x * kRowTile;
+    const int tile = blockIdx.x / SUB, tr0 = (blockIdx.x % SUB) * kHeadThreads;  // first row in the tile
+    const int r0 = tile * kRowTile + tr0;
     const int rowb = WB * K;
     const int nstage = rowb / 64;
     // piece q of this thread's row
-    const uint8_t* src = a.W.w + (size_t)blockIdx.x * kRowTile * rowb + (size_t)tid * 16;
+    const uint8_t* src = a.W.w + (size_t)tile * kRowTile * rowb + (size_t)(tr0 + tid) * 16;
     // stage st = pieces 4 st .. 4 st + 3; stages past the last repeat it, unused
     auto ld = [&](v4u (&p)[4], int st) __attribute__((always_inline)) {
         const size_t c = (size_t)min(st, nstage - 1) * 4 * (kRowTile * 16);
@@ -864,7 +866,7 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
     };
     // Q8_0 scales: piece g holds the f16 d of blocks 8 g .. 8 g + 7 (stages 4 g .. 4 g + 3)
     const int dpieces = K / 256;
-    const uint8_t* dsrc = KIND == KIND_Q8_0 ? a.W.w2 + (size_t)blockIdx.x * kRowTile * (K / 16) + (size_t)tid * 16
+    const uint8_t* dsrc = KIND == KIND_Q8_0 ? a.W.w2 + (size_t)tile * kRowTile * (K / 16) + (size_t)(tr0 + tid) * 16
                                             : nullptr;
     auto ld_d = [&](int g) __attribute__((always_inline)) {
         return *reinterpret_cast<const v4u*>(dsrc + (size_t)min(g, dpieces - 1) * (kRowTile * 16));
@@ -961,17 +963,17 @@ __global__ __launch_bounds__(256) void k_head(HeadArgs a) {
 }
 
 hipError_t launch_head(const HeadArgs& a, hipStream_t s) {
-    const int grid = (a.W.n + 255) / 256;
+    const int grid = head_grid(a.W.n);
     const size_t lds = (2 * (size_t)a.W.k) * sizeof(float);
     if (a.W.kind == KIND_F16) {
         if (a.W.k % 32) return hipErrorInvalidValue;
-        k_head<KIND_F16><<<grid, 256, lds, s>>>(a);
+        k_head<KIND_F16><<<grid, kHeadThreads, lds, s>>>(a);
     } else if (a.W.kind == KIND_F32) {
         if (a.W.k % 16) return hipErrorInvalidValue;
-        k_head<KIND_F32><<<grid, 256, lds, s>>>(a);
+        k_head<KIND_F32><<<grid, kHeadThreads, lds, s>>>(a);
     } else if (a.W.kind == KIND_Q8_0) {
         if (a.W.k % 256) return hipErrorInvalidValue;
-        k_head<KIND_Q8_0><<<grid, 256, lds, s>>>(a);
+        k_head<KIND_Q8_0><<<grid, kHeadThreads, lds, s>>>(a);
     } else {
         return hipErrorInvalidValue;
     }
@@ -1138,7 +1140,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* v, int n, unsigned 
 }
 
 hipError_t launch_argmax(const float* v, int n, unsigned long long* slots, hipStream_t s) {
-    k_argmax<<<head_grid(n), 256, 0, s>>>(v, n, slots);
+    k_argmax<<<argmax_grid(n), 256, 0, s>>>(v, n, slots);
     return hipGetLastError();
 }
 
