@@ -618,11 +618,12 @@ hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {
 // ------------------------------------------------------------------ split form for long rows
 //
 // The same attention as k_attn1 in two kernels, so that long rows use many CUs:
-//   k_attn_scores, one 256-thread workgroup per (KV head, segment of kSplitSeg positions):
-//     RoPE + RMSNorm of the group's q heads (each wavefront its heads, recomputed by every
-//     workgroup) and, in the workgroup whose segment holds the position, of this token's k, with
-//     the bf16 KV store at the position; then one key per lane, scored for each q head of the
-//     wavefront in dot_bf16's order; the scores and each segment's maximum go to global memory.
+//   k_attn_scores, one 512-thread workgroup per (KV head, segment of kSplitSeg positions):
+//     RoPE + RMSNorm of the group's q heads (recomputed by every workgroup) and, in the workgroup
+//     whose segment holds the position, of this token's k, with the bf16 KV store at the
+//     position; then wavefront w scores q head w % 4 over half of the segment, one key per pair
+//     of lanes in dot_bf16's order; the scores and each half-segment's maximum go to global
+//     memory.
 //   k_attn_out, one 512-thread workgroup per (query head, 64 output dimensions): the maximum of
 //     the segment maxima (order-free), e_j = expf(s_j - max), their sum in position order by the
 //     8-wavefront exact segmented sum (rows longer than kSplitWin in chunks, each later chunk
