@@ -30,50 +30,39 @@ __device__ __forceinline__ uint32_t row_max_u(uint32_t v) {
     x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
     return (uint32_t)x;
 }
-__device__ __forceinline__ int row_min_i(int x) {
-    x = min(x, hy_dpp<HY_DPP_QSWAP1>(x));
-    x = min(x, hy_dpp<HY_DPP_QSWAP2>(x));
-    x = min(x, hy_dpp<HY_DPP_HMIRROR>(x));
-    x = min(x, hy_dpp<HY_DPP_MIRROR>(x));
-    return x;
-}
-// the value of half-wavefront `hl` (rows 2hl and 2hl + 1) combined from the row results
-__device__ __forceinline__ uint32_t half_max_u(uint32_t rowv, int hl) {
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)rowv, 48);
-    return hl ? max(c, d) : max(a, b);
-}
-__device__ __forceinline__ int half_min_i(int rowv, int hl) {
-    const int a = __builtin_amdgcn_readlane(rowv, 0), b = __builtin_amdgcn_readlane(rowv, 16);
-    const int c = __builtin_amdgcn_readlane(rowv, 32), d = __builtin_amdgcn_readlane(rowv, 48);
-    return hl ? min(c, d) : min(a, b);
-}
-__device__ __forceinline__ int half_sum_i(int rowv, int hl) {
-    const int a = __builtin_amdgcn_readlane(rowv, 0), b = __builtin_amdgcn_readlane(rowv, 16);
-    const int c = __builtin_amdgcn_readlane(rowv, 32), d = __builtin_amdgcn_readlane(rowv, 48);
-    return hl ? c + d : a + b;
+// Both rows' values of this lane's row pair (rows 0/1 and 2/3, the two half-wavefronts):
+// v_permlane16_swap of v with itself returns the even row's value and the odd row's value in
+// every lane of the pair, so a half-wavefront reduction is a row reduction and one swap, with no
+// round trip through scalar registers.
+__device__ __forceinline__ void hy_row_pair(uint32_t v, uint32_t& even, uint32_t& odd) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    even = r[0], odd = r[1];
 }
 
 // Q8_K of two 256-element blocks (quantize_q8k, src/kernels.c:128-165) held 8 consecutive
 // elements per lane: lanes 0..31 hold dst[0]'s elements 8l..8l+7, lanes 32..63 dst[1]'s.
+// The block's maximum magnitude (|x| bits, as the unsigned integers order them) by a row
+// reduction and a row-pair swap; its first element by a ballot of the lanes holding one (the
+// lowest such lane, then its lowest element).
 __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int lane) {
     const int hl = lane >> 5, jl = lane & 31;
-    uint32_t m = 0;
+    uint32_t ab[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) m = max(m, hy_fbits(e[i]) & 0x7fffffffu);
-    const uint32_t am = half_max_u(row_max_u(m), hl);
-    int f = 256;
+    for (int i = 0; i < 8; i++) ab[i] = hy_fbits(e[i]) & 0x7fffffffu;
+    uint32_t m = max(max(max(ab[0], ab[1]), max(ab[2], ab[3])), max(max(ab[4], ab[5]), max(ab[6], ab[7])));
+    uint32_t me, mo;
+    hy_row_pair(row_max_u(m), me, mo);
+    const uint32_t am = max(me, mo);
+    int li = 8;  // this lane's first element of magnitude am
 #pragma unroll
-    for (int i = 7; i >= 0; i--)
-        if ((hy_fbits(e[i]) & 0x7fffffffu) == am) f = 8 * jl + i;
-    const int frow = row_min_i(f);
-    const int first0 = half_min_i(frow, 0), first1 = half_min_i(frow, 1);
-    const int fi = (hl ? first1 : first0) & 7;
+    for (int i = 7; i >= 0; i--) li = ab[i] == am ? i : li;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(li < 8);  // each half has one: am is one of its values
+    const int l0 = __builtin_ctz((uint32_t)hit), l1 = 32 + __builtin_ctz((uint32_t)(hit >> 32));
     float cand = e[0];
 #pragma unroll
-    for (int i = 1; i < 8; i++) cand = fi == i ? e[i] : cand;
-    const float vm0 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), first0 >> 3));
-    const float vm1 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), 32 + (first1 >> 3)));
+    for (int i = 1; i < 8; i++) cand = li == i ? e[i] : cand;
+    const float vm0 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), l0));
+    const float vm1 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), l1));
     const float vmax = hl ? vm1 : vm0;
     const bool zero = am == 0;
     const float iscale = zero ? 0.f : -127.f / vmax;
@@ -85,7 +74,9 @@ __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int 
     }
     const int s8 = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
     const int s16 = s8 + hy_dpp<HY_DPP_QSWAP1>(s8);  // lanes 2k, 2k+1 hold one 16-element group
-    const int total = half_sum_i(hy_group_sum<16>(s8), hl);
+    uint32_t te, to;
+    hy_row_pair((uint32_t)hy_group_sum<16>(s8), te, to);
+    const int total = (int)(te + to);
     uint32_t p[2];
 #pragma unroll
     for (int w = 0; w < 2; w++)
@@ -189,24 +180,33 @@ __device__ __forceinline__ WSeg load_wseg(int kind, const uint8_t* w, const uint
     return S;
 }
 
+// The panel segment's exact int32 block dot enc (reduced over the block's four lanes), and the
+// fp32 term made from it (src/kernels.c:576): mv1_term for KIND_PANEL in two steps, so that the
+// dot can run before the activation's d and sum are final.
+__device__ __forceinline__ int mv1_panel_enc(const WSeg& S, const ActSeg& A) {
+    const uint32_t w4[4] = {S.a.x, S.a.y, S.a.z, S.a.w};
+    const int4 qa[4] = {A.q0, A.q1, A.q2, A.q3};
+    int p = 0;
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        p = hy_dot4(hy_field(w4[0], l), qa[l].x, p);
+        p = hy_dot4(hy_field(w4[1], l), qa[l].y, p);
+        p = hy_dot4(hy_field(w4[2], l), qa[l].z, p);
+        p = hy_dot4(hy_field(w4[3], l), qa[l].w, p);
+    }
+    return hy_quad_sum(p);
+}
+__device__ __forceinline__ float mv1_panel_term(const WSeg& S, int enc, float d, int sum, int pshift, int poff) {
+    return hy_bitsf(S.sd) * d * (float)((enc << pshift) - poff * sum);
+}
+
 // fp32 block term of one segment, valid in the lane with sub == 0 of each block. Every lane of
 // the block must call it (DPP group reductions).
 template <int KIND>
 __device__ __forceinline__ float mv1_term(const WSeg& S, const ActSeg& A, int sub, int pshift, int poff) {
     if (KIND == KIND_PANEL) {
-        const uint32_t w4[4] = {S.a.x, S.a.y, S.a.z, S.a.w};
-        const int4 qa[4] = {A.q0, A.q1, A.q2, A.q3};
-        int p = 0;
-#pragma unroll
-        for (int l = 0; l < 4; l++) {
-            p = hy_dot4(hy_field(w4[0], l), qa[l].x, p);
-            p = hy_dot4(hy_field(w4[1], l), qa[l].y, p);
-            p = hy_dot4(hy_field(w4[2], l), qa[l].z, p);
-            p = hy_dot4(hy_field(w4[3], l), qa[l].w, p);
-        }
-        const int enc = hy_quad_sum(p);
         // src/kernels.c:576: ps * y.d * float((enc << shift) - off * sum)
-        return hy_bitsf(S.sd) * A.d * (float)((enc << pshift) - poff * A.sum);
+        return mv1_panel_term(S, mv1_panel_enc(S, A), A.d, A.sum, pshift, poff);
     } else if (KIND == KIND_Q4K) {
         const uint32_t w4[4] = {S.a.x, S.a.y, S.a.z, S.a.w};
         int s0 = 0, s1 = 0;
