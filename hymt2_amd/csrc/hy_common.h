@@ -88,28 +88,6 @@ __device__ inline unsigned long long argmax_key(float v, int idx) {
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
 }
 
-__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
-    for (int o = 32; o >= 1; o >>= 1) {
-        const unsigned long long w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
-    return v;
-}
-
-// The greedy argmax key of a workgroup (the maximum of every thread's key) into *slot, written by
-// thread 0: one slot per workgroup, reduced by the step's finishing kernel, so no two workgroups
-// write one address (same-address atomics from a whole grid serialize). Every thread calls it.
-__device__ inline void hy_wg_slot_max(unsigned long long key, unsigned long long* slot) {
-    __shared__ unsigned long long wk[16];
-    key = wave_max_u64(key);
-    const int nw = (blockDim.x + 63) >> 6;
-    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = key;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < nw; w++) key = wk[w] > key ? wk[w] : key;
-        *slot = key;
-    }
-}
 
 __device__ __forceinline__ void hy_lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -137,39 +115,92 @@ __device__ inline int hy_group_sum(int v) {
     return v;
 }
 
-// Whole-wave reductions: DPP inside each 16-lane row, then the four row results through
-// readlane. The result is wave-uniform. Requires all 64 lanes active.
+// Both rows' values of this lane's row pair (rows 0/1 and 2/3, the two half-wavefronts):
+// v_permlane16_swap of v with itself returns the even row's value and the odd row's value in
+// every lane of the pair.
+__device__ __forceinline__ void hy_row_pair(uint32_t v, uint32_t& even, uint32_t& odd) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    even = r[0], odd = r[1];
+}
+// Both halves' values at this lane's position (v_permlane32_swap of v with itself).
+__device__ __forceinline__ void hy_half_pair(uint32_t v, uint32_t& lo, uint32_t& hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    lo = r[0], hi = r[1];
+}
+
+// Whole-wave reductions of an exact, order-free operation: DPP inside each 16-lane row, then the
+// row pairs and the halves by the two permlane swaps, with no round trip through scalar
+// registers (or LDS, as a shuffle would take). Every lane receives the result. Requires all 64
+// lanes active.
+template <typename Op>
+__device__ __forceinline__ uint32_t hy_wave_reduce(uint32_t x, Op op) {
+    x = op(x, (uint32_t)hy_dpp<HY_DPP_QSWAP1>((int)x));
+    x = op(x, (uint32_t)hy_dpp<HY_DPP_QSWAP2>((int)x));
+    x = op(x, (uint32_t)hy_dpp<HY_DPP_HMIRROR>((int)x));
+    x = op(x, (uint32_t)hy_dpp<HY_DPP_MIRROR>((int)x));
+    uint32_t a, b;
+    hy_row_pair(x, a, b);
+    x = op(a, b);
+    hy_half_pair(x, a, b);
+    return op(a, b);
+}
+
 __device__ inline int hy_wave_sum_i(int v) {
-    v = hy_group_sum<16>(v);
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-           __builtin_amdgcn_readlane(v, 48);
+    return (int)hy_wave_reduce((uint32_t)v, [](uint32_t a, uint32_t b) { return a + b; });
 }
 
 __device__ inline uint32_t hy_wave_max_u(uint32_t v) {
-    int x = (int)v;
-    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP1>(x));
-    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP2>(x));
-    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_HMIRROR>(x));
-    x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane(x, 0), b = (uint32_t)__builtin_amdgcn_readlane(x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane(x, 32), d = (uint32_t)__builtin_amdgcn_readlane(x, 48);
-    return max(max(a, b), max(c, d));
+    return hy_wave_reduce(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
 }
 
 __device__ inline int hy_wave_min_i(int x) {
-    x = min(x, hy_dpp<HY_DPP_QSWAP1>(x));
-    x = min(x, hy_dpp<HY_DPP_QSWAP2>(x));
-    x = min(x, hy_dpp<HY_DPP_HMIRROR>(x));
-    x = min(x, hy_dpp<HY_DPP_MIRROR>(x));
-    const int a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
-    const int c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
-    return min(min(a, b), min(c, d));
+    return (int)hy_wave_reduce((uint32_t)x, [](uint32_t a, uint32_t b) { return (int)a < (int)b ? a : b; });
 }
 
 __device__ inline float hy_wave_max(float v) {
     // fmax is exact and order-free; NaN-free inputs assumed
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return __builtin_bit_cast(float, hy_wave_reduce(__builtin_bit_cast(uint32_t, v), [](uint32_t a, uint32_t b) {
+        return __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)));
+    }));
+}
+
+__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
+    // the same DPP row steps and permlane swaps as hy_wave_reduce, on both 32-bit halves
+    uint32_t hi = (uint32_t)(v >> 32), lo = (uint32_t)v;
+    auto take = [&](uint32_t h2, uint32_t l2) __attribute__((always_inline)) {
+        const bool gt = h2 > hi || (h2 == hi && l2 > lo);
+        hi = gt ? h2 : hi;
+        lo = gt ? l2 : lo;
+    };
+    take((uint32_t)hy_dpp<HY_DPP_QSWAP1>((int)hi), (uint32_t)hy_dpp<HY_DPP_QSWAP1>((int)lo));
+    take((uint32_t)hy_dpp<HY_DPP_QSWAP2>((int)hi), (uint32_t)hy_dpp<HY_DPP_QSWAP2>((int)lo));
+    take((uint32_t)hy_dpp<HY_DPP_HMIRROR>((int)hi), (uint32_t)hy_dpp<HY_DPP_HMIRROR>((int)lo));
+    take((uint32_t)hy_dpp<HY_DPP_MIRROR>((int)hi), (uint32_t)hy_dpp<HY_DPP_MIRROR>((int)lo));
+    uint32_t h0, h1, l0, l1;
+    hy_row_pair(hi, h0, h1);
+    hy_row_pair(lo, l0, l1);
+    hi = h0, lo = l0;
+    take(h1, l1);
+    hy_half_pair(hi, h0, h1);
+    hy_half_pair(lo, l0, l1);
+    hi = h0, lo = l0;
+    take(h1, l1);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// The greedy argmax key of a workgroup (the maximum of every thread's key) into *slot, written by
+// thread 0: one slot per workgroup, reduced by the step's finishing kernel, so no two workgroups
+// write one address (same-address atomics from a whole grid serialize). Every thread calls it.
+__device__ inline void hy_wg_slot_max(unsigned long long key, unsigned long long* slot) {
+    __shared__ unsigned long long wk[16];
+    key = wave_max_u64(key);
+    const int nw = (blockDim.x + 63) >> 6;
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < nw; w++) key = wk[w] > key ? wk[w] : key;
+        *slot = key;
+    }
 }
 
 // 4 bytes of 2-bit codes in field l of each byte of w, as 4 unsigned bytes 0..3.

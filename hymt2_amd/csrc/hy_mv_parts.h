@@ -30,15 +30,6 @@ __device__ __forceinline__ uint32_t row_max_u(uint32_t v) {
     x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
     return (uint32_t)x;
 }
-// Both rows' values of this lane's row pair (rows 0/1 and 2/3, the two half-wavefronts):
-// v_permlane16_swap of v with itself returns the even row's value and the odd row's value in
-// every lane of the pair, so a half-wavefront reduction is a row reduction and one swap, with no
-// round trip through scalar registers.
-__device__ __forceinline__ void hy_row_pair(uint32_t v, uint32_t& even, uint32_t& odd) {
-    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    even = r[0], odd = r[1];
-}
-
 // Q8_K of two 256-element blocks (quantize_q8k, src/kernels.c:128-165) held 8 consecutive
 // elements per lane: lanes 0..31 hold dst[0]'s elements 8l..8l+7, lanes 32..63 dst[1]'s.
 // The block's maximum magnitude (|x| bits, as the unsigned integers order them) by a row
