@@ -282,6 +282,14 @@ def config4(b):
     if not (np.array_equal(f["prompt"], prompt) and np.array_equal(ids[:len(f["greedy"])], f["greedy"])):
         raise RuntimeError("config 4: greedy ids differ from the reference's (tests/golden/baseline_config4.npz)")
     _, st1 = fm.generate_device(prompt, 2, chunk=1)          # the same prompt one position per step
+    depth = b.prefill_pipeline(1)                            # chunks one after another
+    try:
+        fm.generate_device(prompt[:chunk + 5], 2, chunk=chunk)
+        ids_seq, st_seq = fm.generate_device(prompt, 2, chunk=chunk)
+    finally:
+        b.prefill_pipeline(depth)
+    if ids_seq[0] != ids[0]:
+        raise RuntimeError("config 4: the pipelined and the one-chunk-after-another prefill disagree")
     weights = sum(L[nm].n * L[nm].k for L in model["layers"] for nm in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"))
     ops = 2.0 * weights * n_prompt
     pre_s = st.prefill_ms / 1e3
@@ -293,7 +301,11 @@ def config4(b):
     return dict(workload=f"config4: Hy-MT2-1.8B-shaped Q2_0C, {n_prompt}-token random prompt in {chunk}-token "
                          f"chunks, then {n_gen} greedy tokens (device loop)",
                 greedy_parity=f"first {len(f['greedy'])} ids identical to the reference's gen_ids at ISA scalar",
+                prefill_schedule=f"{chunk}-token chunks pipelined over the layers, up to {depth} in flight "
+                                 f"(chunk i's layer l in the launches of chunk i + 1's layer l - 1; the same bits "
+                                 f"as one chunk after another)",
                 prefill_tok_s=round(n_prompt / pre_s, 1), prefill_ms=round(st.prefill_ms, 3),
+                prefill_sequential_tok_s=round(n_prompt / (st_seq.prefill_ms / 1e3), 1),
                 prefill_int8_ops=int(ops), prefill_mfma_util=round(ops / pre_s / 1e12 / INT8_PEAK_TOPS, 4),
                 prefill_stepwise_tok_s=round(st1.prefill_steps / (st1.prefill_ms / 1e3), 1),
                 decode_tok_s=round(dec_tok_s, 2), decode_bytes_per_token=int(tok_bytes),

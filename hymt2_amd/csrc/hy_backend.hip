@@ -98,6 +98,10 @@ struct Fused {
     hipGraphExec_t g_fwd[2] = {nullptr, nullptr}, g_step[2] = {nullptr, nullptr};
     hipGraphExec_t g_steps[2] = {nullptr, nullptr};  // kStepsPerGraph steps of the device loop in one graph
     std::vector<const void*> sig_fwd[2], sig_step;
+    // chunk slots of the pipelined prefill (allocated on first use): kPipeMax slots of
+    // HY_MAX_CHUNK token rows each, slot-major
+    float *p_h = nullptr, *p_q = nullptr, *p_k = nullptr, *p_v = nullptr, *p_ao = nullptr, *p_g = nullptr;
+    HyQ8K *p_act_h = nullptr, *p_act_q = nullptr, *p_act_f = nullptr;
     float* norm_ptr(int li, int which) const {  // 0 attn, 1 ffn, 2 q, 3 k
         const size_t per = 2 * (size_t)hidden + 2 * (size_t)hdim;
         float* base = norms + per * li;
@@ -118,6 +122,7 @@ struct Ctx {
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     uint8_t* scratch = nullptr;  // this device's address of `scratch` (hymt2_hip_matmul_static), or null
     int split_from = kSplitFromDefault;  // single-token attention at positions >= this: split form
+    int pipe_depth = kPipeMax;           // chunks in flight in gen_prefill (1: one chunk after another)
 };
 
 // Whether the single-token forward at position pos uses the split attention: long rows, and
@@ -584,8 +589,10 @@ static void free_graphs(Fused* f) {
 static void free_fused(Fused* f) {
     if (!f) return;
     free_graphs(f);
-    void* dev[] = {f->in_dev, f->q, f->k, f->v, f->ao, f->g, f->u, f->logits, f->act_h, f->act_q, f->act_f,
-                   f->rope_c, f->rope_s, f->out_norm, f->norms, f->kc, f->vc, f->slots, f->ids, f->sc, f->segmax};
+    void* dev[] = {f->in_dev,  f->q,       f->k,       f->v,       f->ao,    f->g,       f->u,     f->logits,
+                   f->act_h,   f->act_q,   f->act_f,   f->rope_c,  f->rope_s, f->out_norm, f->norms, f->kc,
+                   f->vc,      f->slots,   f->ids,     f->sc,      f->segmax, f->p_h,     f->p_q,   f->p_k,
+                   f->p_v,     f->p_ao,    f->p_g,     f->p_act_h, f->p_act_q, f->p_act_f};
     for (void* p : dev)
         if (p) (void)hipFree(p);
     if (f->in_host) (void)hipHostFree(f->in_host);
@@ -834,7 +841,8 @@ static bool enqueue_layers(Ctx* c, const hymt2_fused_args* a, int nt, int pos0, 
 // Output RMSNorm + LM head on the last token (src/model.c:887-900), optionally folding the
 // greedy argmax into f->slots (one key per workgroup of the head kernel; f->head_slots of them).
 // Quantized heads run on the decode matvec over the Q8_K of the normalized last token.
-static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax, int vocab_out) {
+static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax, int vocab_out,
+                         const float* h_last = nullptr) {
     Fused* f = c->f;
     const DW* ow = dw(a->outw);
     if (!ow || ow->mw.k != f->hidden) {
@@ -842,7 +850,7 @@ static bool enqueue_head(Ctx* c, const hymt2_fused_args* a, int nt, bool argmax,
         return false;
     }
     if (!ensure_logits(c, f, ow->mw.n)) return false;
-    const float* hl = f->d_h + (size_t)(nt - 1) * f->hidden;
+    const float* hl = h_last ? h_last : f->d_h + (size_t)(nt - 1) * f->hidden;
     if (ow->mw.kind == KIND_F16 || ow->mw.kind == KIND_F32 || ow->mw.kind == KIND_Q8_0) {
         HeadArgs h{};
         h.W = ow->mw;
@@ -1190,6 +1198,147 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
     return 0;
 }
 
+// Whether the pipelined prefill applies: panel weights of the model's shapes in every layer
+// (the GEMM), gate and up pairable, hidden 2048 (its RMSNorm kernel) and the chunk attention
+// kernel with its fused Q8_K output.
+static bool pipe_supported(const Fused* f, const hymt2_fused_args* a) {
+    if (f->hidden != 2048) return false;
+    AttnArgs at{};
+    at.heads = f->heads;
+    at.kv_heads = f->kv_heads;
+    at.hdim = f->hdim;
+    at.ctx = f->ctx;
+    if (!attention_quantizes(at)) return false;
+    auto panel = [](const DW* w, int n, int k) { return w && w->mw.kind == KIND_PANEL && w->mw.n == n && w->mw.k == k; };
+    for (int li = 0; li < a->n_layer; li++) {
+        const hymt2_fused_layer& L = a->layers[li];
+        const int H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
+        if (!panel(dw(L.wq), Q, H) || !panel(dw(L.wk), KV, H) || !panel(dw(L.wv), KV, H) || !panel(dw(L.wo), H, Q) ||
+            !panel(dw(L.wg), F, H) || !panel(dw(L.wu), F, H) || !panel(dw(L.wd), H, F))
+            return false;
+    }
+    return true;
+}
+
+static bool ensure_pipe(Ctx* c, Fused* f) {
+    if (f->p_h) return true;
+    const size_t R = (size_t)kPipeMax * HY_MAX_CHUNK, H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
+    return dalloc(c, &f->p_h, R * H * 4) && dalloc(c, &f->p_q, R * Q * 4) && dalloc(c, &f->p_k, R * KV * 4) &&
+           dalloc(c, &f->p_v, R * KV * 4) && dalloc(c, &f->p_ao, R * Q * 4) && dalloc(c, &f->p_g, R * F * 4) &&
+           dalloc(c, &f->p_act_h, R * (H / 256) * sizeof(HyQ8K)) && dalloc(c, &f->p_act_q, R * (Q / 256) * sizeof(HyQ8K)) &&
+           dalloc(c, &f->p_act_f, R * (F / 256) * sizeof(HyQ8K));
+}
+
+// The prompt of the device loop in chunks, pipelined over the layers: within a group of up to
+// pipe_depth chunks (slot i = chunk g0 + i), launch step st runs layer st - i of every chunk i
+// with 0 <= st - i < n_layer, each kernel of the layer once for all of them. Chunk i at layer l
+// needs its own layer l - 1 (step st - 1) and the K/V that chunks before it stored at layer l
+// (chunk i - 1 at step st - 1), so every chunk is the same forward over the same cache as in
+// the one-after-another order, and the results are the same bits. Leaves the last token's
+// hidden state in its slot for the head.
+static bool enqueue_prefill_pipe(Ctx* c, const hymt2_fused_args* a, int chunk, const float** h_last) {
+    Fused* f = c->f;
+    const int np = f->gen_prompt, nl = f->n_layer, depth = c->pipe_depth;
+    const int nc = (np + chunk - 1) / chunk;
+    const int H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
+    const size_t B = HY_MAX_CHUNK;
+    for (int g0 = 0; g0 < nc; g0 += depth) {
+        const int m = std::min(depth, nc - g0);
+        auto tokens = [&](int i) { return std::min(chunk, np - (g0 + i) * chunk); };
+        for (int i = 0; i < m; i++)
+            HIPCHK(c, launch_embed_rows(f->ids, (g0 + i) * chunk, tokens(i), f->gen_embd, f->p_h + i * B * H, H, c->s));
+        for (int st = 0; st < m + nl - 1; st++) {
+            const int i0 = std::max(0, st - nl + 1), i1 = std::min(m - 1, st);
+            const int nj = i1 - i0 + 1;
+            PipeNorm n1{}, n2{};
+            PipeAttn pa{};
+            PipeQuant pq{};
+            GemmPipeLaunch gq{}, go{}, gu{}, gd{};
+            int rows = 0;
+            for (int j = 0; j < nj; j++) {
+                const int i = i0 + j, li = st - i, nt = tokens(i);
+                const hymt2_fused_layer& L = a->layers[li];
+                float* h = f->p_h + i * B * H;
+                float* q = f->p_q + i * B * Q;
+                float* k = f->p_k + i * B * KV;
+                float* v = f->p_v + i * B * KV;
+                float* g = f->p_g + i * B * F;
+                HyQ8K* ah = f->p_act_h + i * B * (H / 256);
+                HyQ8K* aq = f->p_act_q + i * B * (Q / 256);
+                HyQ8K* af = f->p_act_f + i * B * (F / 256);
+                n1.h[j] = n2.h[j] = h;
+                n1.w[j] = f->norm_ptr(li, 0);
+                n2.w[j] = f->norm_ptr(li, 1);
+                n1.act[j] = n2.act[j] = ah;
+                n1.row0[j] = n2.row0[j] = pa.row0[j] = pq.row0[j] = rows;
+                auto job = [&](GemmPipeLaunch& G, hy_dweight* w, float* out, int ldo, int epi, const HyQ8K* act) {
+                    GemmJob& J = G.job[G.njobs++];
+                    J.W = dw(w)->mw;
+                    J.out = out;
+                    J.ldo = ldo;
+                    J.epi = epi;
+                    J.act = act;
+                    J.nt = nt;
+                };
+                job(gq, L.wq, q, Q, EPI_STORE, ah);
+                job(gq, L.wk, k, KV, EPI_STORE, ah);
+                job(gq, L.wv, v, KV, EPI_STORE, ah);
+                job(go, L.wo, h, H, EPI_ADD, aq);
+                job(gu, L.wg, g, F, EPI_STORE, ah);  // pair: silu(gate) * up into g
+                job(gu, L.wu, g, F, EPI_STORE, ah);
+                job(gd, L.wd, h, H, EPI_ADD, af);
+                AttnArgs& at = pa.a[j];
+                at.q = q;
+                at.k = k;
+                at.v = v;
+                at.kc = f->kc + (size_t)li * f->ctx * KV;
+                at.vc = f->vc + (size_t)li * f->ctx * KV;
+                at.ao = f->p_ao + i * B * Q;
+                at.q_norm = f->norm_ptr(li, 2);
+                at.k_norm = f->norm_ptr(li, 3);
+                at.rope_cos = f->rope_c;
+                at.rope_sin = f->rope_s;
+                at.pos0 = (g0 + i) * chunk;
+                at.nt = nt;
+                at.heads = f->heads;
+                at.kv_heads = f->kv_heads;
+                at.hdim = f->hdim;
+                at.rope_half = f->rope_half;
+                at.ctx = f->ctx;
+                at.eps = f->eps;
+                at.act_out = aq;
+                pq.x[j] = g;
+                pq.act[j] = af;
+                rows += nt;
+            }
+            n1.njobs = n2.njobs = pa.njobs = pq.njobs = nj;
+            n1.eps = n2.eps = f->eps;
+            pq.ldx = F;
+            pq.K = F;
+            gu.pair = 1;
+            HIPCHK(c, launch_rmsnorm_q8k(n1, rows, c->s));
+            HIPCHK(c, launch_gemm_panel(gq, c->s));
+            HIPCHK(c, launch_rope_norm_store(pa, rows, c->s));
+            HIPCHK(c, launch_attention(pa, rows, c->s));
+            HIPCHK(c, launch_gemm_panel(go, c->s));
+            HIPCHK(c, launch_rmsnorm_q8k(n2, rows, c->s));
+            HIPCHK(c, launch_gemm_panel(gu, c->s));
+            HIPCHK(c, launch_quantize_q8k(pq, rows, c->s));
+            HIPCHK(c, launch_gemm_panel(gd, c->s));
+        }
+        if (g0 + m == nc) *h_last = f->p_h + (m - 1) * B * H + (size_t)(tokens(m - 1) - 1) * H;
+    }
+    return true;
+}
+
+int hymt2_hip_prefill_pipeline(void* impl, int depth) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c) return -1;
+    const int prev = c->pipe_depth;
+    if (depth >= 1) c->pipe_depth = std::min(depth, kPipeMax);
+    return prev;
+}
+
 int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) {
     Ctx* c = static_cast<Ctx*>(impl);
     if (!c || c->broken || !c->f || !c->f->gen_total || !shape || !shape->layers) return -1;
@@ -1204,13 +1353,22 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
         return -2;
     }
     const int np = f->gen_prompt;
-    for (int i = 0; i < np; i += chunk) {
-        const int nt = std::min(chunk, np - i);
-        if (launch_embed_rows(f->ids, i, nt, f->gen_embd, f->d_h, f->hidden, c->s) != hipSuccess ||
-            !enqueue_layers(c, shape, nt, i, nullptr, nt == 1 && split_at(c, f, i)) ||
-            (i + nt == np && !enqueue_head(c, shape, nt, true, f->gen_vocab))) {
+    if (chunk > 1 && np > chunk && c->pipe_depth > 1 && pipe_supported(f, shape)) {
+        const float* h_last = nullptr;
+        if (!ensure_pipe(c, f) || !enqueue_prefill_pipe(c, shape, chunk, &h_last) ||
+            !enqueue_head(c, shape, 1, true, f->gen_vocab, h_last)) {
             c->broken = true;
             return -3;
+        }
+    } else {
+        for (int i = 0; i < np; i += chunk) {
+            const int nt = std::min(chunk, np - i);
+            if (launch_embed_rows(f->ids, i, nt, f->gen_embd, f->d_h, f->hidden, c->s) != hipSuccess ||
+                !enqueue_layers(c, shape, nt, i, nullptr, nt == 1 && split_at(c, f, i)) ||
+                (i + nt == np && !enqueue_head(c, shape, nt, true, f->gen_vocab))) {
+                c->broken = true;
+                return -3;
+            }
         }
     }
     // position np - 1 has been processed: the finishing kernel records the first generated id,

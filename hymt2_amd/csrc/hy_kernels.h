@@ -115,19 +115,30 @@ struct GemmJob {
     int ldo;
     int epi;         // EPI_STORE / EPI_ADD
     int tile_begin;  // first row tile of this job in the grid (set by the launcher)
+    const HyQ8K* act;  // this job's activations [nt][nb] (null: the launch's act and nt)
+    int nt;
 };
 
-struct GemmLaunch {
-    GemmJob job[kMaxJobs];
+// Chunks in flight in the pipelined prefill (hymt2_hip_gen_prefill): the chunk kernels and the
+// GEMM take tables of up to this many chunks (the GEMM three weights each) in one launch.
+constexpr int kPipeMax = 8;
+constexpr int kGemmPipeJobs = 3 * kPipeMax;
+
+template <int NJ>
+struct GemmLaunchT {
+    GemmJob job[NJ];
     int njobs;
-    int pair;              // job[0] = gate, job[1] = up of equal shape: job[0].out = silu(g) * u
+    int pair;              // jobs (2p, 2p + 1) = gate, up of equal shape: job[2p].out = silu(g) * u
     int nt;
     const HyQ8K* act;      // [nt][nb]
     int nb;                // set by the launcher
 };
+using GemmLaunch = GemmLaunchT<kMaxJobs>;
+using GemmPipeLaunch = GemmLaunchT<kGemmPipeJobs>;
 // hipErrorNotSupported for weights that are not panels of one K (the caller then uses
 // launch_matvec).
 hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s);
+hipError_t launch_gemm_panel(GemmPipeLaunch& L, hipStream_t s);
 
 struct AttnArgs {
     float* q;              // [nt][qdim]
@@ -151,6 +162,42 @@ hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s);
 bool attention_quantizes(const AttnArgs& a);
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+// Several chunks in one launch (the pipelined prefill): job j owns the grid's token rows
+// row0[j] .. row0[j] + nt_j - 1 (row0[0] = 0, increasing); each workgroup finds its job by row.
+struct PipeAttn {
+    AttnArgs a[kPipeMax];
+    int row0[kPipeMax];
+    int njobs;
+};
+struct PipeNorm {
+    const float* h[kPipeMax];  // [nt_j][2048]
+    const float* w[kPipeMax];  // norm weights [2048]
+    HyQ8K* act[kPipeMax];      // [nt_j][8]
+    int row0[kPipeMax];
+    int njobs;
+    float eps;
+};
+struct PipeQuant {
+    const float* x[kPipeMax];  // [nt_j][ldx]
+    HyQ8K* act[kPipeMax];      // [nt_j][K / 256]
+    int row0[kPipeMax];
+    int njobs, ldx, K;
+};
+// The job of grid row `row` in such a launch (uniform: scalar compares against the table).
+__device__ __forceinline__ int pipe_job(const int* row0, int njobs, int row) {
+    int j = 0;
+#pragma unroll
+    for (int q = 1; q < kPipeMax; q++)
+        if (q < njobs && row >= row0[q]) j = q;
+    return j;
+}
+// rows: the total token rows of the jobs. The attention form is the chunk kernel's only
+// (attention_quantizes() for every job, ctx within its LDS rows): hipErrorNotSupported otherwise.
+hipError_t launch_rope_norm_store(const PipeAttn& J, int rows, hipStream_t s);
+hipError_t launch_attention(const PipeAttn& J, int rows, hipStream_t s);
+hipError_t launch_rmsnorm_q8k(const PipeNorm& J, int rows, hipStream_t s);  // hidden 2048 only
+hipError_t launch_quantize_q8k(const PipeQuant& J, int rows, hipStream_t s);
 
 // Single-token attention, one workgroup per query head (k_attn1, hy_attn_decode.hip): RoPE
 // and RMSNorm of q and k, the bf16 KV store at the position, softmax attention over positions

@@ -58,9 +58,21 @@ __global__ __launch_bounds__(64) void k_quantize_q8k(const float* x, int ldx, Hy
     q8k_quantize_wave(x + (size_t)t * ldx + (size_t)b * HY_QK, act + (size_t)t * nb + b, threadIdx.x);
 }
 
+__global__ __launch_bounds__(64) void k_quantize_q8k_pipe(PipeQuant J) {
+    const int b = blockIdx.x, row = blockIdx.y;
+    const int j = pipe_job(J.row0, J.njobs, row), t = row - J.row0[j], nb = J.K / HY_QK;
+    q8k_quantize_wave(J.x[j] + (size_t)t * J.ldx + (size_t)b * HY_QK, J.act[j] + (size_t)t * nb + b, threadIdx.x);
+}
+
 hipError_t launch_quantize_q8k(const float* x, int ldx, HyQ8K* act, int K, int nt, hipStream_t s) {
     const int nb = K / HY_QK;
     k_quantize_q8k<<<dim3(nb, nt), 64, 0, s>>>(x, ldx, act, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8k(const PipeQuant& J, int rows, hipStream_t s) {
+    if (J.njobs < 1 || J.njobs > kPipeMax || J.K % HY_QK || rows < 1) return hipErrorInvalidValue;
+    k_quantize_q8k_pipe<<<dim3(J.K / HY_QK, rows), 64, 0, s>>>(J);
     return hipGetLastError();
 }
 
@@ -104,12 +116,11 @@ __device__ void quantize_lds_blocks(const float* xs, HyQ8K* act, int K) {
 // H = 2048, Q8_K output only: the decode matvec's prologue per token. Lane l of wavefront w
 // holds values 512 w + 8 l .. + 8: the workgroup-wide exact sum of squares, x * scale * w, then
 // each wavefront quantizes its two blocks.
-__global__ __launch_bounds__(256) void k_rmsnorm_q8k_2048(const float* h, const float* w, float eps,
-                                                          HyQ8K* act_out) {
+__device__ __forceinline__ void rmsnorm_q8k_2048_row(const float* hrow, const float* w, float eps, HyQ8K* act_row) {
     __shared__ HyExactLds ex;
-    const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int off = 512 * wave + 8 * lane;
-    const float* x = h + (size_t)t * 2048 + off;
+    const float* x = hrow + off;
     const float4 a0 = *reinterpret_cast<const float4*>(x), a1 = *reinterpret_cast<const float4*>(x + 4);
     const float4 u0 = *reinterpret_cast<const float4*>(w + off), u1 = *reinterpret_cast<const float4*>(w + off + 4);
     float e[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
@@ -118,7 +129,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm_q8k_2048(const float* h, const 
     const float scale = 1.0f / sqrtf(sum / 2048.0f + eps);
 #pragma unroll
     for (int i = 0; i < 8; i++) e[i] = e[i] * scale * nw[i];
-    q8k_quantize_halves(e, act_out + (size_t)t * 8 + 2 * wave, lane);
+    q8k_quantize_halves(e, act_row + 2 * wave, lane);
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_q8k_2048(const float* h, const float* w, float eps,
+                                                          HyQ8K* act_out) {
+    const int t = blockIdx.x;
+    rmsnorm_q8k_2048_row(h + (size_t)t * 2048, w, eps, act_out + (size_t)t * 8);
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_q8k_2048_pipe(PipeNorm J) {
+    const int row = blockIdx.x, j = pipe_job(J.row0, J.njobs, row), t = row - J.row0[j];
+    rmsnorm_q8k_2048_row(J.h[j] + (size_t)t * 2048, J.w[j], J.eps, J.act[j] + (size_t)t * 8);
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float* w, float eps, int H,
@@ -131,6 +153,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float* h, const float
     if (xn_out)
         for (int i = threadIdx.x; i < H; i += blockDim.x) xn_out[(size_t)t * H + i] = xs[i];
     if (act_out) quantize_lds_blocks(xs, act_out + (size_t)t * (H / HY_QK), H);
+}
+
+hipError_t launch_rmsnorm_q8k(const PipeNorm& J, int rows, hipStream_t s) {
+    if (J.njobs < 1 || J.njobs > kPipeMax || rows < 1) return hipErrorInvalidValue;
+    k_rmsnorm_q8k_2048_pipe<<<rows, 256, 0, s>>>(J);
+    return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_q8k(const float* h, const float* w, float eps, int H, int nt, float* xn_out,
@@ -454,11 +482,11 @@ hipError_t launch_matvec(const MvLaunch& L, int pro, int grid, hipStream_t s) {
 // One wavefront per (token, head-slot): slots [0, heads) are q heads, [heads, heads+kv_heads)
 // are kv heads. NeoX RoPE (src/model.c:754-765), then the per-head RMSNorm (src/model.c:840-841),
 // then for kv heads the bf16 RNE store of k and v at the absolute position (src/model.c:842-847).
-__global__ __launch_bounds__(64) void k_rope_norm_store(AttnArgs a) {
+__device__ __forceinline__ void rope_norm_store_row(const AttnArgs& a, int t, int slot) {
     __shared__ __align__(16) float row[256];
     __shared__ __align__(16) float sq[256];
     __shared__ float scale_slot;
-    const int t = blockIdx.x, slot = blockIdx.y, lane = threadIdx.x;
+    const int lane = threadIdx.x;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
     const int hd = a.hdim, half = a.rope_half;
     const bool is_q = slot < a.heads;
@@ -499,9 +527,26 @@ __global__ __launch_bounds__(64) void k_rope_norm_store(AttnArgs a) {
     }
 }
 
+__global__ __launch_bounds__(64) void k_rope_norm_store(AttnArgs a) { rope_norm_store_row(a, blockIdx.x, blockIdx.y); }
+
+__global__ __launch_bounds__(64) void k_rope_norm_store_pipe(PipeAttn J) {
+    const int row = blockIdx.x, j = pipe_job(J.row0, J.njobs, row);
+    rope_norm_store_row(J.a[j], row - J.row0[j], blockIdx.y);
+}
+
 hipError_t launch_rope_norm_store(const AttnArgs& a, hipStream_t s) {
     if (a.hdim > 256 || a.hdim % 4 || 2 * a.rope_half > a.hdim) return hipErrorInvalidValue;
     k_rope_norm_store<<<dim3(a.nt, a.heads + a.kv_heads), 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_norm_store(const PipeAttn& J, int rows, hipStream_t s) {
+    if (J.njobs < 1 || J.njobs > kPipeMax || rows < 1) return hipErrorInvalidValue;
+    const AttnArgs& a = J.a[0];
+    for (int j = 1; j < J.njobs; j++)
+        if (J.a[j].heads != a.heads || J.a[j].kv_heads != a.kv_heads || J.a[j].hdim != a.hdim) return hipErrorInvalidValue;
+    if (a.hdim > 256 || a.hdim % 4 || 2 * a.rope_half > a.hdim) return hipErrorInvalidValue;
+    k_rope_norm_store_pipe<<<dim3(rows, a.heads + a.kv_heads), 64, 0, s>>>(J);
     return hipGetLastError();
 }
 
@@ -629,7 +674,7 @@ constexpr int kAcMaxCtx = 2048;
 typedef unsigned v4u __attribute__((ext_vector_type(4)));  // arrays of it stay in registers
 
 template <int HD, int GRP>
-__global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
+__device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) {
     constexpr int NW = kAcThreads / 64;
     constexpr int KV4 = HD / 8;
     constexpr int DW = HD / 64;              // wavefronts per head in the output (one dim per lane)
@@ -643,7 +688,6 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
     __shared__ float inv_s[GRP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = blockIdx.x, t = blockIdx.y;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
     const int n = pos + 1;
     const int qdim = a.heads * HD;
@@ -792,11 +836,40 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
     }
 }
 
+template <int HD, int GRP>
+__global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
+    attn_chunk_row<HD, GRP>(a, blockIdx.x, blockIdx.y);
+}
+
+template <int HD, int GRP>
+__global__ __launch_bounds__(kAcThreads) void k_attn_chunk_pipe(PipeAttn J) {
+    const int row = blockIdx.y, j = pipe_job(J.row0, J.njobs, row);
+    attn_chunk_row<HD, GRP>(J.a[j], blockIdx.x, row - J.row0[j]);
+}
+
 bool attention_quantizes(const AttnArgs& a) {
     if (a.ctx > kAcMaxCtx || a.heads % a.kv_heads) return false;
     const int grp = a.heads / a.kv_heads;
     if (!((a.hdim == 128 || a.hdim == 64) && (grp == 4 || grp == 2))) return false;
     return grp * a.hdim % HY_QK == 0;
+}
+
+hipError_t launch_attention(const PipeAttn& J, int rows, hipStream_t s) {
+    if (J.njobs < 1 || J.njobs > kPipeMax || rows < 1) return hipErrorInvalidValue;
+    const AttnArgs& a = J.a[0];
+    for (int j = 0; j < J.njobs; j++) {
+        const AttnArgs& b = J.a[j];
+        if (b.heads != a.heads || b.kv_heads != a.kv_heads || b.hdim != a.hdim || !b.act_out || !attention_quantizes(b))
+            return hipErrorNotSupported;
+    }
+    const int grp = a.heads / a.kv_heads;
+    const dim3 grid(a.kv_heads, rows);
+    if (a.hdim == 128 && grp == 4) k_attn_chunk_pipe<128, 4><<<grid, kAcThreads, 0, s>>>(J);
+    else if (a.hdim == 128 && grp == 2) k_attn_chunk_pipe<128, 2><<<grid, kAcThreads, 0, s>>>(J);
+    else if (a.hdim == 64 && grp == 4) k_attn_chunk_pipe<64, 4><<<grid, kAcThreads, 0, s>>>(J);
+    else if (a.hdim == 64 && grp == 2) k_attn_chunk_pipe<64, 2><<<grid, kAcThreads, 0, s>>>(J);
+    else return hipErrorNotSupported;
+    return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {

@@ -23,6 +23,8 @@
 // pieces, panel bytes, token scales and sums, row block scales) land in a stage of an LDS ring
 // by direct global -> LDS loads, the next blocks' in flight while the current block's MFMAs
 // run.
+#include <algorithm>
+
 #include "hy_kernels.h"
 
 namespace hy {
@@ -100,8 +102,8 @@ struct GemmStage {
 // block pair. Set 0 keeps the running sum in block order; set 1 keeps its NBH fp32 block terms
 // in registers and, after set 0 hands its sums over through LDS, adds them in block order, so
 // each output is the same sequential sum as with KS = 1.
-template <int MT, int NT, int WR, int WT, bool PAIR, int RING, int KS = 1, int NBH = 0>
-__global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunch L) {
+template <int NJ, int MT, int NT, int WR, int WT, bool PAIR, int RING, int KS = 1, int NBH = 0>
+__global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ> L) {
     static_assert(WR * WT == kGemmThreads / 64, "4 wavefronts per workgroup (per K set)");
     static_assert(KS == 1 || (KS == 2 && NBH >= 1), "K split in two halves of NBH blocks");
     static_assert(!PAIR || MT == 2, "pair mode: one gate and one up tile per wavefront");
@@ -119,21 +121,23 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunch L) 
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
     const int half = KS == 2 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;  // K set
     const int wr = wave % WR, wt = wave / WR;
-    const int nb = L.nb, nt = L.nt;
+    const int nb = L.nb;
     const int nbh = KS == 2 ? NBH : nb;  // blocks of this K set, from block hb0
     const int hb0 = half * nbh;
-    const HyQ8K* const act = L.act;
 
-    // job of this row tile (uniform)
+    // job of this row tile (uniform; in pair mode only the gate jobs 2p carry tiles)
     int j = 0;
 #pragma unroll
-    for (int q = 1; q < kMaxJobs; q++)
+    for (int q = 1; q < NJ; q++)
         if (q < L.njobs && (int)blockIdx.x >= L.job[q].tile_begin) j = q;
     const int rows_wg = PAIR ? WR * 16 : SLOTS;
     const int row0 = ((int)blockIdx.x - L.job[j].tile_begin) * rows_wg;
     const int tokw = (int)blockIdx.y * TOK;  // first token of the workgroup
+    const HyQ8K* const act = L.job[j].act;  // a pair's gate and up share their tokens
+    const int nt = L.job[j].nt;
+    if (tokw >= nt) return;  // a shorter chunk of a pipelined launch (uniform)
 
-    auto slot_job = [&](int mt) { return PAIR ? mt : j; };
+    auto slot_job = [&](int mt) { return PAIR ? j + mt : j; };
     // weight row of local row slot s = w_r * MT * 16 + mt * 16 + rr
     auto slot_row = [&](int w_r, int mt, int rr) {
         return PAIR ? row0 + w_r * 16 + rr : row0 + w_r * MT * 16 + mt * 16 + rr;
@@ -376,47 +380,74 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunch L) 
     }
 }
 
-template <int MT, int NT, int WR, int WT, bool PAIR, int RING, int KS = 1, int NBH = 0>
-hipError_t gemm_go(GemmLaunch& L, hipStream_t s) {
+template <int NJ, int MT, int NT, int WR, int WT, bool PAIR, int RING, int KS = 1, int NBH = 0>
+hipError_t gemm_go(GemmLaunchT<NJ>& L, hipStream_t s) {
     const int rows_wg = PAIR ? WR * 16 : WR * MT * 16;
     int tiles = 0;
     for (int q = 0; q < L.njobs; q++) {
+        if (PAIR && q % 2) {
+            L.job[q].tile_begin = 1 << 30;  // an up job: never selected by tile index
+            continue;
+        }
         L.job[q].tile_begin = tiles;
-        if (!PAIR || q == 0) tiles += (L.job[q].W.n + rows_wg - 1) / rows_wg;
+        tiles += (L.job[q].W.n + rows_wg - 1) / rows_wg;
     }
-    if (PAIR) L.job[1].tile_begin = 1 << 30;  // never selected by tile index
     const int toks_wg = WT * NT * 16;
     const dim3 grid(tiles, (L.nt + toks_wg - 1) / toks_wg);
-    k_gemm_panel<MT, NT, WR, WT, PAIR, RING, KS, NBH><<<grid, kGemmThreads * KS, 0, s>>>(L);
+    k_gemm_panel<NJ, MT, NT, WR, WT, PAIR, RING, KS, NBH><<<grid, kGemmThreads * KS, 0, s>>>(L);
     return hipGetLastError();
 }
 
-}  // namespace
-
-hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s) {
-    if (L.njobs < 1 || L.njobs > kMaxJobs || L.nt < 1 || !L.act || (L.pair && L.njobs != 2)) return hipErrorInvalidValue;
+// Checks the jobs and completes the launch: per-job activations default to the launch's, L.nt
+// becomes the largest job's token count. A launch holds one K; in pair mode jobs (2p, 2p + 1)
+// are the gate and up weights of equal rows over the same tokens.
+template <int NJ>
+hipError_t gemm_prepare(GemmLaunchT<NJ>& L) {
+    if (L.njobs < 1 || L.njobs > NJ || (L.pair && L.njobs % 2)) return hipErrorInvalidValue;
     const int K = L.job[0].W.k;
     if (K % 256) return hipErrorNotSupported;
+    int ntmax = 0;
     for (int q = 0; q < L.njobs; q++) {
-        const MvWeight& W = L.job[q].W;
-        if (W.kind != KIND_PANEL || W.k != K || W.nb != K / 256 || W.n < 1 || !L.job[q].out) return hipErrorNotSupported;
+        GemmJob& J = L.job[q];
+        const MvWeight& W = J.W;
+        if (W.kind != KIND_PANEL || W.k != K || W.nb != K / 256 || W.n < 1 || !J.out) return hipErrorNotSupported;
+        if (!J.act) {
+            J.act = L.act;
+            J.nt = L.nt;
+        }
+        if (!J.act || J.nt < 1) return hipErrorInvalidValue;
+        if (L.pair && q % 2 && (W.n != L.job[q - 1].W.n || J.act != L.job[q - 1].act || J.nt != L.job[q - 1].nt))
+            return hipErrorNotSupported;
+        ntmax = std::max(ntmax, J.nt);
     }
-    if (L.pair && L.job[0].W.n != L.job[1].W.n) return hipErrorNotSupported;
+    L.nt = ntmax;
     L.nb = K / 256;
+    return hipSuccess;
+}
+
+template <int NJ>
+hipError_t gemm_dispatch(GemmLaunchT<NJ>& L, hipStream_t s) {
+    const hipError_t e = gemm_prepare(L);
+    if (e != hipSuccess) return e;
     // tiles and ring depths as measured fastest in chunked prefill (128 tokens): gate/up pairs in
     // 32-token tiles with two ring stages, the other contractions in the largest tile that still
     // gives a workgroup per CU (else the smallest) with three
     int rows = 0;
     for (int q = 0; q < L.njobs; q++)
-        if (!L.pair || q == 0) rows += L.job[q].W.n;
+        if (!L.pair || q % 2 == 0) rows += L.job[q].W.n;
     auto wgs = [&](int rt, int tt) { return ((rows + rt - 1) / rt) * ((L.nt + tt - 1) / tt); };
     // K = 2048 and 6144 (8 and 24 blocks) outside pair mode: K split in two inside the
     // workgroup (measured slower for the gate/up pairs)
-    if (L.pair) return gemm_go<2, 1, 2, 2, true, 2>(L, s);
-    if (wgs(64, 64) >= 256) return gemm_go<2, 2, 2, 2, false, 3>(L, s);
-    if (L.nb == 8) return gemm_go<1, 1, 2, 2, false, 3, 2, 4>(L, s);
-    if (L.nb == 24) return gemm_go<1, 1, 2, 2, false, 3, 2, 12>(L, s);
-    return gemm_go<1, 1, 2, 2, false, 3>(L, s);
+    if (L.pair) return gemm_go<NJ, 2, 1, 2, 2, true, 2>(L, s);
+    if (wgs(64, 64) >= 256) return gemm_go<NJ, 2, 2, 2, 2, false, 3>(L, s);
+    if (L.nb == 8) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 4>(L, s);
+    if (L.nb == 24) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 12>(L, s);
+    return gemm_go<NJ, 1, 1, 2, 2, false, 3>(L, s);
 }
+
+}  // namespace
+
+hipError_t launch_gemm_panel(GemmLaunch& L, hipStream_t s) { return gemm_dispatch(L, s); }
+hipError_t launch_gemm_panel(GemmPipeLaunch& L, hipStream_t s) { return gemm_dispatch(L, s); }
 
 }  // namespace hy

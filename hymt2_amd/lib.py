@@ -69,6 +69,7 @@ def load():
         "hymt2_hip_ffn_in": (i, [vp, vp, vp, vp, vp, C.c_float, vp]),
         "hymt2_hip_matmul_static": (C.c_bool, [vp, C.POINTER(vp), C.POINTER(vp), i, vp, i]),
         "hymt2_hip_attn_split_from": (i, [vp, i]),
+        "hymt2_hip_prefill_pipeline": (i, [vp, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -82,7 +83,7 @@ EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops",
            "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_selftest_sqsum", "hymt2_hip_generate", "hymt2_hip_gen_begin",
            "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in",
            "hymt2_hip_gen_prefill", "hymt2_hip_generate_chunked", "hymt2_hip_matmul_static",
-           "hymt2_hip_attn_split_from"]
+           "hymt2_hip_attn_split_from", "hymt2_hip_prefill_pipeline"]
 
 
 def abi_layout() -> dict:
@@ -112,6 +113,11 @@ class Backend:
         """Single-token forwards at positions >= pos use the split attention (-1: default)."""
         if self.L.hymt2_hip_attn_split_from(self.impl, pos) != 0:
             raise RuntimeError("hymt2_hip_attn_split_from failed")
+
+    def prefill_pipeline(self, depth: int) -> int:
+        """Chunks in flight in the device loop's chunked prefill (1: one after another; < 1:
+        query). Returns the previous depth."""
+        return int(self.L.hymt2_hip_prefill_pipeline(self.impl, depth))
 
     def last_error(self) -> str:
         buf = C.create_string_buffer(512)

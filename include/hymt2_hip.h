@@ -200,6 +200,16 @@ HYMT2_HIP_API int hymt2_hip_generate_chunked(void *impl, const hymt2_fused_args 
  * Drops the captured graphs (and ends a device loop in progress). 0 on success. */
 HYMT2_HIP_API int hymt2_hip_attn_split_from(void *impl, int from);
 
+/* Chunks in flight in hymt2_hip_gen_prefill (no counterpart in the reference interface; the
+ * reference runs one chunk after another, src/model.c:914-958). With depth > 1 a prompt of
+ * several chunks runs pipelined over the layers: chunk i's layer l in the same launches as
+ * chunk i + 1's layer l - 1, up to depth chunks at a time. Every chunk is the same forward over
+ * the same KV cache as in the one-after-another order, so the results are the same bits.
+ * Applies to panel-weight models with hidden 2048 and the chunk attention kernel's shapes;
+ * others run one chunk after another. depth 1 turns it off; depth < 1 only queries. Default
+ * and maximum 8. Returns the previous depth, or -1 without a context. */
+HYMT2_HIP_API int hymt2_hip_prefill_pipeline(void *impl, int depth);
+
 /* LM head on device pointers (enqueued on the context stream): logits[r] = row r of an
  * uploaded F16/F32 weight . rmsnorm(h; norm_w, eps), each row summed sequentially in the
  * reference's order (src/model.c:887-900, src/kernels.c:1279-1300). With key != NULL also

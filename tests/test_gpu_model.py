@@ -284,6 +284,33 @@ def test_full_size_model_short_run(backend, mode):
         fm.close()
 
 
+@pytest.mark.parametrize("mode", ["q2", "stq"])
+def test_pipelined_prefill_matches_sequential(backend, mode):
+    """The device loop's chunked prefill pipelined over the layers (up to 8 chunks in flight,
+    chunk i's layer l in the same launches as chunk i + 1's layer l - 1) against one chunk after
+    another and the oracle: a 300-token prompt in chunks of 33 (ten chunks, the last of 3
+    tokens), so the default depth runs a group of eight and a group of two, and depth 3 four
+    groups; greedy ids equal at every depth and equal the oracle's."""
+    shape = synth.ModelShape(n_layer=3, vocab=1000, ctx=320)
+    model = synth.make_model(shape, mode=mode, seed=59)
+    prompt = synth.rand_prompt(synth.rng(60), 300, shape.vocab)
+    want = O.OracleModel(model, threads=8).generate(prompt, 10, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        got = {}
+        for depth in (8, 3, 1):
+            prev = backend.prefill_pipeline(depth)
+            try:
+                got[depth], _ = fm.generate_device(prompt, 10, chunk=33)
+            finally:
+                backend.prefill_pipeline(prev)
+        for depth, ids in got.items():
+            assert np.array_equal(ids, want), f"depth={depth}"
+        assert backend.prefill_pipeline(0) == 8
+    finally:
+        fm.close()
+
+
 def test_full_size_chunked_prefill_config4(backend):
     """BASELINE config 4 at full size: the 1.8B Q2_0C model, a 1024-token prompt in 128-token
     chunks. The last position's logits equal those of a token-by-token prefill (single-token
