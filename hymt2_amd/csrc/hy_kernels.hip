@@ -841,9 +841,11 @@ __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
     attn_chunk_row<HD, GRP>(a, blockIdx.x, blockIdx.y);
 }
 
+// Rows run last to first: the jobs are chunks in position order, so the workgroups with the
+// longest rows start first and the short ones fill in behind them.
 template <int HD, int GRP>
 __global__ __launch_bounds__(kAcThreads) void k_attn_chunk_pipe(PipeAttn J) {
-    const int row = blockIdx.y, j = pipe_job(J.row0, J.njobs, row);
+    const int row = (int)(gridDim.y - 1 - blockIdx.y), j = pipe_job(J.row0, J.njobs, row);
     attn_chunk_row<HD, GRP>(J.a[j], blockIdx.x, row - J.row0[j]);
 }
 
