@@ -487,17 +487,17 @@ struct HyExactLdsT {
     float wtot[NW];            // estimate of each wavefront's total
     double ktot[NW];           // each wavefront's clean contributions
     int dcnt[NW];              // dirty segments of each wavefront
-    double rp[64 * NW];        // dirty rows of wavefront w from 64 w: the wavefront-local exclusive
-    alignas(16) float rv[64 * NW][8];  // prefix of clean contributions, and the 8 addends
+    double rp[128 * NW];       // dirty segments of wavefront w from 128 w: the wavefront-local
+    alignas(16) float rv[128 * NW][4];  // exclusive prefix of clean contributions, and the 4 addends
 };
 using HyExactLds = HyExactLdsT<4>;
 
 // The sequential fp32 sum of n = 512 * NW non-negative addends (SQ: the squares of the given
 // values), the workgroup's NW wavefronts holding 8 consecutive values per lane (lane l of
 // wavefront w: values 512w + 8l .. +8), bit for bit the one-lane loop. The same method as
-// hy_wave_exact_sq_sum_v with 8-addend segments, the estimates and the exact prefix sums
-// carried across wavefronts through LDS. The proof there holds unchanged up to n = 4096: the
-// float estimates and the sequential sum stay within 2^-12 of the exact prefix sums, inside
+// hy_wave_exact_sq_sum_v with two 4-addend segments per lane, the estimates and the exact prefix
+// sums carried across wavefronts through LDS. The proof there holds unchanged up to n = 4096:
+// the float estimates and the sequential sum stay within 2^-12 of the exact prefix sums, inside
 // the 2^-9 classification margin. Every thread of the workgroup must call it; all receive the
 // sum. It ends without a barrier: S must not be written again before the next workgroup barrier.
 template <int NW, bool SQ>
@@ -506,8 +506,10 @@ __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = SQ ? xv[i] * xv[i] : xv[i];
-    const float g = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    // 1. estimate of the running sum before this segment (float sums of non-negative values)
+    const float g0 = (v[0] + v[1]) + (v[2] + v[3]);
+    const float g1 = (v[4] + v[5]) + (v[6] + v[7]);
+    const float g = g0 + g1;
+    // 1. estimate of the running sum before this lane's values (float sums of non-negative values)
     const float estw = hy_wave_incl_scan(
         __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, g), 0x138, 0xF, 0xF, true)));
     if (lane == 63) S.wtot[wave] = estw + g;
@@ -518,38 +520,52 @@ __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW
         if (w < wave) off += S.wtot[w];
         total += S.wtot[w];
     }
-    const float G = off + estw;
     const int ex_total = (int)((hy_fbits(total) >> 23) & 0xffu);
-    // 2. classify the segment
-    const int ex = (int)((hy_fbits(G) >> 23) & 0xffu);
-    const float M = hy_bitsf((uint32_t)ex << 23);
-    const float hu = hy_bitsf((uint32_t)max(ex - 24, 1) << 23);
-    const bool ok = G > 0.f && ex >= 25 && ex <= 253 && ex >= ex_total - 27 && G >= M * 1.001953125f &&
-                    G + g < M * 1.99609375f;
-    float k = 0.f;
-    bool tie = false;
+    // 2. classify the lane's two segments (values 0-3, 4-7)
+    bool clean[2];
+    float K[2];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float r = (M + v[i]) - M;
-        tie |= fabsf(v[i] - r) == hu;
-        k += r;
+    for (int q = 0; q < 2; q++) {
+        const float G = q ? (off + estw) + g0 : off + estw;
+        const float gq = q ? g1 : g0;
+        const int ex = (int)((hy_fbits(G) >> 23) & 0xffu);
+        const float M = hy_bitsf((uint32_t)ex << 23);
+        const float hu = hy_bitsf((uint32_t)max(ex - 24, 1) << 23);
+        const bool ok = G > 0.f && ex >= 25 && ex <= 253 && ex >= ex_total - 27 && G >= M * 1.001953125f &&
+                        G + gq < M * 1.99609375f;
+        float k = 0.f;
+        bool tie = false;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float a = v[4 * q + i];
+            const float r = (M + a) - M;
+            tie |= fabsf(a - r) == hu;
+            k += r;
+        }
+        const bool zero = gq == 0.f;
+        clean[q] = zero || (ok && !tie);
+        K[q] = zero ? 0.f : k;
     }
-    const bool zero = g == 0.f;
-    const bool clean = zero || (ok && !tie);
     // 3. exact prefix sums of the clean contributions within the wavefront; the dirty segments
     //    go to this wavefront's rows in LDS with their local prefix (no cross-wavefront lookup)
-    const double kd = clean && !zero ? (double)k : 0.0;
-    const double pin = hy_wave_incl_scan_d(kd);
-    const double pex = pin - kd;  // exact: the same sums taken apart
-    const uint64_t dm = __builtin_amdgcn_ballot_w64(!clean);
+    const double kd0 = clean[0] ? (double)K[0] : 0.0, kd1 = clean[1] ? (double)K[1] : 0.0;
+    const double kl = kd0 + kd1;
+    const double pin = hy_wave_incl_scan_d(kl);
+    const double pex = pin - kl;  // exact: the same sums taken apart
+    const uint64_t d0 = __builtin_amdgcn_ballot_w64(!clean[0]);
+    const uint64_t d1 = __builtin_amdgcn_ballot_w64(!clean[1]);
     if (lane == 63) S.ktot[wave] = pin;
-    if (lane == 0) S.dcnt[wave] = __builtin_popcountll(dm);
-    if (!clean) {
-        const int r = 64 * wave + __builtin_popcountll(dm & ((1ull << lane) - 1));
-        S.rp[r] = pex;
-        float4* dst = reinterpret_cast<float4*>(S.rv[r]);
-        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
-        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+    if (lane == 0) S.dcnt[wave] = __builtin_popcountll(d0) + __builtin_popcountll(d1);
+    const uint64_t below = (1ull << lane) - 1;
+    const int r0 = 128 * wave + __builtin_popcountll(d0 & below) + __builtin_popcountll(d1 & below);
+    if (!clean[0]) {
+        S.rp[r0] = pex;
+        *reinterpret_cast<float4*>(S.rv[r0]) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (!clean[1]) {
+        const int r1 = r0 + (clean[0] ? 0 : 1);
+        S.rp[r1] = pex + kd0;
+        *reinterpret_cast<float4*>(S.rv[r1]) = make_float4(v[4], v[5], v[6], v[7]);
     }
     __syncthreads();
     // 4. every wavefront: the wavefronts' offsets (one batch of LDS reads), then the dirty rows in
@@ -560,7 +576,9 @@ __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW
     //    multiple of that binade's ulp below M, exact as a float, and s + delta_k is exact. Then
     //    its addends one fp32 add at a time. The walk is one chain: step k adds row k to the
     //    running sum rotated in from lane k - 1 (DPP wave_ror:1, folded into the first add; lane 0
-    //    takes lane 63's, the previous batch's end). Every wavefront walks, so all hold the sum.
+    //    takes lane 63's, the previous batch's end), with the step count uniform (a scalar loop:
+    //    a per-lane counter would put a vector compare before every branch). Every wavefront
+    //    walks, so all hold the sum.
     double koff[NW];
     int roff[NW];
     double ptot = 0.0;
@@ -585,28 +603,23 @@ __device__ inline float hy_block_exact_sum8(const float (&xv)[8], HyExactLdsT<NW
 #pragma unroll
         for (int q = 1; q < NW; q++)
             if (w == q) kw = koff[q];
-        const int r = 64 * w + (gk - roff[w]);
+        const int r = 128 * w + (gk - roff[w]);
         const double P = S.rp[r] + kw;
-        const float4 a0 = reinterpret_cast<const float4*>(S.rv[r])[0];
-        const float4 a1 = reinterpret_cast<const float4*>(S.rv[r])[1];
+        const float4 a = *reinterpret_cast<const float4*>(S.rv[r]);
         // P_{k-1}: lane k - 1's (wave_shr:1; lane 0 gets the previous batch's last)
         const uint64_t pu = __builtin_bit_cast(uint64_t, P);
         const uint32_t plo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)pu, 0x138, 0xF, 0xF, true);
         const uint32_t phi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(pu >> 32), 0x138, 0xF, 0xF, true);
         const double pm = lane ? __builtin_bit_cast(double, ((uint64_t)phi << 32) | plo) : pprev;
         const float delta = (float)(P - pm);
-        const int cnt = min(64, nd - base);
+        const int cnt = __builtin_amdgcn_readfirstlane(min(64, nd - base));
         for (int kk = 0; kk < cnt; kk++) {
             t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x13C, 0xF,
                                                                       0xF, false)) + delta;
-            t += a0.x;
-            t += a0.y;
-            t += a0.z;
-            t += a0.w;
-            t += a1.x;
-            t += a1.y;
-            t += a1.z;
-            t += a1.w;
+            t += a.x;
+            t += a.y;
+            t += a.z;
+            t += a.w;
         }
         pprev = hy_readlane_d(P, 63);
         plast = hy_readlane_d(P, cnt - 1);
