@@ -211,10 +211,11 @@ __device__ inline int hy_dot4(int a, int b, int c) { return __builtin_amdgcn_sdo
 // Sequential fp32 sum p[0] + p[1] + ... + p[n-1] in index order, computed by one whole
 // wavefront (all 64 lanes active; the result is wave-uniform). p may be LDS or global, 16-byte
 // aligned. Lane L loads elements [32L, 32L + 32) of each 2048-element round into registers;
-// then, for L = 0, 1, ..., every lane adds its 32 registers in order to the running sum and
-// the running sum of lane L is broadcast to all lanes (readlane). Only lane L's additions
-// matter in step L, so the result is exactly the one-lane sequential sum, while the chain runs
-// from registers at the add latency. Elements past n are read as +0.0f, which leaves the sum
+// then, for L = 0, 1, ..., lane L adds its 32 registers in order to the running sum that lane
+// L - 1 finished, moved one lane on by DPP (hy_lane_chain32). Only lane L's additions matter
+// in step L, so the result is exactly the one-lane sequential sum, while the chain runs from
+// registers at the add latency with no round trip through a scalar register (a readlane
+// broadcast per step measured slower). Elements past n are read as +0.0f, which leaves the sum
 // unchanged bit for bit because every sum taken here (squares, exponentials) is non-negative,
 // so the running sum is never -0.
 // Lane L's 32 values x[e0 .. e0 + 32) of a row of n (+0 past n): whole groups with 16-byte
@@ -242,19 +243,30 @@ __device__ inline void hy_lane_load32(const float* p, int e0, int n, float (&v)[
     }
 }
 
+// The lane-serial chain over 32 registers per lane: step L adds lane L's 32 values, in order,
+// to the running sum that lane L - 1 finished (moved one lane on by DPP wave_ror:1 and folded
+// into the first add; step 0 starts from s in every lane). nl >= 1 steps, uniform. The result
+// is in lane nl - 1; every lane receives it.
+__device__ inline float hy_lane_chain32(float s, const float (&v)[32], int nl) {
+    float t = s + v[0];
+#pragma unroll
+    for (int i = 1; i < 32; i++) t += v[i];
+    for (int L = 1; L < nl; L++) {
+        t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x13C, 0xF, 0xF, false)) +
+            v[0];
+#pragma unroll
+        for (int i = 1; i < 32; i++) t += v[i];
+    }
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), nl - 1));
+}
+
 __device__ inline float hy_wave_seq_sum(const float* p, int n, int lane) {
     float s = 0.f;
     for (int base = 0; base < n; base += 64 * 32) {
         float v[32];
         const int e0 = base + 32 * lane;
         hy_lane_load32(p, e0, n, v);
-        const int nl = min(64, (n - base + 31) / 32);
-        for (int L = 0; L < nl; L++) {
-            float t = s;
-#pragma unroll
-            for (int i = 0; i < 32; i++) t += v[i];
-            s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), L));
-        }
+        s = hy_lane_chain32(s, v, __builtin_amdgcn_readfirstlane(min(64, (n - base + 31) / 32)));
     }
     return s;
 }
@@ -270,13 +282,7 @@ __device__ inline float hy_wave_seq_sq_sum(const float* x, int n, int lane) {
         hy_lane_load32(x, e0, n, v);
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = v[i] * v[i];  // +0 past n stays +0
-        const int nl = min(64, (n - base + 31) / 32);
-        for (int L = 0; L < nl; L++) {
-            float t = s;
-#pragma unroll
-            for (int i = 0; i < 32; i++) t += v[i];
-            s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), L));
-        }
+        s = hy_lane_chain32(s, v, __builtin_amdgcn_readfirstlane(min(64, (n - base + 31) / 32)));
     }
     return s;
 }

@@ -688,7 +688,9 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
     __shared__ float inv_s[GRP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
+    // uniform (read through a pointer it would count as per-lane, and so would every loop bound
+    // derived from it)
+    const int pos = __builtin_amdgcn_readfirstlane((a.pos_dev ? *a.pos_dev : a.pos0) + t);
     const int n = pos + 1;
     const int qdim = a.heads * HD;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
