@@ -114,6 +114,7 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ
     constexpr int QN = TOK / 4, AN = SLOTS / 16, TOTAL = QN + AN + 3;
     constexpr int MAXI = (TOTAL + 3) / 4;
     static_assert(TOK % 4 == 0 && SLOTS % 16 == 0 && TOK <= 64, "tile shape");
+    static_assert(SLOTS <= 64, "the row block scales are one 64-lane load per block");
     using Stage = GemmStage<SLOTS, TOK>;
     __shared__ Stage ring[RING * KS];
     __shared__ __align__(16) float xch[KS == 2 ? kGemmThreads * MT * NT * 4 : 4];  // set 0's sums
@@ -438,6 +439,13 @@ hipError_t gemm_dispatch(GemmLaunchT<NJ>& L, hipStream_t s) {
     auto wgs = [&](int rt, int tt) { return ((rows + rt - 1) / rt) * ((L.nt + tt - 1) / tt); };
     // K = 2048 and 6144 (8 and 24 blocks) outside pair mode: K split in two inside the
     // workgroup (measured slower for the gate/up pairs)
+    // pipelined launches (up to 8 chunks of 128 tokens): 64-token tiles and two ring stages
+    // throughout, as measured fastest on eight stacked jobs of each shape (gate/up 88.5 ->
+    // 71.2 us, qkv 25.5 -> 20.9 us)
+    if constexpr (NJ == kGemmPipeJobs) {
+        if (L.pair) return gemm_go<NJ, 2, 2, 2, 2, true, 2>(L, s);
+        if (wgs(64, 64) >= 256) return gemm_go<NJ, 2, 2, 2, 2, false, 2>(L, s);
+    }
     if (L.pair) return gemm_go<NJ, 2, 1, 2, 2, true, 2>(L, s);
     if (wgs(64, 64) >= 256) return gemm_go<NJ, 2, 2, 2, 2, false, 3>(L, s);
     if (L.nb == 8) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 4>(L, s);
