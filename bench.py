@@ -393,6 +393,46 @@ def summarize_trace(d: str):
         print(f"`{tgt}`: {len(alone)} back-to-back dispatches (the roofline leg, hymt2_hip_ffn_in) average "
               f"{sum(alone) / len(alone):.2f} us; {len(graph)} dispatches inside the decode graphs average "
               f"{sum(graph) / len(graph):.2f} us.")
+    # the longest run of pipelined-prefill dispatches (job-table kernels, with the chunks'
+    # embedding lookups before them): per kernel and per launch step
+    def pipe(n):
+        return "_pipe" in n or "GemmLaunchT<24>" in n
+    runs, cur = [], []
+    for r in rows:
+        n = r["Kernel_Name"]
+        if pipe(n) or "k_embed_rows" in n:
+            cur.append(r)
+        elif cur:
+            runs.append(cur)
+            cur = []
+    if cur:
+        runs.append(cur)
+    runs = [x for x in runs if any(pipe(r["Kernel_Name"]) for r in x)]
+    if runs:
+        main = max(runs, key=len)
+        wall = (int(main[-1]["End_Timestamp"]) - int(main[0]["Start_Timestamp"])) / 1000.0
+        acc = {}
+        for r in main:
+            n = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("(anonymous namespace)::", "")
+            if "GemmLaunchT<24>" in r["Kernel_Name"]:
+                n = "k_gemm_panel<24, ...> (" + r["Kernel_Name"].split("<", 1)[1].split(">")[0] + ")"
+            a = acc.setdefault(n, [0, 0.0])
+            a[0] += 1
+            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        ksum = sum(v[1] for v in acc.values())
+        print()
+        print(f"Pipelined prefill window: {len(main)} dispatches, {wall:.1f} us from the first start to the last end, "
+              f"{ksum:.1f} us of kernel time.")
+        print()
+        print("| kernel | calls | total us | avg us | % of window kernel time |")
+        print("|---|---:|---:|---:|---:|")
+        for k, (c, s) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
+            print(f"| `{k[:96]}` | {c} | {s:.1f} | {s / c:.2f} | {100 * s / ksum:.1f} |")
+        att = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0 for r in main
+               if "k_attn_chunk_pipe" in r["Kernel_Name"]]
+        if att:
+            print()
+            print("Chunk attention per launch step (us): " + " ".join(f"{x:.0f}" for x in att))
 
 
 def host_loop_rate(fm, prompt, n_tokens: int):
