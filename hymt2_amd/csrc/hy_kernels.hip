@@ -716,6 +716,9 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
         const uint16_t* kr = K + (size_t)j * HD;
         int qo = 0;
         asm volatile("" : "+v"(qo));  // q is read per key, not held in registers across keys
+        // (qo is 0: the rows stay 16-byte aligned, so the reads are 16-byte LDS loads with
+        // immediate offsets rather than 4-byte pairs with an address add each)
+        const float* qrow = static_cast<const float*>(__builtin_assume_aligned(&qs[0][0] + qo, 16));
         float acc[GRP][4];
 #pragma unroll
         for (int h = 0; h < GRP; h++) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.f;
@@ -727,8 +730,8 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
                                  hy_bitsf(kv.w << 16), hy_bitsf(kv.w & 0xffff0000u)};
 #pragma unroll
             for (int h = 0; h < GRP; h++) {
-                const float4 qa = *reinterpret_cast<const float4*>(&qs[h][0] + qo + 8 * i);
-                const float4 qb = *reinterpret_cast<const float4*>(&qs[h][0] + qo + 8 * i + 4);
+                const float4 qa = *reinterpret_cast<const float4*>(qrow + h * HD + 8 * i);
+                const float4 qb = *reinterpret_cast<const float4*>(qrow + h * HD + 8 * i + 4);
                 acc[h][0] += qa.x * kf[0];
                 acc[h][1] += qa.y * kf[1];
                 acc[h][2] += qa.z * kf[2];
