@@ -388,6 +388,28 @@ def test_split_attention_head_dim_256(backend):
         fm.close()
 
 
+@pytest.mark.parametrize("kv_heads", [1, 2])
+def test_chunk_attention_long_rows(backend, kv_heads):
+    """Chunk attention at head dim 128 over rows of up to 1500 positions, 4 or 2 query heads per
+    KV head: the softmax sums of rows up to 256 positions by the lane-serial chain, up to 1024 by
+    the exact segmented workgroup sum with two wavefronts a head, beyond by four wavefronts a head
+    in rounds. The last logits of a 1500-token prompt in 128-token chunks and 16 device greedy
+    ids after it, against the oracle."""
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=kv_heads, hdim=128, vocab=600, ctx=1536)
+    model = synth.make_model(shape, mode="q2", seed=83 + kv_heads)
+    prompt = synth.rand_prompt(synth.rng(85 + kv_heads), 1500, shape.vocab)
+    om = O.OracleModel(model, threads=16)
+    ref = _stepwise_logits(om, prompt)
+    want = O.OracleModel(model, threads=16).generate(prompt, 16, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt), batch=128)), bits(ref))
+        ids, _ = fm.generate_device(prompt, 16, chunk=128)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
 def test_long_context_beyond_4096(backend):
     """Context 4400 (past the one-kernel form's 4096 and the chunk kernel's 2048): two layers, a
     4150-token prompt in 128-token chunks (the general chunk attention, rows up to 4150), the last
