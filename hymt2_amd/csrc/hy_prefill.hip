@@ -447,7 +447,10 @@ hipError_t gemm_dispatch(GemmLaunchT<NJ>& L, hipStream_t s) {
         if (wgs(64, 64) >= 256) return gemm_go<NJ, 2, 2, 2, 2, false, 2>(L, s);
     }
     if (L.pair) return gemm_go<NJ, 2, 1, 2, 2, true, 2>(L, s);
-    if (wgs(64, 64) >= 256) return gemm_go<NJ, 2, 2, 2, 2, false, 3>(L, s);
+    // large single contractions (8192+ rows at 128 tokens; none in a layer of the 1.8B model):
+    // 64 rows x 32 tokens, the four wavefronts down the rows, two ring stages (the 12288 x 2048
+    // panel over 128 tokens: 12.1 against 15.2 us with 64 x 64 tiles and three stages)
+    if (wgs(64, 64) >= 256) return gemm_go<NJ, 1, 2, 4, 1, false, 2>(L, s);
     if (L.nb == 8) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 4>(L, s);
     if (L.nb == 24) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 12>(L, s);
     return gemm_go<NJ, 1, 1, 2, 2, false, 3>(L, s);

@@ -286,6 +286,7 @@ GEMM_SHAPES = [
     (abi.GT_STQ1_0, 1, 256),      # one row, one block
     (abi.GT_Q2_0C, 1, 512),       # one row, one Q2_0C block (two panel pieces)
     (abi.GT_STQ1_0, 100, 1536),
+    (abi.GT_Q2_0C, 8200, 2048),   # the large-contraction tiles at 128 tokens, ragged rows
 ]
 
 
