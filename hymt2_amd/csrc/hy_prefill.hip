@@ -451,7 +451,9 @@ hipError_t gemm_dispatch(GemmLaunchT<NJ>& L, hipStream_t s) {
     // 64 rows x 32 tokens, the four wavefronts down the rows, two ring stages (the 12288 x 2048
     // panel over 128 tokens: 12.1 against 15.2 us with 64 x 64 tiles and three stages)
     if (wgs(64, 64) >= 256) return gemm_go<NJ, 1, 2, 4, 1, false, 2>(L, s);
-    if (L.nb == 8) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 4>(L, s);
+    // K = 2048, one chunk (qkv: 3072 rows, o: 2048): the four wavefronts of each K set down the
+    // rows, two ring stages (qkv 8.2 -> 6.7 us with 32-token tiles, o 6.3 -> 5.9 us with 16)
+    if (L.nb == 8) return rows >= 3072 ? gemm_go<NJ, 1, 2, 4, 1, false, 2, 2, 4>(L, s) : gemm_go<NJ, 1, 1, 4, 1, false, 2, 2, 4>(L, s);
     if (L.nb == 24) return gemm_go<NJ, 1, 1, 2, 2, false, 3, 2, 12>(L, s);
     return gemm_go<NJ, 1, 1, 2, 2, false, 3>(L, s);
 }
