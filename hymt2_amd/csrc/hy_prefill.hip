@@ -86,15 +86,15 @@ __device__ __forceinline__ void wait_vm() {
 //      16 t + (c ^ (t & 15)), so the 16 tokens of a B-fragment read hit 16 bank groups;
 //   a: the workgroup's ROWS panel rows x 4 pieces of 16 bytes; piece g of row r at slot
 //      4 r + (g ^ ((r >> 2) & 3)), conflict-free the same way for the A-fragment reads;
-//   d, sum: the tokens' Q8_K scale and sum; ps: the rows' block scale (one 64-lane direct load
-//   each, so sized for 64).
+//   d, sum: the tokens' Q8_K scale and sum (one 64-lane direct load each); ps: the rows' block
+//   scales (one 64-lane direct load per 64 row slots).
 template <int ROWS, int TOK>
 struct GemmStage {
     alignas(16) uint8_t q[TOK * 256];
     alignas(16) uint8_t a[ROWS * 64];
     alignas(16) float d[64];
     alignas(16) int sum[64];
-    alignas(16) float ps[64];
+    alignas(16) float ps[ROWS > 64 ? 128 : 64];
 };
 
 // KS = 2 splits K inside the workgroup: two sets of 4 wavefronts own the same output tile,
@@ -111,10 +111,10 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ
     constexpr int TOK = WT * NT * 16;    // tokens of the workgroup
     // direct loads of one block: QN of qp, AN of panel bytes, then d, sum and the rows' block
     // scales (64 lanes each), dealt round-robin to the wavefronts: load k goes to wavefront k % 4
-    constexpr int QN = TOK / 4, AN = SLOTS / 16, TOTAL = QN + AN + 3;
+    constexpr int QN = TOK / 4, AN = SLOTS / 16, PSN = (SLOTS + 63) / 64, TOTAL = QN + AN + 2 + PSN;
     constexpr int MAXI = (TOTAL + 3) / 4;
     static_assert(TOK % 4 == 0 && SLOTS % 16 == 0 && TOK <= 64, "tile shape");
-    static_assert(SLOTS <= 64, "the row block scales are one 64-lane load per block");
+    static_assert(SLOTS <= 128, "the row block scales are at most two 64-lane loads per block");
     using Stage = GemmStage<SLOTS, TOK>;
     __shared__ Stage ring[RING * KS];
     __shared__ __align__(16) float xch[KS == 2 ? kGemmThreads * MT * NT * 4 : 4];  // set 0's sums
@@ -188,8 +188,9 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ
             src[i] = reinterpret_cast<const char*>(&act[(size_t)min(tokw + lane, nt - 1) * nb].d) + (k == QN + AN ? 0 : 4);
             stride[i] = sizeof(HyQ8K);
             dst[i] = k == QN + AN ? offsetof(Stage, d) : offsetof(Stage, sum);
-        } else {  // block scale of row slot `lane` (slots past SLOTS load a valid row, unused)
-            const int sl = min(lane, SLOTS - 1);
+        } else {  // block scale of row slot 64 part + lane (slots past SLOTS load a valid row, unused)
+            const int part = k - (QN + AN + 2);
+            const int sl = min(64 * part + lane, SLOTS - 1);
             const int w_r = sl / (MT * 16), mt = (sl / 16) % MT, rr = sl % 16;
             const float* pb = psbase[0];
             int nr = nrow[0];
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ
                 if (mt == m) pb = psbase[m], nr = nrow[m];
             src[i] = reinterpret_cast<const char*>(pb + (size_t)min(slot_row(w_r, mt, rr), nr - 1) * nb);
             stride[i] = 4;
-            dst[i] = offsetof(Stage, ps);
+            dst[i] = offsetof(Stage, ps) + 256 * part;
         }
     }
     const uint32_t ring0 = lds_addr(&ring[0]);
@@ -441,9 +442,11 @@ hipError_t gemm_dispatch(GemmLaunchT<NJ>& L, hipStream_t s) {
     // workgroup (measured slower for the gate/up pairs)
     // pipelined launches (up to 8 chunks of 128 tokens): 64-token tiles and two ring stages
     // throughout, as measured fastest on eight stacked jobs of each shape (gate/up 88.5 ->
-    // 71.2 us, qkv 25.5 -> 20.9 us)
+    // 71.2 us, qkv 25.5 -> 20.9 us); gate/up pairs in 64 pairs x 64 tokens with the four
+    // wavefronts down the rows when that still gives a workgroup per CU (eight stacked jobs:
+    // 71-75 -> 57 us; 128-row tiles of the other shapes measured within noise)
     if constexpr (NJ == kGemmPipeJobs) {
-        if (L.pair) return gemm_go<NJ, 2, 2, 2, 2, true, 2>(L, s);
+        if (L.pair) return wgs(64, 64) >= 256 ? gemm_go<NJ, 2, 4, 4, 1, true, 2>(L, s) : gemm_go<NJ, 2, 2, 2, 2, true, 2>(L, s);
         if (wgs(64, 64) >= 256) return gemm_go<NJ, 2, 2, 2, 2, false, 2>(L, s);
     }
     if (L.pair) return gemm_go<NJ, 2, 1, 2, 2, true, 2>(L, s);
