@@ -666,24 +666,33 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 // (src/kernels.c:1111-1121) times 1/sqrtf(hd), max, expf, the sum in position order,
 // p_j = e_j * (1 / sum) once per position, then o[d] += p_j * V_j[d] in position order
 // (axpy_bf16, :1122-1124). Scores: one key per thread for every head of the group. Sums:
-// wavefront h for head h. Output: one (head, dimension) chain per lane over fp32 V tiles in LDS.
+// wavefront h for head h. Output: the chains of two heads at one dimension per lane, over fp32
+// V tiles in LDS.
 constexpr int kAcThreads = 512;
-constexpr int kAcTile = 64;     // positions per V tile in LDS
 constexpr int kAcMaxCtx = 2048;
+// positions per fp32 V tile in LDS: 64 for a launch of one chunk (two workgroups a CU at any
+// tile size); 32 for the pipelined launch, whose 51 KB of LDS and 74 VGPRs let three of its
+// workgroups share a CU (config-4 prefill, with two heads a lane: 73.0-73.6k -> 79.2-80.1k
+// tok/s; the same tile in the one-chunk launch measured 1 % slower)
+constexpr int kAcTileRow = 64;
+constexpr int kAcTilePipe = 32;
+// output chains per lane: two heads of the group at one dimension, so each V element read from
+// LDS serves both (one head a lane measured 1 % slower, four 3 % slower)
+constexpr int kAcHeadsPerLane = 2;
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));  // arrays of it stay in registers
 
-template <int HD, int GRP>
+template <int HD, int GRP, int TILE>
 __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) {
     constexpr int NW = kAcThreads / 64;
     constexpr int KV4 = HD / 8;
     constexpr int DW = HD / 64;              // wavefronts per head in the output (one dim per lane)
     static_assert(GRP * DW <= NW && GRP <= NW, "heads x dims fit the workgroup");
-    constexpr int VPT = kAcTile * KV4 / kAcThreads;  // 16-byte V pieces per thread per tile
-    static_assert(VPT >= 1, "tile split");
+    constexpr int VPC = TILE * KV4;                           // 16-byte V pieces of a tile
+    constexpr int VPT = (VPC + kAcThreads - 1) / kAcThreads;  // per thread
     __shared__ __align__(16) float qs[GRP][HD];
     __shared__ __align__(16) float sc[GRP][kAcMaxCtx];   // scores, then e_j, then p_j
-    __shared__ __align__(16) float vt[kAcTile * HD];     // fp32 V tile [j][d]
+    __shared__ __align__(16) float vt[TILE * HD];        // fp32 V tile [j][d]
     __shared__ float red[GRP][NW];
     __shared__ float inv_s[GRP];
 
@@ -703,7 +712,7 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const int f = tid + kAcThreads * i, j = f / KV4;
-        vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
+        if (VPC % kAcThreads == 0 || f < VPC) vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
     }
     __syncthreads();
 
@@ -784,15 +793,20 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
 #pragma unroll
             for (int h = 0; h < GRP; h++) sc[h][j] = sc[h][j] * inv[h];
     }
-    // output chains: head oh, dimension od over fp32 V tiles; the next tile's loads in flight
-    // while the current one is summed
-    const int oh = wave / DW, od = (wave % DW) * 64 + lane;
-    float o = 0.f;
-    for (int t0 = 0; t0 < n; t0 += kAcTile) {
+    // output chains: HPL heads from oh0 at dimension od per lane (each V element read once for
+    // them), over fp32 V tiles; the next tile's loads in flight while the current one is summed
+    constexpr int HPL = GRP % kAcHeadsPerLane == 0 ? kAcHeadsPerLane : 1;
+    constexpr int OW = GRP / HPL * DW;  // output wavefronts
+    const int oh0 = (wave / DW) * HPL, od = (wave % DW) * 64 + lane;
+    float o[HPL];
+#pragma unroll
+    for (int hh = 0; hh < HPL; hh++) o[hh] = 0.f;
+    for (int t0 = 0; t0 < n; t0 += TILE) {
         __syncthreads();  // previous tile consumed (the first time: the p_j written)
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const int f = tid + kAcThreads * i;
+            if (VPC % kAcThreads != 0 && f >= VPC) break;
             float* dstv = &vt[(f / KV4) * HD + 8 * (f % KV4)];
             const v4u w = vr[i];
             *reinterpret_cast<float4*>(dstv) =
@@ -800,33 +814,42 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
             *reinterpret_cast<float4*>(dstv + 4) =
                 make_float4(hy_bitsf(w.z << 16), hy_bitsf(w.z & 0xffff0000u), hy_bitsf(w.w << 16), hy_bitsf(w.w & 0xffff0000u));
         }
-        if (t0 + kAcTile < n) {
+        if (t0 + TILE < n) {
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
-                const int f = tid + kAcThreads * i, j = t0 + kAcTile + f / KV4;
-                vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
+                const int f = tid + kAcThreads * i, j = t0 + TILE + f / KV4;
+                if (VPC % kAcThreads == 0 || f < VPC) vr[i] = *reinterpret_cast<const v4u*>(V + (size_t)min(j, pos) * HD + 8 * (f % KV4));
             }
         }
         __syncthreads();  // tile in LDS
-        if (oh < GRP) {
-            const float* pj = sc[oh] + t0;
+        if (wave < OW) {
             const float* vd = vt + od;
-            const int cnt = min(kAcTile, n - t0);
+            const int cnt = min(TILE, n - t0);
             int q = 0;
             for (; q + 8 <= cnt; q += 8) {
-                const float4 p0 = *reinterpret_cast<const float4*>(pj + q);
-                const float4 p1 = *reinterpret_cast<const float4*>(pj + q + 4);
-                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
                 float vv[8];
 #pragma unroll
                 for (int k = 0; k < 8; k++) vv[k] = vd[(q + k) * HD];
 #pragma unroll
-                for (int k = 0; k < 8; k++) o += pv[k] * vv[k];
+                for (int hh = 0; hh < HPL; hh++) {
+                    const float* pj = sc[oh0 + hh] + t0 + q;
+                    const float4 p0 = *reinterpret_cast<const float4*>(pj);
+                    const float4 p1 = *reinterpret_cast<const float4*>(pj + 4);
+                    const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                    for (int k = 0; k < 8; k++) o[hh] += pv[k] * vv[k];
+                }
             }
-            for (; q < cnt; q++) o += pj[q] * vd[q * HD];
+            for (; q < cnt; q++) {
+                const float vq = vd[q * HD];
+#pragma unroll
+                for (int hh = 0; hh < HPL; hh++) o[hh] += sc[oh0 + hh][t0 + q] * vq;
+            }
         }
     }
-    if (oh < GRP) a.ao[(size_t)t * qdim + (size_t)(g * GRP + oh) * HD + od] = o;
+    if (wave < OW)
+#pragma unroll
+        for (int hh = 0; hh < HPL; hh++) a.ao[(size_t)t * qdim + (size_t)(g * GRP + oh0 + hh) * HD + od] = o[hh];
     // the group's GRP * HD outputs are whole Q8_K blocks of the row: quantize them here
     // (quantize_q8k, src/kernels.c:128-165) for the o-projection
     if constexpr (GRP * HD % HY_QK == 0) {
@@ -834,7 +857,9 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
             constexpr int NB = GRP * HD / HY_QK;
             static_assert(NB <= NW, "one wavefront per block");
             __syncthreads();  // every chain has read its last V tile
-            if (oh < GRP) vt[oh * HD + od] = o;
+            if (wave < OW)
+#pragma unroll
+                for (int hh = 0; hh < HPL; hh++) vt[(oh0 + hh) * HD + od] = o[hh];
             __syncthreads();
             if (wave < NB) q8k_quantize_wave(vt + wave * HY_QK, a.act_out + (size_t)t * (qdim / HY_QK) + g * NB + wave, lane);
         }
@@ -843,15 +868,15 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
 
 template <int HD, int GRP>
 __global__ __launch_bounds__(kAcThreads) void k_attn_chunk(AttnArgs a) {
-    attn_chunk_row<HD, GRP>(a, blockIdx.x, blockIdx.y);
+    attn_chunk_row<HD, GRP, kAcTileRow>(a, blockIdx.x, blockIdx.y);
 }
 
 // Rows run last to first: the jobs are chunks in position order, so the workgroups with the
 // longest rows start first and the short ones fill in behind them.
 template <int HD, int GRP>
-__global__ __launch_bounds__(kAcThreads) void k_attn_chunk_pipe(PipeAttn J) {
+__global__ __launch_bounds__(kAcThreads, 3) void k_attn_chunk_pipe(PipeAttn J) {
     const int row = (int)(gridDim.y - 1 - blockIdx.y), j = pipe_job(J.row0, J.njobs, row);
-    attn_chunk_row<HD, GRP>(J.a[j], blockIdx.x, row - J.row0[j]);
+    attn_chunk_row<HD, GRP, kAcTilePipe>(J.a[j], blockIdx.x, row - J.row0[j]);
 }
 
 bool attention_quantizes(const AttnArgs& a) {
