@@ -260,6 +260,38 @@ __device__ inline float hy_lane_chain32(float s, const float (&v)[32], int nl) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), nl - 1));
 }
 
+// Up to four sequential fp32 sums in index order by one wavefront, one per 16-lane row: row r
+// sums p[r * stride + 0 .. n) (rows from ROWS on repeat the last one). Lane i of a row holds
+// elements [32 i, 32 i + 32) of each 512-element round, and the chain steps as in
+// hy_lane_chain32 with DPP row_ror:1 (lane i takes lane i - 1 of its own row), so the four
+// sums run in the same instructions and cost what one costs. A full round ends in lane 15 of
+// the row and rotates into lane 0 as the next round's start. Every lane receives all the sums.
+template <int ROWS>
+__device__ inline void hy_row_seq_sums(const float* p, int stride, int n, int lane, float (&s)[4]) {
+    static_assert(ROWS >= 1 && ROWS <= 4, "one sum per 16-lane row");
+    const float* pr = p + (size_t)min(lane >> 4, ROWS - 1) * stride;
+    const int e = 32 * (lane & 15);
+    float c = 0.f, t = 0.f;  // c: in lane 0 of row r, row r's sum before the round
+    int nl = 1;
+    for (int base = 0; base < n; base += 16 * 32) {
+        float v[32];
+        hy_lane_load32(pr, base + e, n, v);
+        nl = __builtin_amdgcn_readfirstlane(min(16, (n - base + 31) / 32));
+        t = c + v[0];
+#pragma unroll
+        for (int i = 1; i < 32; i++) t += v[i];
+        for (int L = 1; L < nl; L++) {
+            t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x121, 0xF, 0xF, false)) +
+                v[0];
+#pragma unroll
+            for (int i = 1; i < 32; i++) t += v[i];
+        }
+        c = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x121, 0xF, 0xF, false));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 16 * r + nl - 1));
+}
+
 __device__ inline float hy_wave_seq_sum(const float* p, int n, int lane) {
     float s = 0.f;
     for (int base = 0; base < n; base += 64 * 32) {

@@ -665,8 +665,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 // (src/model.c:767-795) per (token, head): scores by dot_bf16's four partial sums in order
 // (src/kernels.c:1111-1121) times 1/sqrtf(hd), max, expf, the sum in position order,
 // p_j = e_j * (1 / sum) once per position, then o[d] += p_j * V_j[d] in position order
-// (axpy_bf16, :1122-1124). Scores: one key per thread for every head of the group. Sums:
-// wavefront h for head h. Output: the chains of two heads at one dimension per lane, over fp32
+// (axpy_bf16, :1122-1124). Scores: one key per thread for every head of the group. Sums: one
+// 16-lane row of wavefront 0 per head. Output: the chains of two heads at one dimension per lane, over fp32
 // V tiles in LDS.
 constexpr int kAcThreads = 512;
 constexpr int kAcMaxCtx = 2048;
@@ -690,7 +690,6 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
     static_assert(GRP * DW <= NW && GRP <= NW, "heads x dims fit the workgroup");
     constexpr int VPC = TILE * KV4;                           // 16-byte V pieces of a tile
     constexpr int VPT = (VPC + kAcThreads - 1) / kAcThreads;  // per thread
-    __shared__ __align__(16) float qs[GRP][HD];
     __shared__ __align__(16) float sc[GRP][kAcMaxCtx];   // scores, then e_j, then p_j
     __shared__ __align__(16) float vt[TILE * HD];        // fp32 V tile [j][d]
     __shared__ float red[GRP][NW];
@@ -705,8 +704,11 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
 
-    // q rows of the group's heads (RoPE'd and normed by k_rope_norm_store)
-    for (int i = tid; i < GRP * HD; i += kAcThreads) qs[i / HD][i % HD] = a.q[(size_t)t * qdim + (size_t)(g * GRP) * HD + i];
+    // q rows of the group's heads (RoPE'd and normed by k_rope_norm_store), read through the
+    // constant address space: their addresses are uniform, so the reads are scalar loads into
+    // SGPRs that the multiplies take directly (nothing is written to them in this kernel)
+    typedef __attribute__((address_space(4))) const float cfloat;
+    const uint64_t qaddr = (uint64_t)(uintptr_t)(a.q + (size_t)t * qdim + (size_t)(g * GRP) * HD);
     // first V tile
     v4u vr[VPT];
 #pragma unroll
@@ -723,11 +725,9 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
     for (int h = 0; h < GRP; h++) lmax[h] = -__builtin_inff();
     for (int j = tid; j < n; j += kAcThreads) {
         const uint16_t* kr = K + (size_t)j * HD;
-        int qo = 0;
-        asm volatile("" : "+v"(qo));  // q is read per key, not held in registers across keys
-        // (qo is 0: the rows stay 16-byte aligned, so the reads are 16-byte LDS loads with
-        // immediate offsets rather than 4-byte pairs with an address add each)
-        const float* qrow = static_cast<const float*>(__builtin_assume_aligned(&qs[0][0] + qo, 16));
+        uint64_t qa = qaddr;
+        asm volatile("" : "+s"(qa));  // q is loaded per key, not held (or spilled) across keys
+        const cfloat* qc = (const cfloat*)qa;
         float acc[GRP][4];
 #pragma unroll
         for (int h = 0; h < GRP; h++) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.f;
@@ -739,16 +739,9 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
                                  hy_bitsf(kv.w << 16), hy_bitsf(kv.w & 0xffff0000u)};
 #pragma unroll
             for (int h = 0; h < GRP; h++) {
-                const float4 qa = *reinterpret_cast<const float4*>(qrow + h * HD + 8 * i);
-                const float4 qb = *reinterpret_cast<const float4*>(qrow + h * HD + 8 * i + 4);
-                acc[h][0] += qa.x * kf[0];
-                acc[h][1] += qa.y * kf[1];
-                acc[h][2] += qa.z * kf[2];
-                acc[h][3] += qa.w * kf[3];
-                acc[h][0] += qb.x * kf[4];
-                acc[h][1] += qb.y * kf[5];
-                acc[h][2] += qb.z * kf[6];
-                acc[h][3] += qb.w * kf[7];
+                const cfloat* qh = qc + h * HD + 8 * i;
+#pragma unroll
+                for (int c = 0; c < 8; c++) acc[h][c & 3] += qh[c] * kf[c];
             }
         }
 #pragma unroll
@@ -778,10 +771,14 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
             for (int h = 0; h < GRP; h++) sc[h][j] = hy_expf(sc[h][j] - mx[h]);
     }
     __syncthreads();
-    // the sum of head h in position order by wavefront h
-    if (wave < GRP) {
-        const float sum = hy_wave_seq_sum(sc[wave], n, lane);
-        if (lane == 0) inv_s[wave] = 1.0f / sum;
+    // the sums of the heads in position order, together in the 16-lane rows of wavefront 0
+    // (the chain's instructions once for all heads)
+    if (wave == 0) {
+        float sum[4];
+        hy_row_seq_sums<GRP>(&sc[0][0], kAcMaxCtx, n, lane, sum);
+        if (lane == 0)
+#pragma unroll
+            for (int h = 0; h < GRP; h++) inv_s[h] = 1.0f / sum[h];
     }
     __syncthreads();
     // p_j = e_j * inv, once per position (sc[j] * inv)
