@@ -694,6 +694,7 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
     __shared__ __align__(16) float vt[TILE * HD];        // fp32 V tile [j][d]
     __shared__ float red[GRP][NW];
     __shared__ float inv_s[GRP];
+    __shared__ uint64_t etab[32];  // expf table (a lookup is an LDS read, not a global load)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // uniform (read through a pointer it would count as per-lane, and so would every loop bound
@@ -707,6 +708,7 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
     // q rows of the group's heads (RoPE'd and normed by k_rope_norm_store), read through the
     // constant address space: their addresses are uniform, so the reads are scalar loads into
     // SGPRs that the multiplies take directly (nothing is written to them in this kernel)
+    if (tid < 32) etab[tid] = hy_exp_tab_entry(tid);  // read after the barrier past the scores
     typedef __attribute__((address_space(4))) const float cfloat;
     const uint64_t qaddr = (uint64_t)(uintptr_t)(a.q + (size_t)t * qdim + (size_t)(g * GRP) * HD);
     // first V tile
@@ -768,7 +770,7 @@ __device__ __forceinline__ void attn_chunk_row(const AttnArgs& a, int g, int t) 
         }
         for (int j = tid; j < n; j += kAcThreads)
 #pragma unroll
-            for (int h = 0; h < GRP; h++) sc[h][j] = hy_expf(sc[h][j] - mx[h]);
+            for (int h = 0; h < GRP; h++) sc[h][j] = hy_expf_tab(sc[h][j] - mx[h], etab);
     }
     __syncthreads();
     // the sums of the heads in position order, together in the 16-lane rows of wavefront 0
