@@ -118,8 +118,10 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ
     using Stage = GemmStage<SLOTS, TOK>;
     __shared__ Stage ring[RING * KS];
     __shared__ __align__(16) float xch[KS == 2 ? kGemmThreads * MT * NT * 4 : 4];  // set 0's sums
+    __shared__ uint64_t etab[PAIR ? 32 : 1];  // expf table of the SwiGLU epilogue (LDS lookups)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
+    if (PAIR && tid < 32) etab[tid] = hy_exp_tab_entry(tid);  // read after the block barriers
     const int half = KS == 2 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;  // K set
     const int wr = wave % WR, wt = wave / WR;
     const int nb = L.nb;
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(kGemmThreads * KS) void k_gemm_panel(GemmLaunchT<NJ
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float gt = accf[0][n][r], up = accf[1][n][r];
-                v[r] = gt / (1.0f + hy_expf(-gt)) * up;
+                v[r] = gt / (1.0f + hy_expf_tab(-gt, etab)) * up;
             }
             float* o = out + (size_t)t * ldo + row;
             if (row + 3 < nout && ((ldo | row) & 3) == 0) {
