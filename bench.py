@@ -106,7 +106,7 @@ def ffn_in_roofline(model, b, copies: int = 64, passes: int = 3):
     algo = wg.nbytes_device() + wu.nbytes_device() + 2 * s.hidden * 4 + wg.n * 4
     return dict(bound="hbm", achieved=round(algo / avg_s / 1e9, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(algo / avg_s / 1e9 / HBM_PEAK_GBS, 4), traffic=_pmc_traffic("ffn_in"),
-                kernel="k_mv1<PANEL, SPL 1, ITERS 8, PRO_NORM> pair mode (hymt2_hip_ffn_in): fused FFN input of "
+                kernel="k_mv1<PANEL, SPL 1, ITERS 6, PRO_NORM> pair mode, 256 workgroups of 24 gate+up row pairs (hymt2_hip_ffn_in): fused FFN input of "
                        "one decode token (RMSNorm + Q8_K prologue, gate+up 2x6144x2048 STQ1_0 panel, SwiGLU)",
                 avg_us=round(avg_s * 1e6, 2), bytes_per_launch=algo,
                 timing=f"HIP events on the backend stream over {copies * passes} launches rotating {copies} "
