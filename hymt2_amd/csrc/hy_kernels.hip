@@ -493,14 +493,41 @@ __device__ __forceinline__ void rope_norm_store_row(const AttnArgs& a, int t, in
     const int head = is_q ? slot : slot - a.heads;
     const int qdim = a.heads * hd, kvdim = a.kv_heads * hd;
     const float* src = is_q ? a.q + (size_t)t * qdim + (size_t)head * hd : a.k + (size_t)t * kvdim + (size_t)head * hd;
-    for (int d = lane; d < hd; d += 64) row[d] = src[d];
-    __syncthreads();
     const float* c = a.rope_cos + (size_t)pos * half;
     const float* sn = a.rope_sin + (size_t)pos * half;
-    for (int i = lane; i < half; i += 64) {
-        const float x0 = row[i], x1 = row[i + half];
-        row[i] = x0 * c[i] - x1 * sn[i];
-        row[i + half] = x0 * sn[i] + x1 * c[i];
+    const float* nw = is_q ? a.q_norm : a.k_norm;
+    const float* v = a.v + (size_t)t * kvdim + (size_t)head * hd;
+    // every global operand of the row up front (dimensions lane + 64 k), so the kernel waits on
+    // memory once rather than once per phase
+    float xs[4], ws[4], vs[4], cs[2], ss[2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int d = lane + 64 * k;
+        xs[k] = ws[k] = vs[k] = 0.f;
+        if (d < hd) {
+            xs[k] = src[d];
+            ws[k] = nw[d];
+            if (!is_q) vs[k] = v[d];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = lane + 64 * k;
+        cs[k] = ss[k] = 0.f;
+        if (i < half) cs[k] = c[i], ss[k] = sn[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (lane + 64 * k < hd) row[lane + 64 * k] = xs[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = lane + 64 * k;
+        if (i < half) {
+            const float x0 = row[i], x1 = row[i + half];
+            row[i] = x0 * cs[k] - x1 * ss[k];
+            row[i + half] = x0 * ss[k] + x1 * cs[k];
+        }
     }
     __syncthreads();
     for (int d = lane; d < hd; d += 64) sq[d] = row[d] * row[d];
@@ -511,18 +538,20 @@ __device__ __forceinline__ void rope_norm_store_row(const AttnArgs& a, int t, in
     }
     __syncthreads();
     const float scale = scale_slot;
-    const float* nw = is_q ? a.q_norm : a.k_norm;
-    for (int d = lane; d < hd; d += 64) row[d] = row[d] * scale * nw[d];
-    __syncthreads();
     if (is_q) {
         float* dst = a.q + (size_t)t * qdim + (size_t)head * hd;
-        for (int d = lane; d < hd; d += 64) dst[d] = row[d];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (lane + 64 * k < hd) dst[lane + 64 * k] = row[lane + 64 * k] * scale * ws[k];
     } else {
         const size_t off = ((size_t)head * a.ctx + pos) * hd;
-        const float* v = a.v + (size_t)t * kvdim + (size_t)head * hd;
-        for (int d = lane; d < hd; d += 64) {
-            a.kc[off + d] = hy_to_bf16(row[d]);
-            a.vc[off + d] = hy_to_bf16(v[d]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int d = lane + 64 * k;
+            if (d < hd) {
+                a.kc[off + d] = hy_to_bf16(row[d] * scale * ws[k]);
+                a.vc[off + d] = hy_to_bf16(vs[k]);
+            }
         }
     }
 }
