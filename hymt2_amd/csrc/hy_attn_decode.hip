@@ -624,35 +624,45 @@ hipError_t launch_attn1(const Attn1Args& a, hipStream_t s) {
 //     position; then wavefront w scores q head w % 4 over half of the segment, one key per pair
 //     of lanes in dot_bf16's order; the scores and each half-segment's maximum go to global
 //     memory.
-//   k_attn_out, one 512-thread workgroup per (query head, 64 output dimensions): the maximum of
-//     the segment maxima (order-free), e_j = expf(s_j - max), their sum in position order by the
-//     8-wavefront exact segmented sum (rows longer than kSplitWin in chunks, each later chunk
-//     taking the running sum as its first addend, which continues the same sequential sum),
-//     p_j = e_j * (1 / sum), then o[d] += p_j * V_j[d] in position order: wavefronts 1-7 form the
-//     products p_j * V_j[d] (rounded to fp32, as the reference's multiply) into [d][j] tiles of
-//     128 positions, and wavefront 0 (one lane per dimension) adds them in position order, four
-//     per LDS read, with only the dependent adds on its critical path.
+//   k_attn_out, one 512-thread workgroup per (query head, kSoDims output dimensions): the maximum
+//     of the segment maxima (order-free), e_j = expf(s_j - max) (positions dealt to the threads
+//     round-robin, through LDS), their sum in position order by the 8-wavefront exact segmented
+//     sum (rows longer than kSplitWin in chunks, each later chunk taking the running sum as its
+//     first addend, which continues the same sequential sum), p_j = e_j * (1 / sum), then
+//     o[d] += p_j * V_j[d] in position order: wavefronts 1-3 and 5-7 form the products
+//     p_j * V_j[d] (rounded to fp32, as the reference's multiply) into [d][j] tiles of 256
+//     positions, and wavefront 0 (one lane per dimension) adds them in position order, four per
+//     LDS read, with only the dependent adds on its critical path. Wavefront 4, which shares
+//     wavefront 0's SIMD, only keeps the barriers: an instruction it issued would delay the
+//     chain's next add (measured 8.9 against 6.4 cycles an add). The output chains of a head are sequential
+//     in position, so the work spreads over the dimensions: 16 a workgroup keeps the products
+//     of a tile (4096) off the chain's path and puts 8 workgroups on each head.
 
 namespace {
 
 constexpr int kSpThreads = 512;                // k_attn_scores: eight wavefronts
 constexpr int kSpGridX = 128;                  // score workgroups per KV head (more segments loop)
 constexpr int kSoThreads = 512;                // k_attn_out
+constexpr int kSoNW = kSoThreads / 64;         // its wavefronts
+constexpr int kSoDims = 16;                    // output dimensions per k_attn_out workgroup
+constexpr int kSoDG = kSoDims / 8;             // 16-byte V pieces (8 dimensions) per position
 constexpr int kSoTile = 256;                   // positions per product tile
-constexpr int kSoPad = kSoTile + 4;            // [d][j] row length (16-byte rows, no bank conflicts)
-constexpr int kSoPieces = kSoTile * 8;         // (position, 8 dimensions) pieces of a tile
-constexpr int kSoProd = kSoThreads - 64;       // producer threads (wavefronts 1-7)
+constexpr int kSoPad = kSoTile + 4;            // [d][j] row length (16-byte rows)
+constexpr int kSoPieces = kSoTile * kSoDG;     // (position, 8 dimensions) pieces of a tile
+constexpr int kSoProd = kSoThreads - 128;      // producer threads (wavefronts 1-3 and 5-7)
 constexpr int kSoPPT = (kSoPieces + kSoProd - 1) / kSoProd;  // pieces per producer thread
-static_assert(kSplitWin % kSoTile == 0 && kSplitWin == 8 * kSoThreads, "windows of whole tiles, 8 per thread");
-static_assert(kSoProd % 64 == 0 && kSoTile % 32 == 0, "whole rows per wavefront load; swizzle within 32 positions");
+constexpr int kSoEPT = kSplitWin / kSoThreads;               // positions of a window per thread
+static_assert(kSoEPT == 8, "hy_block_exact_sum8 takes eight addends a thread");
+static_assert(kSplitWin % kSoTile == 0, "windows of whole tiles");
+static_assert(kSoTile % 32 == 0 && kSoDims % 8 == 0 && kSoDims <= 64, "swizzle within 32 positions; whole pieces");
 
 struct SoSmem {
-    alignas(16) float pj[kSplitWin];  // p_j of the current window
+    alignas(16) float pj[kSplitWin];  // e_j, then p_j, of the current window
     union {
-        HyExactLdsT<kA1Waves> exs;                    // the softmax sum
-        alignas(16) float prod[2][64][kSoPad];        // then two product tiles [d][j]
+        HyExactLdsT<kSoNW> exs;                       // the softmax sum
+        alignas(16) float prod[2][kSoDims][kSoPad];   // then two product tiles [d][j]
     };
-    float red[kSoThreads / 64];
+    float red[kSoNW];
     uint64_t etab[32];  // expf table
 };
 
@@ -767,24 +777,23 @@ __global__ __launch_bounds__(kSpThreads) void k_attn_scores(Attn1Args a) {
 
 namespace {
 
-// Product tile layout: buf[d][c], d the dimension (of this workgroup's 64), c a swizzled position:
-// position j of the tile sits at column j ^ (4 * (d / 8)). The XOR moves whole groups of four
-// positions within aligned groups of 32, so the chain's 16-byte reads of four consecutive
-// positions stay contiguous, and the producers' stores of one instruction (eight positions times
-// eight 8-dimension groups) spread over all LDS banks.
+// Product tile layout: buf[d][c], d the dimension (of this workgroup's kSoDims), c a swizzled
+// position: position j of the tile sits at column j ^ (4 * (d / 8)). The XOR moves whole groups
+// of four positions within aligned groups of 32, so the chain's 16-byte reads of four
+// consecutive positions stay contiguous, and the producers' stores of one instruction (32
+// positions times two 8-dimension groups) spread over the LDS banks.
 
 // V pieces of the tile at t0 for producer thread pt: piece q = pt + kSoProd k is position
-// t0 + q / 8, dimensions 8 (q % 8) .. + 8 of this workgroup's 64 (V is offset to them), so that
-// eight lanes read one row's 128 contiguous bytes; rows clamped inside the cache (pieces past the
-// row are never added). Every load is issued, also for pieces past the tile's (q clamped, the
-// value unused): with a conditional load the compiler cannot count the loads in flight and waits
-// for all of them.
+// t0 + q / kSoDG, dimensions 8 (q % kSoDG) .. + 8 of this workgroup's kSoDims (V is offset to
+// them); rows clamped inside the cache (pieces past the row are never added). Every load is
+// issued, also for pieces past the tile's (q clamped, the value unused): with a conditional load
+// the compiler cannot count the loads in flight and waits for all of them.
 template <int HD>
 __device__ __forceinline__ void so_load_v(uint4 (&v)[kSoPPT], const uint16_t* V, int t0, int pt, int cap) {
 #pragma unroll
     for (int k = 0; k < kSoPPT; k++) {
         const int q = min(pt + kSoProd * k, kSoPieces - 1);
-        v[k] = *reinterpret_cast<const uint4*>(V + (size_t)min(t0 + q / 8, cap) * HD + 8 * (q % 8));
+        v[k] = *reinterpret_cast<const uint4*>(V + (size_t)min(t0 + q / kSoDG, cap) * HD + 8 * (q % kSoDG));
     }
 }
 
@@ -794,7 +803,7 @@ __device__ __forceinline__ void so_products(const uint4 (&v)[kSoPPT], float (*bu
     for (int k = 0; k < kSoPPT; k++) {
         const int q = pt + kSoProd * k;
         if (q < kSoPieces) {
-            const int j = q / 8, dg = q % 8;
+            const int j = q / kSoDG, dg = q % kSoDG;
             const float p = pj[j];
             float f[8];
             bf16x8f(v[k], f);
@@ -806,46 +815,63 @@ __device__ __forceinline__ void so_products(const uint4 (&v)[kSoPPT], float (*bu
 }
 
 // o += the products of positions 0 .. cnt - 1 of lane d's row, one add at a time in position
-// order. Reads run 16 positions ahead of the adds; scheduling barriers keep them there. A partial
-// tile adds +0 past cnt, which leaves o unchanged (o is never -0: it starts at +0, and a sum of
-// nonzero addends that cancels rounds to +0).
+// order (cnt uniform). Whole 32-position chunks run double-buffered: the reads of chunk c + 1 are
+// issued before the 32 adds of chunk c, so an LDS round trip (longer than 16 dependent adds) is
+// hidden; scheduling barriers keep the reads there. A partial last chunk adds +0 past cnt, which
+// leaves o unchanged (o is never -0: it starts at +0, and a sum of nonzero addends that cancels
+// rounds to +0).
 __device__ __forceinline__ void so_chain(const float* row, int d, int cnt, float& o) {
+    constexpr int CH = 32;  // positions per chunk
     const int sw = 4 * (d >> 3);
-    auto ld = [&](float4 (&x)[4], int c) __attribute__((always_inline)) {
+    auto ld = [&](float4 (&x)[CH / 4], int c) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) x[k] = *reinterpret_cast<const float4*>(row + ((16 * c + 4 * k) ^ sw));
+        for (int k = 0; k < CH / 4; k++) x[k] = *reinterpret_cast<const float4*>(row + ((CH * c + 4 * k) ^ sw));
     };
-    auto add = [&](const float4 (&x)[4]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            o += x[k].x;
-            o += x[k].y;
-            o += x[k].z;
-            o += x[k].w;
-        }
+    // 16 dependent adds as one block: one wait for all of its operands before it, and the
+    // running sum kept in one register (the compiler otherwise waits on the LDS counter every
+    // four to eight adds and moves the sum between registers: 8.7 against 6.4 cycles an add)
+    auto add16 = [&](const float4& a, const float4& b, const float4& c, const float4& e) __attribute__((always_inline)) {
+        asm volatile(
+            "v_add_f32 %0, %0, %1\n\tv_add_f32 %0, %0, %2\n\tv_add_f32 %0, %0, %3\n\tv_add_f32 %0, %0, %4\n\t"
+            "v_add_f32 %0, %0, %5\n\tv_add_f32 %0, %0, %6\n\tv_add_f32 %0, %0, %7\n\tv_add_f32 %0, %0, %8\n\t"
+            "v_add_f32 %0, %0, %9\n\tv_add_f32 %0, %0, %10\n\tv_add_f32 %0, %0, %11\n\tv_add_f32 %0, %0, %12\n\t"
+            "v_add_f32 %0, %0, %13\n\tv_add_f32 %0, %0, %14\n\tv_add_f32 %0, %0, %15\n\tv_add_f32 %0, %0, %16"
+            : "+v"(o)
+            : "v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(b.x), "v"(b.y), "v"(b.z), "v"(b.w), "v"(c.x), "v"(c.y),
+              "v"(c.z), "v"(c.w), "v"(e.x), "v"(e.y), "v"(e.z), "v"(e.w));
     };
-    constexpr int C = kSoTile / 16;
-    if (cnt == kSoTile) {
-        float4 A[4], B[4];
-        ld(A, 0);
-        for (int c = 0; c < C; c += 2) {  // no exit inside the body: the reads stay ahead
-            ld(B, c + 1);
-            __builtin_amdgcn_sched_barrier(0);
-            add(A);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(A, min(c + 2, C - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            add(B);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    } else {
-        for (int c = 0; 16 * c < cnt; c++) {
-            float4 A[4];
-            ld(A, c);
-            const float f[16] = {A[0].x, A[0].y, A[0].z, A[0].w, A[1].x, A[1].y, A[1].z, A[1].w,
-                                 A[2].x, A[2].y, A[2].z, A[2].w, A[3].x, A[3].y, A[3].z, A[3].w};
+    auto add = [&](const float4 (&x)[CH / 4]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) o += 16 * c + i < cnt ? f[i] : 0.f;
+        for (int k = 0; k < CH / 4; k += 4) add16(x[k], x[k + 1], x[k + 2], x[k + 3]);
+    };
+    constexpr int C = kSoTile / CH;
+    const int full = cnt / CH;
+    float4 A[CH / 4], B[CH / 4];
+    ld(A, 0);
+    int c = 0;
+    for (; c + 2 <= full; c += 2) {  // A holds chunk c
+        ld(B, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        add(A);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(A, min(c + 2, C - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        add(B);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c < full) {  // an odd whole chunk
+        add(A);
+        c++;
+        if (CH * c < cnt) ld(A, c);
+    }
+    if (CH * c < cnt) {
+#pragma unroll
+        for (int k = 0; k < CH / 4; k++) {
+            const int j = CH * c + 4 * k;
+            o += j < cnt ? A[k].x : 0.f;
+            o += j + 1 < cnt ? A[k].y : 0.f;
+            o += j + 2 < cnt ? A[k].z : 0.f;
+            o += j + 3 < cnt ? A[k].w : 0.f;
         }
     }
 }
@@ -854,8 +880,7 @@ __device__ __forceinline__ void so_chain(const float* row, int d, int cnt, float
 
 template <int HD>
 __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
-    constexpr int PARTS = HD / 64;
-    constexpr int NW = kSoThreads / 64;
+    constexpr int PARTS = HD / kSoDims;
     __shared__ SoSmem S;
     hy_sgpr_pin(a.vc), hy_sgpr_pin(a.pos_dev), hy_sgpr_pin(a.pos0), hy_sgpr_pin(a.ao), hy_sgpr_pin(a.heads),
         hy_sgpr_pin(a.kv_heads), hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.sc), hy_sgpr_pin(a.segmax),
@@ -863,21 +888,22 @@ __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = blockIdx.x / PARTS, part = blockIdx.x % PARTS;
     const int g = h / (a.heads / a.kv_heads);
-    const uint16_t* V = a.vc + (size_t)g * a.ctx * HD + 64 * part;
-    const bool prd = wave >= 1;
-    const int pt = tid - 64;  // producer index
+    const uint16_t* V = a.vc + (size_t)g * a.ctx * HD + kSoDims * part;
+    const bool prd = wave >= 1 && wave != 4;        // producer wavefronts
+    const int pt = tid - (wave < 4 ? 64 : 128);     // producer index
     const int cap = a.ctx - 1;
-    float* sc = a.sc + (size_t)h * a.sc_stride;
+    const float* sc = a.sc + (size_t)h * a.sc_stride;
 
     // 0. loads that do not wait for the position, oldest first (their waits then leave the
-    //    younger ones in flight): this thread's eight scores and one segment maximum (masked by
-    //    the position below), then the producers' V pieces of the first three tiles
-    const int e0 = 8 * tid;
+    //    younger ones in flight): this thread's scores of the first window (positions
+    //    tid + kSoThreads i) and one segment maximum (masked by the position below), then the
+    //    producers' V pieces of the first three tiles
     const uint64_t etv = tid < 32 ? hy_exp_tab_entry(tid) : 0;  // expf table entry, into LDS before the max
-    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
-    if (e0 < a.sc_stride) {
-        s0 = *reinterpret_cast<const float4*>(sc + e0);
-        s1 = *reinterpret_cast<const float4*>(sc + e0 + 4);
+    float sv[kSoEPT];
+#pragma unroll
+    for (int i = 0; i < kSoEPT; i++) {
+        const int j = tid + kSoThreads * i;
+        sv[i] = j < a.sc_stride ? sc[j] : 0.f;
     }
     const float m0 = tid < a.seg_stride ? a.segmax[(size_t)h * a.seg_stride + tid] : -__builtin_inff();
     uint4 va[kSoPPT], vb[kSoPPT], vc[kSoPPT];
@@ -899,26 +925,50 @@ __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
     hy_lds_barrier();
     float mx = S.red[0];
 #pragma unroll
-    for (int w = 1; w < NW; w++) mx = fmaxf(mx, S.red[w]);
+    for (int w = 1; w < kSoNW; w++) mx = fmaxf(mx, S.red[w]);
 
-    // 2. e_j = expf(s_j - max) and their sum in position order (src/model.c:784-785); thread t
-    //    holds positions 8t .. 8t + 7 of a chunk
+    // 2. e_j = expf(s_j - max) and their sum in position order (src/model.c:784-785); the sum
+    //    takes thread t's addends as positions 8t .. 8t + 7 of a chunk
     const bool one = n <= kSplitWin;
-    float e[8];
     float sum;
     if (one) {
-        if (e0 < n) {
-            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        // each thread forms the exponentials of its round-robin positions (at most
+        // ceil(n / kSoThreads) each), then reads its eight consecutive ones back
 #pragma unroll
-            for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? hy_expf_tab(sv[i] - mx, S.etab) : 0.f;
+        for (int i = 0; i < kSoEPT; i++) {
+            const int j = tid + kSoThreads * i;
+            if (j < n) S.pj[j] = hy_expf_tab(sv[i] - mx, S.etab);
+        }
+        hy_lds_barrier();
+        float e[8];
+        const int e0 = 8 * tid;
+        if (e0 < n) {
+            const float4 x0 = *reinterpret_cast<const float4*>(S.pj + e0);
+            const float4 x1 = *reinterpret_cast<const float4*>(S.pj + e0 + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) e[i] = e0 + i < n ? xv[i] : 0.f;
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++) e[i] = 0.f;
         }
-        sum = hy_block_exact_sum8<NW, false>(e, S.exs, wave, lane);
+        sum = hy_block_exact_sum8<kSoNW, false>(e, S.exs, wave, lane);
+        // p_j = e_j * inv over this thread's own eight positions (read back above, so no other
+        // thread writes them); the first tile's barrier publishes them
+        const float inv = 1.0f / sum;
+        if (e0 < n) {
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) p[i] = e[i] * inv;
+            *reinterpret_cast<float4*>(S.pj + e0) = make_float4(p[0], p[1], p[2], p[3]);
+            *reinterpret_cast<float4*>(S.pj + e0 + 4) = make_float4(p[4], p[5], p[6], p[7]);
+        }
     } else {
         // chunks of kSplitWin addends; a later chunk's first addend is the running sum, so the
-        // chunk continues the one sequential sum. e_j goes back over s_j for the windows below.
+        // chunk continues the one sequential sum. The score row is only read: the head's other
+        // workgroups read the same row, so e_j is formed again from s_j where the windows of p_j
+        // are filled below.
+        float e[8];
         float carry = 0.f;
         for (int base = 0, c = 0; base < n; c++) {
             const int off = c ? 1 : 0;
@@ -929,45 +979,42 @@ __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
                     e[i] = carry;
                 } else if (j < n) {
                     e[i] = hy_expf_tab(sc[j] - mx, S.etab);
-                    sc[j] = e[i];
                 } else {
                     e[i] = 0.f;
                 }
             }
-            carry = hy_block_exact_sum8<NW, false>(e, S.exs, wave, lane);
-            __syncthreads();  // the sum's LDS is written again; the e_j stores are seen below
+            carry = hy_block_exact_sum8<kSoNW, false>(e, S.exs, wave, lane);
+            __syncthreads();  // the sum's LDS is written again by the next chunk
             base += kSplitWin - off;
         }
         sum = carry;
     }
     const float inv = 1.0f / sum;
 
-    // 3. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16), p_j = e_j * inv. p_j goes
-    //    to LDS a window of kSplitWin positions at a time (a barrier after each fill), then one
-    //    barrier per tile: before barrier t the producers have formed tile t into buffer t % 2,
-    //    after it the chain adds tile t (tile t - 1's buffer was read before barrier t, when the
-    //    producers fill it with tile t + 1).
+    // 3. o[d] = sum_j p_j * V_j[d] in position order (axpy_bf16), p_j = e_j * inv. Rows past
+    //    kSplitWin: the producers fill p_j into LDS a window at a time (a barrier after each
+    //    fill). Then one barrier per tile: before barrier t the producers have formed tile t into
+    //    buffer t % 2, after it the chain adds tile t (tile t - 1's buffer was read before
+    //    barrier t, when the producers fill it with tile t + 1).
     constexpr int WT = kSplitWin / kSoTile;  // tiles per window
     const int tiles = (n + kSoTile - 1) / kSoTile;
-    if (one) {
-        if (e0 < n) {
-            float p[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) p[i] = e[i] * inv;
-            *reinterpret_cast<float4*>(S.pj + e0) = make_float4(p[0], p[1], p[2], p[3]);
-            *reinterpret_cast<float4*>(S.pj + e0 + 4) = make_float4(p[4], p[5], p[6], p[7]);
+    if (wave == 4) {
+        // the chain's SIMD neighbour: the barriers of the producers' steps and nothing else
+        for (int t = 0; t < tiles; t++) {
+            if (t % WT == 0) hy_lds_barrier();
+            hy_lds_barrier();
         }
-    }
-    float o = 0.f;
-    if (!prd) {
+    } else if (!prd) {
         __builtin_amdgcn_s_setprio(3);  // the chain is the critical path: its adds issue first
-        const float* row = &S.prod[0][lane][0];
+        const int d = lane % kSoDims;   // lanes past kSoDims repeat a chain and store nothing
+        const float* row = &S.prod[0][d][0];
+        float o = 0.f;
         for (int t = 0; t < tiles; t++) {
             if (t % WT == 0) hy_lds_barrier();  // the window's p_j
             hy_lds_barrier();
-            so_chain(row + (t & 1) * 64 * kSoPad, lane, min(kSoTile, n - t * kSoTile), o);
+            so_chain(row + (t & 1) * kSoDims * kSoPad, d, min(kSoTile, n - t * kSoTile), o);
         }
-        a.ao[(size_t)h * HD + 64 * part + lane] = o;
+        if (lane < kSoDims) a.ao[(size_t)h * HD + kSoDims * part + lane] = o;
     } else {
         // one step per tile, unrolled by three over three register sets of V pieces, each
         // refilled three tiles ahead: every load is issued a full three tiles before its use and
@@ -977,7 +1024,7 @@ __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
                 if (t % WT == 0) {
                     if (!one) {
                         const int w0 = t * kSoTile, wn = min(kSplitWin, n - w0);
-                        for (int j = pt; j < wn; j += kSoProd) S.pj[j] = sc[w0 + j] * inv;
+                        for (int j = pt; j < wn; j += kSoProd) S.pj[j] = hy_expf_tab(sc[w0 + j] - mx, S.etab) * inv;
                     }
                     hy_lds_barrier();
                 }
@@ -999,7 +1046,7 @@ hipError_t launch_attn_split(const Attn1Args& a, hipStream_t s) {
         !a.segmax || a.sc_stride < split_sc_stride(a.ctx) || a.seg_stride < split_seg_stride(a.ctx))
         return hipErrorNotSupported;
     const dim3 g1(min(split_seg_stride(a.ctx), kSpGridX), a.kv_heads);
-    const int g2 = a.heads * (a.hdim / 64);
+    const int g2 = a.heads * (a.hdim / kSoDims);
     switch (a.hdim) {
     case 64:
         k_attn_scores<64><<<g1, kSpThreads, 0, s>>>(a);

@@ -220,7 +220,7 @@ struct Attn1Args {
     int heads, kv_heads, hdim, rope_half, ctx;
     float eps;
     // split form only (launch_attn_split): scores and per-segment maxima of each query head
-    float* sc;             // [heads][sc_stride] fp32 scores, then expf(s - max) for rows > kSplitWin
+    float* sc;             // [heads][sc_stride] fp32 scores (written by k_attn_scores, only read after)
     float* segmax;         // [heads][seg_stride] maximum score of each kSplitMaxSeg positions
     int sc_stride, seg_stride;
 };
