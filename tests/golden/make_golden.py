@@ -18,15 +18,15 @@ scalar ISA (the bit-exact contract of the HIP backend):
                   The reference's own greedy loop (gen_ids, src/model.c:914-958, through
                   hymt2_debug_generate_ids) runs the chat prompt whose encoding is the config's
                   prompt ids: config 3 = 64 prompt ids then 128 greedy ids; config 4 = 1024 prompt
-                  ids then 32 greedy ids. Logits (hymt2_debug_logits) are stored as a sha256 of
-                  their bits plus the top 32 (index, value) pairs: at the end of the prompt and,
-                  for config 3, after the prompt and the first 127 generated ids (the input of
-                  the loop's last forward). A control run at the auto-detected ISA records how
+                  ids then 256 greedy ids. Logits (hymt2_debug_logits) are stored as a sha256 of
+                  their bits plus the top 32 (index, value) pairs: at the end of the prompt and
+                  after the prompt and all generated ids but the last (the input of the loop's
+                  last forward). A control run at the auto-detected ISA records how
                   many leading greedy ids agree with the scalar run.
 
 Inputs are stored in the fixtures (or, for the models, regenerated from a seed and checked
 against a stored digest). Run from the repository root: python tests/golden/make_golden.py
-[--baseline]
+[--baseline [config3|config4]]
 """
 import hashlib
 import os
@@ -123,15 +123,18 @@ def ref_greedy(rm, text: str, n_gen: int) -> np.ndarray:
     return ids.astype(np.int32)
 
 
-def baseline_fixtures():
+def baseline_fixtures(which=("config3", "config4")):
     os.environ.update(HYMT2_DEVICE="cpu", HYMT2_ISA="scalar", HYMT2_REPACK="1", HYMT2_PREFAULT="0")
-    baseline_fixture("config3", synth.CONFIG3, synth.CONFIG3["n_gen"], last_logits=True)
-    baseline_fixture("config4", synth.CONFIG4, 32, last_logits=False)
+    if "config3" in which:
+        baseline_fixture("config3", synth.CONFIG3, synth.CONFIG3["n_gen"], last_logits=True)
+    if "config4" in which:
+        baseline_fixture("config4", synth.CONFIG4, synth.CONFIG4["n_gen"], last_logits=True)
 
 
 def main():
     if "--baseline" in sys.argv:
-        baseline_fixtures()
+        rest = [a for a in sys.argv[sys.argv.index("--baseline") + 1:] if not a.startswith("-")]
+        baseline_fixtures(tuple(rest) or ("config3", "config4"))
         return
     R.set_isa("scalar")
     L = R.load()

@@ -4,8 +4,8 @@ The fixtures (tests/golden/baseline_config3.npz, baseline_config4.npz) hold what
 host compiled from its sources computes at the scalar ISA on the same seeded 1.8B-shaped models
 and prompts (tests/golden/make_golden.py --baseline): gen_ids (src/model.c:914-958) on the chat
 prompt whose encoding is the config's prompt ids, and hymt2_debug_logits at the end of the prompt
-(and, for config 3, at the input of the loop's last forward). Ids are compared exactly, logits by
-the sha256 of their bits."""
+and at the input of the loop's last forward. Ids are compared exactly, logits by the sha256 of
+their bits."""
 import hashlib
 import os
 
@@ -57,14 +57,19 @@ def test_config3_greedy_identity(backend):
 
 def test_config4_greedy_identity(backend):
     """1024 prompt ids in 128-token chunks (int8-MFMA GEMMs, chunk attention over the growing KV
-    cache), then 32 greedy ids; the logits at the end of the 128-token-chunk prefill."""
+    cache, pipelined over the layers), then all 256 greedy ids of the decode (single-token steps
+    at positions 1024-1279, the split attention); the logits at the end of the 128-token-chunk
+    prefill and after 1024 + 255 positions (10 chunks, the last one ragged), through the reference
+    host's boundary (fused_forward in chunks of 128)."""
     f, model = fixture("config4")
     prompt, want = f["prompt"], f["greedy"]
-    assert len(prompt) == 1024 and len(want) == 32
+    assert len(prompt) == 1024 and len(want) == 256
     fm = lib.FusedModel(backend, model)
     try:
-        ids, _ = fm.generate_device(prompt, len(want), chunk=128)
+        ids, st = fm.generate_device(prompt, len(want), chunk=128)
         assert np.array_equal(ids, want), f"first difference at {np.argmax(ids != want)}"
+        assert st.decode_steps == len(want) - 1
         check_logits(f, "prompt_logits", fm.prefill(list(prompt), batch=128))
+        check_logits(f, "last_logits", fm.prefill(list(prompt) + list(want[:-1]), batch=128))
     finally:
         fm.close()
