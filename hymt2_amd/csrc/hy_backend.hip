@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -87,9 +88,21 @@ struct Fused {
     int* ids = nullptr;
     int ids_cap = 0;
     int gen_total = 0;   // positions of the current device loop (0: no loop begun)
-    int gen_steps = 0;   // steps enqueued so far
+    int gen_steps = 0;   // steps enqueued so far (positions processed, the reused prefix included)
     int gen_prompt = 0, gen_vocab = 0;
+    int gen_keep = 0;    // prompt positions whose K/V the loop reused (its first step's position)
     MvWeight gen_embd{};  // embedding of the current device loop
+    // stop ids of the device loop and the first stop position (FinishArgs::stop), and the
+    // host-mapped copy of that position the host loop polls
+    int* stop = nullptr;
+    int* stop_host = nullptr;
+    int* stop_host_dev = nullptr;
+    // the ids whose K/V the cache holds after the last hymt2_hip_generate_ids call (positions
+    // 0 .. cache_n - 1), and what they were computed with; any other writer of the cache
+    // (fused_forward, the other device-loop entry points) sets cache_n to 0
+    std::vector<int> cache_tok;
+    int cache_n = 0;
+    std::vector<const void*> cache_sig;
     // attention scratch of the split form (launch_attn_split): scores [heads][sc_stride] and
     // segment maxima [heads][seg_stride]
     float *sc = nullptr, *segmax = nullptr;
@@ -120,6 +133,7 @@ struct Ctx {
     size_t out_cap = 0;
     Fused* f = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    hipEvent_t ring[2] = {nullptr, nullptr};  // the last two decode launches of hymt2_hip_generate_ids
     uint8_t* scratch = nullptr;  // this device's address of `scratch` (hymt2_hip_matmul_static), or null
     int split_from = kSplitFromDefault;  // single-token attention at positions >= this: split form
     int pipe_depth = kPipeMax;           // chunks in flight in gen_prefill (1: one chunk after another)
@@ -596,6 +610,8 @@ static void free_fused(Fused* f) {
     for (void* p : dev)
         if (p) (void)hipFree(p);
     if (f->in_host) (void)hipHostFree(f->in_host);
+    if (f->stop) (void)hipFree(f->stop);
+    if (f->stop_host) (void)hipHostFree(f->stop_host);
     delete f;
 }
 
@@ -665,7 +681,10 @@ static bool hip_fused_prepare(void* impl, const hymt2_fused_args* a) {
          dalloc(c, &f->kc, (size_t)a->n_layer * a->ctx * KV * 2) &&
          dalloc(c, &f->vc, (size_t)a->n_layer * a->ctx * KV * 2) && dalloc(c, &f->slots, (size_t)kArgSlots * 8) &&
          dalloc(c, &f->sc, (size_t)a->heads * split_sc_stride(a->ctx) * 4) &&
-         dalloc(c, &f->segmax, (size_t)a->heads * split_seg_stride(a->ctx) * 4);
+         dalloc(c, &f->segmax, (size_t)a->heads * split_seg_stride(a->ctx) * 4) &&
+         dalloc(c, &f->stop, (kStopIds + 1) * sizeof(int));
+    ok = ok && hipHostMalloc(&f->stop_host, 64, hipHostMallocMapped) == hipSuccess &&
+         hipHostGetDevicePointer(reinterpret_cast<void**>(&f->stop_host_dev), f->stop_host, 0) == hipSuccess;
     if (!ok) {
         free_fused(f);
         return false;
@@ -944,6 +963,7 @@ static bool hip_fused_forward(void* impl, hymt2_fused_args* a) {
         a->pos0 < 0 || a->pos0 + a->nt > c->f->ctx)
         return false;
     Fused* f = c->f;
+    f->cache_n = 0;  // this forward writes K/V the device loop's prefix record does not know
     const int nt = a->nt;
     const size_t hbytes = (size_t)nt * f->hidden * 4;
     const bool logits = a->want_logits && a->outw && a->logits;
@@ -993,6 +1013,8 @@ static void hip_destroy_impl(void* impl) {
     if (c->out) (void)hipFree(c->out);
     for (hipEvent_t e : c->ev)
         if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : c->ring)
+        if (e) (void)hipEventDestroy(e);
     if (c->s) (void)hipStreamDestroy(c->s);
     delete c;
 }
@@ -1031,6 +1053,7 @@ void* hymt2_hip_open(char* info, size_t cap) {
         return nullptr;
     }
     for (hipEvent_t& e : c->ev) (void)hipEventCreate(&e);
+    for (hipEvent_t& e : c->ring) (void)hipEventCreateWithFlags(&e, hipEventDisableTiming);
     c->scratch = scratch_address(c->dev);  // device 0 is current
     if (info && cap) snprintf(info, cap, "%s (%s, %d CUs)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName,
                               prop.multiProcessorCount);
@@ -1114,11 +1137,14 @@ int hymt2_hip_attn_split_from(void* impl, int from) {
     return 0;
 }
 
-int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out,
-                        const int* prompt, int n_prompt, int n_total) {
-    Ctx* c = static_cast<Ctx*>(impl);
-    if (!c || c->broken || !shape || !prompt || n_prompt < 1 || n_total <= n_prompt) return -1;
-    if (!hip_fused_prepare(impl, shape)) return -2;
+// Begins a device loop over positions 0 .. n_total - 1 whose first keep positions (keep <
+// n_prompt) already hold the prompt's K/V; stop ids (at most kStopIds) are recorded by k_finish.
+static int gen_begin_at(Ctx* c, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
+                        int n_prompt, int n_total, int keep, const int* stop_ids, int n_stop) {
+    if (!c || c->broken || !shape || !prompt || n_prompt < 1 || n_total <= n_prompt || keep < 0 || keep >= n_prompt ||
+        n_stop < 0 || n_stop > kStopIds || (n_stop && !stop_ids))
+        return -1;
+    if (!hip_fused_prepare(c, shape)) return -2;
     Fused* f = c->f;
     f->gen_total = 0;
     const DW* e = dw(embd);
@@ -1163,8 +1189,9 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
         auto one_step = [&](int v) {
             if (!enqueue_layers(c, shape, 1, 0, f->d_pos, v == 1) || !enqueue_head(c, shape, 1, true, vocab_out))
                 return false;
-            const FinishArgs fa{f->slots, f->head_slots, f->ids, f->d_pos, n_prompt, e->mw, f->d_h, f->hidden,
-                                n_total, f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
+            const FinishArgs fa{f->slots,  f->head_slots, f->ids,    f->d_pos,     n_prompt, e->mw,
+                                f->d_h,    f->hidden,     n_total,   f->rope_c,    f->rope_s, f->d_rope,
+                                f->rope_half, f->ctx,     f->stop,   f->stop_host_dev};
             return launch_finish(fa, c->s) == hipSuccess;
         };
         for (int v = 0; v < 2; v++) {
@@ -1179,10 +1206,16 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
         }
         f->sig_step = sig;
     }
-    // start state: ids[0..n_prompt) = prompt, pos = 0, h = embedding of ids[0]
+    // start state: ids[0..n_prompt) = prompt, pos = keep, h = embedding of ids[keep]; the stop
+    // ids (-1 pads: no argmax equals it) and no stop yet
+    int stv[kStopIds + 1];
+    for (int j = 0; j < kStopIds; j++) stv[j] = j < n_stop ? stop_ids[j] : -1;
+    stv[kStopIds] = INT_MAX;
+    *f->stop_host = INT_MAX;
     memset(f->in_host, 0, f->in_bytes);
-    stage_pos(f, shape, 0);
+    stage_pos(f, shape, keep);
     if (hipMemcpyAsync(f->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, c->s) != hipSuccess ||
+        hipMemcpyAsync(f->stop, stv, sizeof stv, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         hipMemcpyAsync(f->in_dev, f->in_host, kInH, hipMemcpyHostToDevice, c->s) != hipSuccess ||
         launch_embed(f->ids, f->d_pos, e->mw, f->d_h, f->hidden, c->s) != hipSuccess ||
         hipStreamSynchronize(c->s) != hipSuccess) {
@@ -1191,11 +1224,19 @@ int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* e
         return -8;
     }
     f->gen_total = n_total;
-    f->gen_steps = 0;
+    f->gen_steps = keep;
+    f->gen_keep = keep;
     f->gen_prompt = n_prompt;
     f->gen_vocab = vocab_out;
     f->gen_embd = e->mw;
     return 0;
+}
+
+int hymt2_hip_gen_begin(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out,
+                        const int* prompt, int n_prompt, int n_total) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (c && c->f) c->f->cache_n = 0;  // a loop the prefix record does not follow
+    return gen_begin_at(c, shape, embd, vocab_out, prompt, n_prompt, n_total, 0, nullptr, 0);
 }
 
 // Whether the pipelined prefill applies: panel weights of the model's shapes in every layer
@@ -1238,15 +1279,16 @@ static bool ensure_pipe(Ctx* c, Fused* f) {
 // hidden state in its slot for the head.
 static bool enqueue_prefill_pipe(Ctx* c, const hymt2_fused_args* a, int chunk, const float** h_last) {
     Fused* f = c->f;
-    const int np = f->gen_prompt, nl = f->n_layer, depth = c->pipe_depth;
-    const int nc = (np + chunk - 1) / chunk;
+    const int np = f->gen_prompt, nl = f->n_layer, depth = c->pipe_depth, p0 = f->gen_keep;
+    const int nc = (np - p0 + chunk - 1) / chunk;  // chunks of positions p0 .. np - 1
     const int H = f->hidden, F = f->ffn, Q = f->qdim, KV = f->kvdim;
     const size_t B = HY_MAX_CHUNK;
     for (int g0 = 0; g0 < nc; g0 += depth) {
         const int m = std::min(depth, nc - g0);
-        auto tokens = [&](int i) { return std::min(chunk, np - (g0 + i) * chunk); };
+        auto tokens = [&](int i) { return std::min(chunk, np - p0 - (g0 + i) * chunk); };
         for (int i = 0; i < m; i++)
-            HIPCHK(c, launch_embed_rows(f->ids, (g0 + i) * chunk, tokens(i), f->gen_embd, f->p_h + i * B * H, H, c->s));
+            HIPCHK(c, launch_embed_rows(f->ids, p0 + (g0 + i) * chunk, tokens(i), f->gen_embd, f->p_h + i * B * H, H,
+                                        c->s));
         for (int st = 0; st < m + nl - 1; st++) {
             const int i0 = std::max(0, st - nl + 1), i1 = std::min(m - 1, st);
             const int nj = i1 - i0 + 1;
@@ -1298,7 +1340,7 @@ static bool enqueue_prefill_pipe(Ctx* c, const hymt2_fused_args* a, int chunk, c
                 at.k_norm = f->norm_ptr(li, 3);
                 at.rope_cos = f->rope_c;
                 at.rope_sin = f->rope_s;
-                at.pos0 = (g0 + i) * chunk;
+                at.pos0 = p0 + (g0 + i) * chunk;
                 at.nt = nt;
                 at.heads = f->heads;
                 at.kv_heads = f->kv_heads;
@@ -1343,7 +1385,7 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     Ctx* c = static_cast<Ctx*>(impl);
     if (!c || c->broken || !c->f || !c->f->gen_total || !shape || !shape->layers) return -1;
     Fused* f = c->f;
-    if (f->gen_steps != 0 || chunk < 1 || chunk > HY_MAX_CHUNK || !same_shape(f, shape)) {
+    if (f->gen_steps != f->gen_keep || chunk < 1 || chunk > HY_MAX_CHUNK || !same_shape(f, shape)) {
         set_err(c, "gen_prefill: needs a fresh loop of the same shape and 1 <= chunk <= %d", HY_MAX_CHUNK);
         return -2;
     }
@@ -1352,8 +1394,8 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
         set_err(c, "gen_prefill: weights differ from the ones gen_begin captured");
         return -2;
     }
-    const int np = f->gen_prompt;
-    if (chunk > 1 && np > chunk && c->pipe_depth > 1 && pipe_supported(f, shape)) {
+    const int np = f->gen_prompt, p0 = f->gen_keep;
+    if (chunk > 1 && np - p0 > chunk && c->pipe_depth > 1 && pipe_supported(f, shape)) {
         const float* h_last = nullptr;
         if (!ensure_pipe(c, f) || !enqueue_prefill_pipe(c, shape, chunk, &h_last) ||
             !enqueue_head(c, shape, 1, true, f->gen_vocab, h_last)) {
@@ -1361,7 +1403,7 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
             return -3;
         }
     } else {
-        for (int i = 0; i < np; i += chunk) {
+        for (int i = p0; i < np; i += chunk) {
             const int nt = std::min(chunk, np - i);
             if (launch_embed_rows(f->ids, i, nt, f->gen_embd, f->d_h, f->hidden, c->s) != hipSuccess ||
                 !enqueue_layers(c, shape, nt, i, nullptr, nt == 1 && split_at(c, f, i)) ||
@@ -1373,8 +1415,9 @@ int hymt2_hip_gen_prefill(void* impl, const hymt2_fused_args* shape, int chunk) 
     }
     // position np - 1 has been processed: the finishing kernel records the first generated id,
     // embeds it and advances the step counter to np, where the step graph continues
-    const FinishArgs fa{f->slots, f->head_slots, f->ids, f->d_pos, np, f->gen_embd, f->d_h, f->hidden, f->gen_total,
-                        f->rope_c, f->rope_s, f->d_rope, f->rope_half, f->ctx};
+    const FinishArgs fa{f->slots,  f->head_slots, f->ids,       f->d_pos,  np,       f->gen_embd,
+                        f->d_h,    f->hidden,     f->gen_total, f->rope_c, f->rope_s, f->d_rope,
+                        f->rope_half, f->ctx,     f->stop,      f->stop_host_dev};
     if (launch_set_int(f->d_pos, np - 1, c->s) != hipSuccess || launch_finish(fa, c->s) != hipSuccess) {
         set_err(c, "gen_prefill: launch failed");
         c->broken = true;
@@ -1427,7 +1470,8 @@ int hymt2_hip_generate_chunked(void* impl, const hymt2_fused_args* shape, hy_dwe
                                hymt2_gen_stats* stats) {
     Ctx* c = static_cast<Ctx*>(impl);
     if (!c || !out_ids || n_gen < 1 || chunk < 1) return -1;
-    int rc = hymt2_hip_gen_begin(impl, shape, embd, vocab_out, prompt, n_prompt, n_prompt + n_gen);
+    if (c->f) c->f->cache_n = 0;  // a loop the prefix record does not follow
+    int rc = gen_begin_at(c, shape, embd, vocab_out, prompt, n_prompt, n_prompt + n_gen, 0, nullptr, 0);
     if (rc) return rc;
     (void)hipEventRecord(c->ev[0], c->s);
     if ((rc = chunk > 1 ? hymt2_hip_gen_prefill(impl, shape, chunk) : hymt2_hip_gen_steps(impl, n_prompt))) return rc;
@@ -1443,6 +1487,7 @@ int hymt2_hip_generate_chunked(void* impl, const hymt2_fused_args* shape, hy_dwe
         stats->decode_ms = b;
         stats->prefill_steps = n_prompt;
         stats->decode_steps = n_gen - 1;
+        stats->cached_tokens = 0;
     }
     return n_gen;
 }
@@ -1450,6 +1495,110 @@ int hymt2_hip_generate_chunked(void* impl, const hymt2_fused_args* shape, hy_dwe
 int hymt2_hip_generate(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out, const int* prompt,
                        int n_prompt, int n_gen, int* out_ids, hymt2_gen_stats* stats) {
     return hymt2_hip_generate_chunked(impl, shape, embd, vocab_out, prompt, n_prompt, n_gen, 1, out_ids, stats);
+}
+
+// What the K/V of a device-loop sequence depends on besides its ids: the weights, the norms,
+// the RoPE tables and eps (the shape is the Fused's own).
+static std::vector<const void*> cache_sig(const hymt2_fused_args* a, const hy_dweight* embd) {
+    std::vector<const void*> s = weight_sig(a);
+    s.push_back(embd);
+    s.push_back(a->rope_cos);
+    s.push_back(a->rope_sin);
+    for (int li = 0; li < a->n_layer; li++) {
+        const hymt2_fused_layer& L = a->layers[li];
+        for (const void* p : {(const void*)L.attn_norm, (const void*)L.ffn_norm, (const void*)L.q_norm,
+                              (const void*)L.k_norm})
+            s.push_back(p);
+    }
+    uint32_t eb;
+    memcpy(&eb, &a->eps, 4);
+    s.push_back(reinterpret_cast<const void*>((uintptr_t)eb));
+    return s;
+}
+
+int hymt2_hip_generate_ids(void* impl, const hymt2_fused_args* shape, hy_dweight* embd, int vocab_out,
+                           const int* prompt, int n_prompt, int max_tokens, const hymt2_gen_opts* opts,
+                           int* out_ids, hymt2_gen_stats* stats) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || c->broken || !shape || !shape->layers || !prompt || n_prompt < 1 || !out_ids) return -1;
+    const int chunk = opts && opts->chunk > 0 ? opts->chunk : 1;
+    const int n_stop = opts ? opts->n_stop : 0;
+    if (chunk > HY_MAX_CHUNK || n_stop < 0 || n_stop > kStopIds || (n_stop && !opts->stop_ids)) {
+        set_err(c, "generate_ids: chunk must be 1..%d and at most %d stop ids", HY_MAX_CHUNK, kStopIds);
+        return -1;
+    }
+    if (!hip_fused_prepare(impl, shape)) return -2;
+    Fused* f = c->f;
+    // max_tokens capped at the positions the context has left (src/model.c:925-926)
+    if (n_prompt + max_tokens > f->ctx) max_tokens = f->ctx - n_prompt;
+    if (max_tokens <= 0) {
+        set_err(c, "generate_ids: a prompt of %d ids leaves no room in ctx %d", n_prompt, f->ctx);
+        return -4;
+    }
+    // the K/V of the longest common prefix with the cached sequence, at most n - 1 positions
+    // (src/model.c:930-936)
+    const std::vector<const void*> sig = cache_sig(shape, embd);
+    int keep = 0;
+    if (opts && opts->reuse_prefix && f->cache_sig == sig)
+        while (keep < f->cache_n && keep < n_prompt - 1 && f->cache_tok[keep] == prompt[keep]) keep++;
+    f->cache_n = 0;  // until this loop has finished
+    int rc = gen_begin_at(c, shape, embd, vocab_out, prompt, n_prompt, n_prompt + max_tokens, keep,
+                          n_stop ? opts->stop_ids : nullptr, n_stop);
+    if (rc) return rc;
+    (void)hipEventRecord(c->ev[0], c->s);
+    if ((rc = chunk > 1 ? hymt2_hip_gen_prefill(impl, shape, chunk) : hymt2_hip_gen_steps(impl, n_prompt - keep)))
+        return rc;
+    (void)hipEventRecord(c->ev[1], c->s);
+    // decode steps in launches of kStepsPerGraph, at most two in flight: before a launch the host
+    // waits for the one two launches back and reads the stop position, so the GPU always has the
+    // next launch queued and at most two launches' steps run on past a stop (their K/V lies past
+    // the sequence's end and their ids are not read)
+    const int total = max_tokens - 1;
+    int done = 0;
+    for (int launch = 0; done < total; launch++) {
+        if (launch >= 2) {
+            if (hipEventSynchronize(c->ring[launch & 1]) != hipSuccess) {
+                set_err(c, "generate_ids: event wait failed");
+                c->broken = true;
+                return -3;
+            }
+            if (*reinterpret_cast<volatile int*>(f->stop_host) != INT_MAX) break;
+        }
+        const int k = std::min(kStepsPerGraph, total - done);
+        if ((rc = hymt2_hip_gen_steps(impl, k))) return rc;
+        (void)hipEventRecord(c->ring[launch & 1], c->s);
+        done += k;
+    }
+    (void)hipEventRecord(c->ev[2], c->s);
+    int stop_at = INT_MAX;
+    if (hipMemcpyAsync(&stop_at, f->stop + kStopIds, sizeof stop_at, hipMemcpyDeviceToHost, c->s) != hipSuccess ||
+        hipStreamSynchronize(c->s) != hipSuccess) {
+        set_err(c, "generate_ids: reading the stop position failed");
+        c->broken = true;
+        return -3;
+    }
+    // the ids before the stop id, or max_tokens of them (src/model.c:944-951)
+    const bool stopped = stop_at != INT_MAX;
+    const int ng = stopped ? stop_at - n_prompt : max_tokens;
+    if (ng > 0 && (rc = hymt2_hip_gen_read(impl, out_ids, n_prompt, ng)) != ng) return rc < 0 ? rc : -3;
+    // the cache holds the prompt and the ids fed back: all generated ids after a stop, all but
+    // the last after a full run (src/model.c:948-953)
+    const int fed = stopped ? ng : ng - 1;
+    f->cache_tok.assign(prompt, prompt + n_prompt);
+    f->cache_tok.insert(f->cache_tok.end(), out_ids, out_ids + fed);
+    f->cache_n = n_prompt + fed;
+    f->cache_sig = sig;
+    if (stats) {
+        float a = 0.f, b = 0.f;
+        (void)hipEventElapsedTime(&a, c->ev[0], c->ev[1]);
+        (void)hipEventElapsedTime(&b, c->ev[1], c->ev[2]);
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->prefill_steps = n_prompt - keep;
+        stats->decode_steps = done;
+        stats->cached_tokens = keep;
+    }
+    return ng;
 }
 
 bool hymt2_hip_matmul_static(void* impl, hy_dweight* const* ws, float* const* outs, int cnt,

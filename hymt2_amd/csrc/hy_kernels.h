@@ -268,7 +268,13 @@ struct FinishArgs {
     const float* rope_sin; // rope_cur (cos then sin) for the next step's attention
     float* rope_cur;
     int rope_half, ctx;
+    // stop ids of the loop (tok_is_stop, src/tokenizer.c:179): stop[0..kStopIds) (-1 pads), then
+    // stop[kStopIds] = the first position whose generated id is one of them (INT_MAX: none yet);
+    // stop_host (host-mapped) receives the same position when it is set
+    int* stop;
+    int* stop_host;
 };
+constexpr int kStopIds = 8;
 hipError_t launch_finish(const FinishArgs& a, hipStream_t s);
 // True for the embedding kinds embed_row dequantizes (src/kernels.c:1304-1329).
 inline bool embed_kind(int kind) {

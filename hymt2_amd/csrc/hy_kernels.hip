@@ -1194,8 +1194,13 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
     hy_sgpr_pin(a.slots), hy_sgpr_pin(a.nslots), hy_sgpr_pin(a.ids), hy_sgpr_pin(a.step), hy_sgpr_pin(a.n_prompt),
         hy_sgpr_pin(a.E.w), hy_sgpr_pin(a.E.kind), hy_sgpr_pin(a.h), hy_sgpr_pin(a.H), hy_sgpr_pin(a.n_total),
         hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin), hy_sgpr_pin(a.rope_half),
-        hy_sgpr_pin(a.ctx), hy_sgpr_pin(blockDim.x);
+        hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.stop), hy_sgpr_pin(a.stop_host), hy_sgpr_pin(blockDim.x);
     __shared__ unsigned long long kw[4];
+    // the stop ids and the first stop position (uniform: loaded with the arguments, off the
+    // critical path)
+    int stv[kStopIds + 1];
+#pragma unroll
+    for (int j = 0; j <= kStopIds; j++) stv[j] = a.stop[j];
     // the slot maxima, eight loads in flight per thread; indices past the end re-read the last
     // slot (a maximum is unchanged by repeats), so every load is unconditional
     unsigned long long key = 0ull;
@@ -1226,7 +1231,18 @@ __global__ __launch_bounds__(256) void k_finish(FinishArgs a) {
     embed_row(a.E, next_tok, a.h, a.H);
     __syncthreads();
     if (threadIdx.x == 0) {
-        if (nx >= a.n_prompt && nx < a.n_total) a.ids[nx] = best;
+        if (nx >= a.n_prompt && nx < a.n_total) {
+            a.ids[nx] = best;
+            // the reference's loop ends before a stop id (src/model.c:949); the device loop runs
+            // on and only records the first position where that happened
+            bool hit = false;
+#pragma unroll
+            for (int j = 0; j < kStopIds; j++) hit |= best == stv[j];
+            if (hit && stv[kStopIds] > nx) {
+                a.stop[kStopIds] = nx;
+                *a.stop_host = nx;
+            }
+        }
         *a.step = nx;
     }
 }

@@ -26,7 +26,11 @@ LIB_PATH = os.path.join(HERE, "libhymt2_hip.so")
 
 class GenStats(C.Structure):
     _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double),
-                ("prefill_steps", C.c_int), ("decode_steps", C.c_int)]
+                ("prefill_steps", C.c_int), ("decode_steps", C.c_int), ("cached_tokens", C.c_int)]
+
+
+class GenOpts(C.Structure):
+    _fields_ = [("stop_ids", C.c_void_p), ("n_stop", C.c_int), ("chunk", C.c_int), ("reuse_prefix", C.c_int)]
 
 
 _lib = None
@@ -65,6 +69,8 @@ def load():
         "hymt2_hip_generate_chunked": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i, i, vp,
                                            C.POINTER(GenStats)]),
         "hymt2_hip_gen_read": (i, [vp, vp, i, i]),
+        "hymt2_hip_generate_ids": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i, C.POINTER(GenOpts), vp,
+                                       C.POINTER(GenStats)]),
         "hymt2_hip_head": (i, [vp, vp, vp, vp, C.c_float, vp, i, vp]),
         "hymt2_hip_ffn_in": (i, [vp, vp, vp, vp, vp, C.c_float, vp]),
         "hymt2_hip_matmul_static": (C.c_bool, [vp, C.POINTER(vp), C.POINTER(vp), i, vp, i]),
@@ -83,7 +89,7 @@ EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops",
            "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_selftest_sqsum", "hymt2_hip_generate", "hymt2_hip_gen_begin",
            "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in",
            "hymt2_hip_gen_prefill", "hymt2_hip_generate_chunked", "hymt2_hip_matmul_static",
-           "hymt2_hip_attn_split_from", "hymt2_hip_prefill_pipeline"]
+           "hymt2_hip_attn_split_from", "hymt2_hip_prefill_pipeline", "hymt2_hip_generate_ids"]
 
 
 def abi_layout() -> dict:
@@ -254,6 +260,24 @@ class FusedModel:
         if rc != n_gen:
             raise RuntimeError(f"hymt2_hip_generate failed ({rc}): {self.b.last_error()}")
         return out, st
+
+    def generate_ids(self, prompt, max_tokens: int, stop_ids=(), chunk: int = 1, reuse_prefix: bool = False):
+        """The reference's greedy loop gen_ids (src/model.c:914-958) on the device: ids before a
+        stop id (or max_tokens of them), the prompt in chunks of `chunk`, optionally reusing the
+        K/V prefix of the previous call's sequence. Returns (ids, GenStats)."""
+        if self.embd_dev is None:
+            raise ValueError("device generation needs an F16/F32/Q8_0/Q4_K/Q6_K embedding table")
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        stop = np.ascontiguousarray(stop_ids, dtype=np.int32)
+        out = np.zeros(max(max_tokens, 1), dtype=np.int32)
+        opts = GenOpts(stop.ctypes.data if len(stop) else None, len(stop), chunk, int(reuse_prefix))
+        st = GenStats()
+        rc = self.b.L.hymt2_hip_generate_ids(self.b.impl, C.byref(self.args), self.embd_dev, self.vocab_out,
+                                             prompt.ctypes.data, len(prompt), max_tokens, C.byref(opts),
+                                             out.ctypes.data, C.byref(st))
+        if rc < 0:
+            raise RuntimeError(f"hymt2_hip_generate_ids failed ({rc}): {self.b.last_error()}")
+        return out[:rc].copy(), st
 
     def gen_begin(self, prompt, n_total: int):
         if self.embd_dev is None:

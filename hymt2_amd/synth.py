@@ -414,6 +414,32 @@ def baseline_model(cfg: dict, ctx: int) -> dict:
     return model
 
 
+# A small "words"-vocabulary model whose greedy runs end at EOS (id 2): the tied embedding's EOS
+# row is scaled by 2.5 so that it wins the argmax after some steps (13 ids on the first prompt of
+# GEN_IDS_CALLS). It pins the stop rule and the prefix-KV reuse of the reference's greedy loop
+# (gen_ids, src/model.c:914-958). Each call is (user word ids, max_tokens); the calls run in
+# order on one model, so each sees the cache the one before it left: the second prompt shares
+# its first 12 words with the first, the third repeats the second, the fourth is capped at 5 ids.
+GEN_IDS_SHAPE = ModelShape(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=2, hdim=128, vocab=1000, ctx=256)
+
+
+def gen_ids_model() -> dict:
+    model = make_model(GEN_IDS_SHAPE, mode="stq", seed=211)
+    e = model["embd"].data.view(np.float16)
+    e[2] = (e[2].astype(np.float32) * 2.5).astype(np.float16)
+    model["vocab_style"] = "words"
+    return model
+
+
+def gen_ids_calls():
+    from . import gguf
+    v = GEN_IDS_SHAPE.vocab
+    w1 = rng(212).integers(gguf.FIRST_WORD, v, size=20)
+    w2 = np.concatenate([w1[:12], rng(213).integers(gguf.FIRST_WORD, v, size=6)])
+    w3 = rng(214).integers(gguf.FIRST_WORD, v, size=10)
+    return [(w1, 64), (w2, 64), (w2, 64), (w3, 5)]
+
+
 def baseline_prompt(cfg: dict, vocab: int = HYMT2_1_8B.vocab):
     """(ids, user text) of the config's prompt: n_prompt ids whose chat-templated text the
     reference encodes to exactly these ids."""

@@ -158,7 +158,8 @@ HYMT2_HIP_API int hymt2_hip_selftest_sqsum(void *impl, const float *x_dev, int n
  * position through the fused forward and the LM head; the argmax (first index on ties over
  * the first vocab_out rows, src/model.c:945-948) becomes the next step's token, whose
  * embedding row the device gathers itself. While the prompt lasts, its next id is used
- * instead. Stop tokens are not checked. `shape` is a hy_fused_args carrying layers, outw,
+ * instead. These entry points run a fixed number of steps from position 0 (stop ids and prefix
+ * reuse: hymt2_hip_generate_ids below). `shape` is a hy_fused_args carrying layers, outw,
  * norms and RoPE tables (prepared on first use); `embd` is the uploaded F16/F32 token
  * embedding (the tied head weight is allowed).
  *   gen_begin: uploads the prompt, resets position/argmax state, embeds prompt[0]; n_total is
@@ -179,6 +180,7 @@ typedef struct hymt2_gen_stats {
     double prefill_ms;  /* steps that consume prompt ids */
     double decode_ms;   /* steps that consume generated ids */
     int prefill_steps, decode_steps;
+    int cached_tokens;  /* prompt positions whose K/V was reused (hymt2_hip_generate_ids) */
 } hymt2_gen_stats;
 HYMT2_HIP_API int hymt2_hip_gen_begin(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
                                       const int *prompt, int n_prompt, int n_total);
@@ -191,6 +193,33 @@ HYMT2_HIP_API int hymt2_hip_generate(void *impl, const hymt2_fused_args *shape, 
 HYMT2_HIP_API int hymt2_hip_generate_chunked(void *impl, const hymt2_fused_args *shape, hy_dweight *embd,
                                              int vocab_out, const int *prompt, int n_prompt, int n_gen, int chunk,
                                              int *out_ids, hymt2_gen_stats *stats);
+
+/* The reference's greedy loop gen_ids (src/model.c:914-958) from the prompt ids on, on the
+ * device (the chat template and the tokenizer stay with the host; src/model.c:915-923):
+ *   - max_tokens is capped at ctx - n_prompt (src/model.c:925-926; nothing left: error);
+ *   - with reuse_prefix, the K/V of the longest common prefix of the prompt and the sequence the
+ *     previous hymt2_hip_generate_ids call left in the cache is kept, at most n_prompt - 1
+ *     positions (src/model.c:930-936); only the same weights, norms, RoPE tables and eps reuse
+ *     it, and any fused_forward or other device loop in between drops it;
+ *   - the rest of the prompt runs in chunks of `chunk` positions (1: single-token steps);
+ *   - then greedy ids (first index on ties) until one of stop_ids comes up, which ends the loop
+ *     and is not returned (tok_is_stop, src/tokenizer.c:179: the model's eos and eog), or
+ *     max_tokens ids. The device checks the ids itself; the host keeps at most two launches of
+ *     8 steps in flight and stops launching after a stop (those steps' K/V lies past the end of
+ *     the sequence and their ids are not read).
+ * Returns the number of ids written to out_ids (>= 0), negative on errors (hymt2_hip_last_error).
+ * stats (optional): prefill_steps = positions computed for the prompt, decode_steps = steps
+ * run after it, cached_tokens = positions reused. No counterpart in the reference interface:
+ * its loop calls fused_forward once per token and reads the logits back. */
+typedef struct hymt2_gen_opts {
+    const int *stop_ids; /* ids that end the loop (eos, eog); up to 8 */
+    int n_stop;
+    int chunk;           /* prompt positions per forward, 1 .. 128 (0: 1) */
+    int reuse_prefix;    /* nonzero: reuse the K/V prefix as the reference's loop does */
+} hymt2_gen_opts;
+HYMT2_HIP_API int hymt2_hip_generate_ids(void *impl, const hymt2_fused_args *shape, hy_dweight *embd, int vocab_out,
+                                         const int *prompt, int n_prompt, int max_tokens,
+                                         const hymt2_gen_opts *opts, int *out_ids, hymt2_gen_stats *stats);
 
 /* Single-token attention form by position (no counterpart in the reference interface): a forward
  * at position >= from (fused_forward with nt == 1, and the device loop's steps) runs the split

@@ -483,6 +483,8 @@ struct oc_state {
     float *h, *xn, *q, *k, *v, *ao, *gate, *up, *tmp, *scores;
     oc_q8k *xq_h, *xq_q, *xq_f;
     int cap_nt;
+    int *cache_tok; /* [ctx] ids whose K/V the cache holds (oc_gen_ids), n_cache of them */
+    int n_cache;
 };
 
 static int g_threads = 0;
@@ -525,7 +527,7 @@ void oc_state_free(oc_state *s) {
     if (!s) return;
     free(s->kc); free(s->vc); free(s->h); free(s->xn); free(s->q); free(s->k); free(s->v);
     free(s->ao); free(s->gate); free(s->up); free(s->tmp); free(s->scores);
-    free(s->xq_h); free(s->xq_q); free(s->xq_f);
+    free(s->xq_h); free(s->xq_q); free(s->xq_f); free(s->cache_tok);
     free(s);
 }
 
@@ -679,4 +681,54 @@ int oc_generate(oc_state *s, const int *prompt, int n_prompt, int n_gen, int bat
     }
     free(logits);
     return n_gen;
+}
+
+
+/* The reference's greedy loop gen_ids (src/model.c:914-958) from the prompt ids on (the chat
+ * template and the tokenizer are outside the path): max_tokens capped at ctx - n (:925-926);
+ * the K/V of the longest common prefix with the ids the cache holds is kept, at most n - 1
+ * positions (:930-936); the rest of the prompt runs in chunks of `batch` (forward_tokens,
+ * :904-909); then per step the first-index argmax (:945-948), a stop id ends the loop before it
+ * is emitted (:949, tok_is_stop: src/tokenizer.c:179), and every emitted id but the last of a
+ * full run is fed back (:950-953). Returns the number of ids written to out (-2: the prompt
+ * leaves no room, -1: a bad id); *keep_out = the positions reused. */
+int oc_gen_ids(oc_state *s, const int *prompt, int n, int max_tokens, int batch, const int *stop, int n_stop,
+               int *out, int *keep_out) {
+    const int ctx = s->m.ctx;
+    if (n < 1) return -1;
+    if (n + max_tokens > ctx) max_tokens = ctx - n;
+    if (max_tokens <= 0) return -2;
+    if (!s->cache_tok) s->cache_tok = (int *)calloc((size_t)ctx, sizeof(int));
+    if (batch < 1) batch = 1;
+    if (batch > s->cap_nt) batch = s->cap_nt;
+    int keep = 0;
+    while (keep < s->n_cache && keep < n - 1 && s->cache_tok[keep] == prompt[keep]) keep++;
+    s->n_cache = keep;
+    float *logits = (float *)malloc(sizeof(float) * (size_t)s->m.outw.n);
+    for (int i = keep; i < n; i += batch) {
+        const int nt = n - i < batch ? n - i : batch;
+        if (oc_forward(s, prompt + i, nt, i, i + nt == n, logits)) {
+            free(logits);
+            return -1;
+        }
+    }
+    memcpy(s->cache_tok + keep, prompt + keep, sizeof(int) * (size_t)(n - keep));
+    s->n_cache = n;
+    int ng = 0;
+    for (int i = 0; i < max_tokens; i++) {
+        const int best = oc_argmax(logits, s->m.vocab_out);
+        int is_stop = 0;
+        for (int j = 0; j < n_stop; j++) is_stop |= best == stop[j];
+        if (is_stop) break;
+        out[ng++] = best;
+        if (i + 1 == max_tokens) break;
+        if (oc_forward(s, &best, 1, s->n_cache, 1, logits)) {
+            free(logits);
+            return -1;
+        }
+        s->cache_tok[s->n_cache++] = best;
+    }
+    free(logits);
+    if (keep_out) *keep_out = keep;
+    return ng;
 }

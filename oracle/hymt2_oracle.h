@@ -103,6 +103,10 @@ int oc_argmax(const float *logits, int n);
 void oc_rmsnorm(const float *x, const float *w, float *y, int dim, float eps);
 /* greedy loop: prompt ids -> n_gen ids written to out; stop ids ignored. Returns n_gen. */
 int oc_generate(oc_state *s, const int *prompt, int n_prompt, int n_gen, int batch, int *out);
+/* gen_ids (src/model.c:914-958) from the prompt ids: prefix reuse against the ids this state's
+ * cache holds, chunked prompt, greedy ids up to a stop id. Returns the ids written to out. */
+int oc_gen_ids(oc_state *s, const int *prompt, int n, int max_tokens, int batch, const int *stop, int n_stop,
+               int *out, int *keep_out);
 void oc_set_threads(int n);
 
 #ifdef __cplusplus

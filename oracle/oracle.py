@@ -57,6 +57,7 @@ def lib():
             "oc_state_new": (vp, [C.POINTER(OcModel)]), "oc_state_free": (None, [vp]),
             "oc_forward": (i, [vp, vp, i, i, i, vp]), "oc_state_hidden": (vp, [vp]),
             "oc_argmax": (i, [vp, i]), "oc_generate": (i, [vp, vp, i, i, i, vp]),
+            "oc_gen_ids": (i, [vp, vp, i, i, i, vp, i, vp, C.POINTER(i)]),
             "oc_set_threads": (None, [i]), "oc_rmsnorm": (None, [vp, vp, vp, i, f]), "oc_expf_n": (None, [vp, vp, i]),
         }
         for name, (res, args) in sig.items():
@@ -190,3 +191,16 @@ class OracleModel:
         if lib().oc_generate(self.state, prompt.ctypes.data, len(prompt), n_gen, batch, out.ctypes.data) < 0:
             raise ValueError("oc_generate: prompt + generated ids exceed ctx, or an id is out of range")
         return out
+
+    def gen_ids(self, prompt, max_tokens: int, stop_ids=(), batch: int = 16):
+        """gen_ids (src/model.c:914-958) from the prompt ids: (ids before a stop id, positions of
+        the prompt whose K/V this state's cache kept from the previous gen_ids call)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        stop = np.ascontiguousarray(stop_ids, dtype=np.int32)
+        out = np.zeros(max(max_tokens, 1), dtype=np.int32)
+        keep = C.c_int(0)
+        n = lib().oc_gen_ids(self.state, prompt.ctypes.data, len(prompt), max_tokens, batch,
+                             stop.ctypes.data if len(stop) else None, len(stop), out.ctypes.data, C.byref(keep))
+        if n < 0:
+            raise ValueError(f"oc_gen_ids: {n}")
+        return out[:n].copy(), keep.value

@@ -13,6 +13,11 @@ scalar ISA (the bit-exact contract of the HIP backend):
 * bf16.npz        dot_bf16 / axpy_bf16 (src/kernels.c:1111-1124) and f32_to_bf16 (:107-111)
 * model_<m>.npz   whole-model logits (hymt2_debug_logits) and 8 greedy ids of a tiny
                   synthetic model loaded from a GGUF by the reference host (src/model.c)
+* gen_ids.npz     (with --gen-ids) the reference's greedy loop gen_ids (src/model.c:914-958) on
+                  hymt2_amd.synth.gen_ids_model(), whose greedy runs end at EOS: the calls of
+                  synth.gen_ids_calls() in order on one model, so each reuses the K/V prefix the
+                  one before it left. Per call: the prompt ids, the returned ids (before the stop
+                  id) and hymt2_model_stats's cached and prefilled token counts.
 * baseline_config3.npz / baseline_config4.npz (with --baseline): the BASELINE decode
                   workloads on the Hy-MT2-1.8B-shaped models (hymt2_amd.synth.CONFIG3 / CONFIG4).
                   The reference's own greedy loop (gen_ids, src/model.c:914-958, through
@@ -26,7 +31,7 @@ scalar ISA (the bit-exact contract of the HIP backend):
 
 Inputs are stored in the fixtures (or, for the models, regenerated from a seed and checked
 against a stored digest). Run from the repository root: python tests/golden/make_golden.py
-[--baseline [config3|config4]]
+[--baseline [config3|config4]] [--gen-ids]
 """
 import hashlib
 import os
@@ -131,7 +136,35 @@ def baseline_fixtures(which=("config3", "config4")):
         baseline_fixture("config4", synth.CONFIG4, synth.CONFIG4["n_gen"], last_logits=True)
 
 
+def gen_ids_fixture(threads: int = 4):
+    os.environ.update(HYMT2_DEVICE="cpu", HYMT2_ISA="scalar", HYMT2_REPACK="1", HYMT2_PREFAULT="0")
+    model = synth.gen_ids_model()
+    rec = dict(digest=synth.model_digest(model))
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "gen_ids.gguf")
+        gguf.write_model(path, model)
+        R.set_isa("scalar")
+        rm = R.RefModel(path, threads=threads, ctx=synth.GEN_IDS_SHAPE.ctx)
+        for i, (words, max_tokens) in enumerate(synth.gen_ids_calls()):
+            text = gguf.chat_text(words)
+            prompt = np.array(gguf.chat_ids(words), dtype=np.int32)
+            assert np.array_equal(rm.encode_chat(text), prompt), "chat text does not encode to the prompt ids"
+            ids, st = rm.generate_text(text, max_tokens)
+            rec[f"prompt{i}"] = prompt
+            rec[f"max{i}"] = np.int32(max_tokens)
+            rec[f"ids{i}"] = ids.astype(np.int32)
+            rec[f"cached{i}"] = np.int32(st["cached_tokens"])
+            rec[f"prefill{i}"] = np.int32(st["prefill_tokens"])
+            print(f"call {i}: {len(prompt)} prompt ids, {st['cached_tokens']} cached, {len(ids)} ids: {ids.tolist()}",
+                  flush=True)
+        rm.close()
+    np.savez(os.path.join(OUT, "gen_ids.npz"), **rec)
+
+
 def main():
+    if "--gen-ids" in sys.argv:
+        gen_ids_fixture()
+        return
     if "--baseline" in sys.argv:
         rest = [a for a in sys.argv[sys.argv.index("--baseline") + 1:] if not a.startswith("-")]
         baseline_fixtures(tuple(rest) or ("config3", "config4"))

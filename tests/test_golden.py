@@ -106,3 +106,21 @@ def test_baseline_config3_oracle():
     assert hashlib.sha256(bits(logits).tobytes()).hexdigest() == str(f["prompt_logits_sha256"])
     ids = O.OracleModel(model, threads=8).generate(prompt, 4, batch=8)
     assert np.array_equal(ids, f["greedy"][:4])
+
+
+def test_gen_ids_golden():
+    """The oracle's gen_ids (src/model.c:914-958 from the prompt ids on) against the reference's
+    own loop on the EOS-ending model: the calls in order on one state, each reusing the cache the
+    one before it left; ids before the stop id and the reused prefix length, call by call. A
+    mutant that feeds or emits the stop id, drops the n - 1 bound on the reuse, or feeds the last
+    id of a full run fails one of the calls (13 ids then EOS; 14 positions reused; n - 1 reused;
+    a run capped at 5)."""
+    f = load("gen_ids")
+    model = synth.gen_ids_model()
+    assert synth.model_digest(model) == str(f["digest"])
+    om = O.OracleModel(model, threads=8)
+    for i in range(len(synth.gen_ids_calls())):
+        ids, keep = om.gen_ids(f[f"prompt{i}"], int(f[f"max{i}"]), stop_ids=[2])
+        assert np.array_equal(ids, f[f"ids{i}"]), f"call {i}"
+        assert keep == int(f[f"cached{i}"]), f"call {i}: reused {keep}, the reference {int(f[f'cached{i}'])}"
+        assert len(f[f"prompt{i}"]) - keep == int(f[f"prefill{i}"])
