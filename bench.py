@@ -12,12 +12,16 @@ CONFIG3). The greedy ids are checked against the reference's own greedy loop on 
 The cpu_baseline leg times the reference library itself (oracle/_ref/libhymt2_ref.so, built
 from the reference's sources) on the host with HYMT2_DEVICE=cpu, HYMT2_REPACK=1, the ISA it
 auto-detects and HYMT2_THREADS = the host's physical cores, on the same workload: the chat
-text that encodes to the same 64 prompt ids, then 128 greedy decode tokens.
+text that encodes to the same 64 prompt ids, then 128 greedy decode tokens. The same leg runs
+the reference's unchanged host with this backend linked in place of its CUDA one
+(oracle/_ref/libhymt2_host.so, HYMT2_DEVICE=cuda) in a child process, fused (host_dropin) and
+per-op (HYMT2_FUSED=0, per_op), and reports the host's own decode rate (hymt2_model_stats).
 """
 import argparse
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import tempfile
 import time
@@ -483,7 +487,64 @@ def kernels_only(args):
     b.close()
 
 
-def cpu_baseline(model, prompt, text, gpu_ids, n_tokens: int):
+def host_leg_child(path: str, ctx: int, fused: bool, n_tokens: int, text: str):
+    """In a fresh process: the reference's unchanged host (oracle/_ref/libhymt2_host.so, its
+    sources linked with libhymt2_hip.a in place of src/cuda.c) on the GGUF with
+    HYMT2_DEVICE=cuda, fused or per-op (HYMT2_FUSED=0), the ISA it detects; its own greedy loop
+    gen_ids (src/model.c:914-958) on the chat text, as the CPU baseline runs it. Prints one JSON
+    line: the model info, the ids and hymt2_model_stats."""
+    from oracle import refbind
+    os.environ.update(HYMT2_DEVICE="cuda", HYMT2_REPACK="1")
+    os.environ.pop("HYMT2_ISA", None)
+    if not fused:
+        os.environ["HYMT2_FUSED"] = "0"
+    L = refbind.load(refbind.HOST_LIB)
+    isa = L.hymt2_isa().decode()
+    threads = int(os.environ["HYMT2_THREADS"])  # the parent's choice (the host's physical cores)
+    rm = refbind.RefModel(path, threads=threads, ctx=ctx, path=refbind.HOST_LIB)
+    info = rm.info()
+    rm.generate_text(text, 4)  # warm: graphs captured, page faults (the prompt KV is then reused)
+    rm.logits([0])             # reset the prefix cache so the timed run prefills the whole prompt
+    t0 = time.perf_counter()
+    ids, st = rm.generate_text(text, n_tokens)
+    wall = time.perf_counter() - t0
+    rm.close()
+    print(json.dumps(dict(info=info, isa=isa, threads=threads, ids=[int(i) for i in ids], stats=st, wall=wall)),
+          flush=True)
+
+
+def host_legs(path: str, ctx: int, prompt, text: str, gpu_ids, n_fused: int = 128, n_per_op: int = 32):
+    """The reference host over this backend (host_leg_child), fused and per-op. The fused leg's
+    ids must equal the device loop's (its numbers all come from the device; the host only takes
+    the argmax); the per-op leg runs norms, RoPE, attention and the F16 head on the host at its
+    ISA, so its ids follow that ISA's fp32 order (counted, not required)."""
+    out = {}
+    for name, fused, n in (("host_dropin", True, n_fused), ("per_op", False, n_per_op)):
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--host-leg", path, str(ctx),
+                            "1" if fused else "0", str(n), text], capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError(f"{name} leg failed: {r.stdout[-2000:]} {r.stderr[-2000:]}")
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        st, ids = d["stats"], np.array(d["ids"], dtype=np.int32)
+        if st["decode_tokens"] != n or st["prefill_tokens"] != len(prompt) or st["decode_ms"] <= 0:
+            raise RuntimeError(f"{name} leg: {st}, expected a {len(prompt)}-token prompt and {n} tokens")
+        m = min(len(ids), len(gpu_ids))
+        agree = int(np.argmin(np.append(ids[:m] == gpu_ids[:m], False)))
+        if fused and (agree != m or "gpu=hip+fused" not in d["info"]):
+            raise RuntimeError(f"host_dropin leg: {d['info']}; ids agree with the device loop for {agree} of {m}")
+        out[name] = dict(value=round(st["decode_tokens"] / (st["decode_ms"] / 1000.0), 2), unit="tok/s",
+                         ms_per_token=round(st["decode_ms"] / st["decode_tokens"], 4),
+                         prefill_tok_s=round(st["prefill_tokens"] / (st["prefill_ms"] / 1000.0), 1),
+                         tokens=n, info=d["info"], isa=d["isa"], threads=d["threads"],
+                         ids_agree_with_device_loop=f"{agree} of {m}",
+                         note=("the reference's gen_ids with this backend linked in (HYMT2_DEVICE=cuda): "
+                               + ("fused_forward per token, logits D2H, host argmax" if fused else
+                                  "HYMT2_FUSED=0: the layer matvecs per op on the GPU (weight_out outputs), "
+                                  "norms, RoPE, attention and the F16 head on the host")))
+    return out
+
+
+def cpu_baseline(model, prompt, text, gpu_ids, n_tokens: int, host: bool = True):
     """The reference's own greedy loop (gen_ids, src/model.c:914-958, compiled from the
     reference's sources into oracle/_ref/libhymt2_ref.so) on the host cores, on the same weights
     and the same 64 prompt ids: the chat text it is given encodes to exactly the GPU leg's prompt
@@ -515,6 +576,7 @@ def cpu_baseline(model, prompt, text, gpu_ids, n_tokens: int):
         wall = time.perf_counter() - t0
         info = rm.info()
         rm.close()
+        legs = host_legs(path, ctx, prompt, text, gpu_ids) if host else {}
     if len(ids) != n_tokens or st["decode_tokens"] != n_tokens or st["decode_ms"] <= 0 or st["prefill_tokens"] != len(prompt):
         raise RuntimeError(f"cpu baseline: reference decoded {len(ids)} tokens ({st}), expected a "
                            f"{len(prompt)}-token prompt and {n_tokens} tokens")
@@ -527,7 +589,36 @@ def cpu_baseline(model, prompt, text, gpu_ids, n_tokens: int):
                        f"{wall:.1f} s wall",
                 prefill_tok_s=round(st["prefill_tokens"] / (st["prefill_ms"] / 1000.0), 2),
                 ids_agree_with_gpu=f"{agree} of {n} leading ids (the auto ISA's fp32 order differs from the "
-                                   f"scalar order the GPU matches)")
+                                   f"scalar order the GPU matches)"), legs
+
+
+def boundary_costs(vocab: int, hidden: int, reps: int = 200):
+    """Per-token pieces the reference host's loop adds to the device step (src/cuda.c:339-421 and
+    src/model.c:945-948 for the reference's own backend): the input block H2D (the host's
+    embedding row, the position and its RoPE row: 16 KB from pinned staging), the logits D2H into
+    the host's pageable buffer (vocab floats), and an argmax over them (numpy's; the reference's is
+    a scalar loop). Each timed alone with a synchronisation, as the loop runs them."""
+    import torch
+    dev = torch.empty(vocab, dtype=torch.float32, device="cuda")
+    pageable = torch.empty(vocab, dtype=torch.float32)
+    hin = torch.empty(4096, dtype=torch.float32, pin_memory=True)
+    din = torch.empty(4096, dtype=torch.float32, device="cuda")
+    lg = np.random.default_rng(0).standard_normal(vocab).astype(np.float32)
+
+    def per_call_us(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return round((time.perf_counter() - t0) / reps * 1e6, 1)
+
+    def h2d():
+        din.copy_(hin, non_blocking=True)
+        torch.cuda.synchronize()
+
+    return dict(input_h2d_us=per_call_us(h2d), logits_d2h_us=per_call_us(lambda: pageable.copy_(dev)),
+                host_argmax_us=per_call_us(lambda: np.argmax(lg)), hidden=hidden, vocab=vocab)
 
 
 def main():
@@ -545,9 +636,16 @@ def main():
                     help="only the standalone kernel launches used for rocprofv3 counter passes")
     ap.add_argument("--no-q6k", action="store_true", help="skip the Q6_K-head model leg")
     ap.add_argument("--q6k-only", action="store_true", help="only the Q6_K-head model leg (for profiling)")
+    ap.add_argument("--host-leg", nargs=5, metavar=("GGUF", "CTX", "FUSED", "TOKENS", "TEXT"),
+                    help=argparse.SUPPRESS)  # child process of the cpu_baseline leg's host legs
+    ap.add_argument("--no-host-legs", action="store_true", help="skip the reference-host legs (host_dropin, per_op)")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print the kernel table of a rocprofv3 --kernel-trace output directory and exit")
     args = ap.parse_args()
+    if args.host_leg:
+        g, ctx, fused, n, text = args.host_leg
+        host_leg_child(g, int(ctx), fused == "1", int(n), text)
+        return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return
@@ -618,11 +716,19 @@ def main():
         c4 = config4(b)
         c4["gemm_roofline"] = gemm_roofline(b)
         log(f"config 4: {c4}")
-    cpu = None
+    costs = boundary_costs(shape.vocab, shape.hidden)
+    log(f"boundary pieces per token: {costs}")
+    cpu, legs = None, {}
     if not args.no_cpu:
         t = time.time()
-        cpu = cpu_baseline(model, prompt, text, ids, args.cpu_tokens)
+        cpu, legs = cpu_baseline(model, prompt, text, ids, args.cpu_tokens, host=not args.no_host_legs)
         log(f"cpu baseline in {time.time() - t:.1f} s: {cpu}")
+        for k, v in legs.items():
+            log(f"{k}: {v}")
+    if "host_dropin" in legs:
+        hd = legs["host_dropin"]
+        hd["over_device_loop_us_per_token"] = round((hd["ms_per_token"] - dt / args.steps * 1e3) * 1e3, 1)
+        hd["pieces"] = costs
     avg_pos = len(prompt) + args.warmup + (args.steps - 1) / 2.0
     kv_read = 2 * shape.n_layer * shape.kvdim * 2 * (avg_pos + 1)
     token_bytes = wb["layers"] + wb["head"] + kv_read
@@ -641,6 +747,8 @@ def main():
         "roofline": roof,
         "head_roofline": head,
         "host_loop": host,
+        "host_dropin": legs.get("host_dropin"),
+        "per_op": legs.get("per_op"),
         "layer_sets": sets,
         "q6k_head_model": q6,
         "config4_prefill": c4,

@@ -20,9 +20,11 @@ pytestmark = pytest.mark.gpu
 RUNNER = os.path.join(ROOT, "tests", "helpers", "dropin_run.py")
 
 
-def run_leg(env_extra, path, ctx, out, prompt, text, max_tokens):
+def run_leg(env_extra, path, ctx, out, prompt, text, max_tokens, unset=()):
     env = dict(os.environ, HYMT2_ISA="scalar", HYMT2_REPACK="1", HYMT2_PREFAULT="0", HYMT2_THREADS="4",
                HYMT2_VERBOSE="1", **env_extra)
+    for k in unset:
+        env.pop(k, None)
     r = subprocess.run([sys.executable, RUNNER, path, str(ctx), out, ",".join(str(int(t)) for t in prompt), text,
                         str(max_tokens)], capture_output=True, text=True, env=env, timeout=300)
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
@@ -68,6 +70,30 @@ def test_reference_host_per_op_path(tmp_path, mode):
     cpu, _ = run_leg({"HYMT2_DEVICE": "cpu-ref"}, path, shape.ctx, str(tmp_path / "cpu.npz"), prompt, text, 12)
     info = str(gpu["info"])
     assert "gpu=hip" in info and "+fused" not in info, info + log[-2000:]
+    for key in ("logits", "stepwise"):
+        assert np.array_equal(gpu[key].view(np.uint32), cpu[key].view(np.uint32)), key
+    assert len(cpu["ids"]) > 0 and np.array_equal(gpu["ids"], cpu["ids"])
+
+
+def test_reference_host_auto_selects_hip(tmp_path):
+    """HYMT2_DEVICE unset (auto): the host tries cuda first (src/device.c:112, src/model.c:457),
+    uploads every weight, times a CPU step against a fused step and keeps the fused path only
+    when it is at least 10% faster (src/model.c:338-373). On two 1.8B-shaped layers the backend
+    wins its calibration against the host cores: the host reports gpu=hip+fused, and its logits,
+    stepwise logits and greedy ids equal the same host's on the CPU."""
+    if not (refbind.available(refbind.HOST_LIB) and refbind.available(refbind.REF_LIB)):
+        pytest.skip("oracle/_ref host libraries not built (needs the reference tree at build time)")
+    shape = synth.ModelShape(n_layer=2, vocab=4000, ctx=96)
+    model = synth.make_model(shape, mode="stq", seed=59)
+    path = str(tmp_path / "m_auto.gguf")
+    gguf.write_model(path, model)
+    prompt = synth.rand_prompt(synth.rng(60), 17, shape.vocab)
+    text = "t5 t17 t300 t42"
+    gpu, log = run_leg({}, path, shape.ctx, str(tmp_path / "gpu.npz"), prompt, text, 12,
+                       unset=("HYMT2_DEVICE", "HYMT2_VK", "HYMT2_FUSED"))
+    cpu, _ = run_leg({"HYMT2_DEVICE": "cpu-ref"}, path, shape.ctx, str(tmp_path / "cpu.npz"), prompt, text, 12)
+    assert "gpu=hip+fused" in str(gpu["info"]), str(gpu["info"]) + log[-2000:]
+    assert "auto -> hip+fused" in log, log[-2000:]
     for key in ("logits", "stepwise"):
         assert np.array_equal(gpu[key].view(np.uint32), cpu[key].view(np.uint32)), key
     assert len(cpu["ids"]) > 0 and np.array_equal(gpu["ids"], cpu["ids"])
