@@ -114,7 +114,8 @@ def ffn_in_roofline(model, b, copies: int = 64, passes: int = 3):
                        "one decode token (RMSNorm + Q8_K prologue, gate+up 2x6144x2048 STQ1_0 panel, SwiGLU)",
                 avg_us=round(avg_s * 1e6, 2), bytes_per_launch=algo,
                 timing=f"HIP events on the backend stream over {copies * passes} launches rotating {copies} "
-                       f"weight copies")
+                       f"weight copies",
+                in_graph=_in_graph_figure(algo))
 
 
 def head_roofline(fm, b, reps: int = 20):
@@ -385,18 +386,31 @@ def summarize_trace(d: str):
     print("|---|---:|---:|---:|---:|---:|")
     for k, v in sorted(dur.items(), key=lambda kv: -sum(kv[1]))[:24]:
         print(f"| `{k[:96]}` | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | {100 * sum(v) / tot:.2f} |")
-    tgt = "k_mv1<0, 1, 8, 1>"
-    alone, graph = [], []
-    for i, r in enumerate(rows):
-        if tgt not in r["Kernel_Name"]:
-            continue
-        t = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
-        (alone if i and tgt in rows[i - 1]["Kernel_Name"] else graph).append(t)
-    if alone:
+    # the FFN-input kernel is the RMSNorm-prologue decode matvec (k_mv1<0, 1, ITERS, 1>) that the
+    # roofline leg launches back to back; the qkv matvec shares the form with other ITERS
+    import re
+    norm_mv = [k for k in dur if re.search(r"k_mv1<0, 1, \d+, 1>", k)]
+    b2b = {k: sum(1 for i, r in enumerate(rows) if i and r["Kernel_Name"] == k and rows[i - 1]["Kernel_Name"] == k)
+           for k in norm_mv}
+    tgt = max(b2b, key=b2b.get) if b2b and max(b2b.values()) > 0 else None
+    summary = {"kernel_avg_us": {k[:120]: round(sum(v) / len(v), 3) for k, v in dur.items() if "hy::" in k}}
+    if tgt is None:
+        print()
+        print("warning: no back-to-back dispatches of an RMSNorm-prologue decode matvec (the roofline leg's "
+              "FFN-input kernel) in this trace")
+    else:
+        alone, graph = [], []
+        for i, r in enumerate(rows):
+            if r["Kernel_Name"] != tgt:
+                continue
+            t = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+            (alone if i and rows[i - 1]["Kernel_Name"] == tgt else graph).append(t)
         print()
         print(f"`{tgt}`: {len(alone)} back-to-back dispatches (the roofline leg, hymt2_hip_ffn_in) average "
               f"{sum(alone) / len(alone):.2f} us; {len(graph)} dispatches inside the decode graphs average "
-              f"{sum(graph) / len(graph):.2f} us.")
+              f"{sum(graph) / max(len(graph), 1):.2f} us.")
+        summary["ffn_in"] = dict(kernel=tgt, standalone_avg_us=round(sum(alone) / len(alone), 3),
+                                 in_graph_avg_us=round(sum(graph) / max(len(graph), 1), 3), in_graph_dispatches=len(graph))
     # the longest run of pipelined-prefill dispatches (job-table kernels, with the chunks'
     # embedding lookups before them): per kernel and per launch step
     def pipe(n):
@@ -437,6 +451,8 @@ def summarize_trace(d: str):
         if att:
             print()
             print("Chunk attention per launch step (us): " + " ".join(f"{x:.0f}" for x in att))
+    print()
+    print(json.dumps(summary))
 
 
 def host_loop_rate(fm, prompt, n_tokens: int):
@@ -455,6 +471,23 @@ def host_loop_rate(fm, prompt, n_tokens: int):
     dt = time.perf_counter() - t0
     return dict(value=round(n_tokens / dt, 2), unit="tok/s", tokens=n_tokens,
                 note="hy_device_ops.fused_forward per token with logits D2H and host argmax")
+
+
+def _in_graph_figure(algo: int):
+    """The FFN-input kernel's average duration inside the decode graphs, from the committed
+    kernel-trace summary of the decode bench (profiles/decode_config3_kernels.json, written by
+    --summarize-trace from a rocprofv3 run of this bench): HIP events time graph launches, not the
+    kernels inside them. None when the profile is missing."""
+    p = os.path.join(ROOT, "profiles", "decode_config3_kernels.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        d = json.load(f).get("ffn_in")
+    if not d:
+        return None
+    us = d["in_graph_avg_us"]
+    return dict(avg_us=us, achieved=round(algo / (us * 1e-6) / 1e9, 1), frac=round(algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                kernel=d["kernel"], dispatches=d["in_graph_dispatches"], source="profiles/decode_config3_kernels.json")
 
 
 def _pmc_traffic(kernel: str):
@@ -478,12 +511,92 @@ def kernels_only(args):
     b = lib.Backend()
     roof = ffn_in_roofline(model, b, copies=64, passes=1)
     log(f"ffn_in: {roof['avg_us']} us, {roof['achieved']} GB/s")
+    calibration_copy()
+    b.close()
+
+
+def calibration_copy():
+    """The counter runs' calibration kernel: torch.neg over 64 Mi fp32 (268,435,456 B read and
+    268,435,456 B written), whose FETCH_SIZE / WRITE_SIZE give the counters' scale."""
+    import torch
     src = torch.randn(64 << 20, device="cuda", dtype=torch.float32)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    torch.neg(src, out=dst)  # the calibration kernel: 256 MiB in, 256 MiB out
+    torch.neg(src, out=dst)
     torch.cuda.synchronize()
     log("calibration copy: torch.neg over 67108864 fp32 (268435456 B read, 268435456 B written)")
+
+
+def attn_traffic():
+    """Decode steps for the attention kernels' counter passes, then the calibration copy: the
+    config-3 model at positions 64-79 (k_attn1, one workgroup per head, short rows) and the
+    config-4 model at positions 1024-1039 after its 1024-token prompt (the split form:
+    k_attn_scores, k_attn_out)."""
+    from hymt2_amd import lib, synth
+    b = lib.Backend()
+    for cfg, chunk in ((synth.CONFIG3, 64), (synth.CONFIG4, 128)):
+        prompt, _ = synth.baseline_prompt(cfg)
+        model = synth.baseline_model(cfg, len(prompt) + 128)
+        fm = lib.FusedModel(b, model)
+        log(f"{len(prompt)}-token prompt: model uploaded")
+        fm.gen_begin(prompt, len(prompt) + 17)
+        fm.gen_prefill(chunk)
+        fm.gen_read(0, 1)
+        log("prompt done")
+        for _ in range(2):
+            fm.gen_steps(8)
+            fm.gen_read(0, 1)
+            log("8 decode steps done")
+        fm.close()
+        del model
+    calibration_copy()
+    b.close()
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str):
+    """HBM bytes per dispatch of every kernel in two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the calibration copy
+    (torch.neg of 268,435,456 B in and out). Prints a table and a JSON object."""
+    import csv
+
+    def load(d, counter):
+        rows = list(csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))))
+        acc = {}
+        for r in rows:
+            if r["Counter_Name"] != counter:
+                continue
+            a = acc.setdefault(r["Kernel_Name"], [0, 0.0])
+            a[0] += 1
+            a[1] += float(r["Counter_Value"])
+        cal = [v[1] / v[0] for k, v in acc.items() if "neg" in k.lower()]
+        if not cal:
+            raise RuntimeError(f"no calibration kernel in {d}")
+        scale = 268435456.0 / (max(cal) * 1024.0)
+        return {k: (v[0], v[1] / v[0] * 1024.0 * scale) for k, v in acc.items()}, scale
+
+    fetch, fs = load(fetch_dir, "FETCH_SIZE")
+    write, ws = load(write_dir, "WRITE_SIZE")
+    print(f"scale factors: FETCH_SIZE {fs:.4f}, WRITE_SIZE {ws:.4f}")
+    print()
+    print("| kernel | dispatches | fetch B / dispatch | write B / dispatch |")
+    print("|---|---:|---:|---:|")
+    out = {}
+    for k in sorted(fetch, key=lambda k: -fetch[k][1]):
+        if "neg" in k.lower():
+            continue
+        n, fb = fetch[k]
+        wb = write.get(k, (0, 0.0))[1]
+        out[k] = dict(dispatches=n, fetch_bytes=round(fb), write_bytes=round(wb))
+        print(f"| `{k[:90]}` | {n} | {fb:,.0f} | {wb:,.0f} |")
+    print()
+    print(json.dumps(dict(fetch_scale=round(fs, 4), write_scale=round(ws, 4), kernels=out)))
+
+
+def layer_sets_only():
+    """The configs 0-2 matvec legs alone (for a kernel trace of their launches)."""
+    from hymt2_amd import lib
+    b = lib.Backend()
+    print(json.dumps(layer_sets(b)), flush=True)
     b.close()
 
 
@@ -639,6 +752,11 @@ def main():
     ap.add_argument("--host-leg", nargs=5, metavar=("GGUF", "CTX", "FUSED", "TOKENS", "TEXT"),
                     help=argparse.SUPPRESS)  # child process of the cpu_baseline leg's host legs
     ap.add_argument("--no-host-legs", action="store_true", help="skip the reference-host legs (host_dropin, per_op)")
+    ap.add_argument("--attn-traffic", action="store_true",
+                    help="only decode steps of the config-3 and config-4 models and the calibration copy (counter runs)")
+    ap.add_argument("--layer-sets-only", action="store_true", help="only the configs 0-2 matvec legs (kernel trace)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print HBM bytes per dispatch from two rocprofv3 --pmc output directories and exit")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print the kernel table of a rocprofv3 --kernel-trace output directory and exit")
     args = ap.parse_args()
@@ -649,6 +767,9 @@ def main():
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the Hy-MT2 token loop at batch 1 runs on a single MI355X "
               "(multi-GPU figures are not part of this build); run with --gpus 1", file=sys.stderr)
@@ -658,6 +779,12 @@ def main():
 
     if args.kernels_only:
         kernels_only(args)
+        return
+    if args.attn_traffic:
+        attn_traffic()
+        return
+    if args.layer_sets_only:
+        layer_sets_only()
         return
     if args.q6k_only:
         b = lib.Backend()

@@ -327,6 +327,16 @@ __device__ __forceinline__ void a1_produce(uint2 (&v)[A1Split<HD>::IPT], float* 
     if (t0 < n) hy_lds_barrier();
 }
 
+// The query head of this k_attn1 workgroup. Workgroups go to the 8 XCDs round-robin (workgroup b
+// on XCD b % 8), each XCD with its own L2: consecutive heads share an XCD (heads 2x, 2x + 1 on XCD
+// x for 16 heads), so a KV head's K and V rows are fetched by half as many L2s as in id order
+// (measured 5.5x the algorithmic bytes in id order at 4 query heads per KV head). Head counts
+// that are not a multiple of 8 keep id order.
+__device__ __forceinline__ int a1_head(int heads) {
+    const int b = blockIdx.x;
+    return heads % 8 ? b : (b % 8) * (heads / 8) + b / 8;
+}
+
 // LDS of one head's attention.
 template <int HD>
 struct A1Smem {
@@ -365,7 +375,7 @@ __device__ __forceinline__ void a1_core(const Attn1Args& a, A1Smem<HD>& S, const
     float* red = S.red;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = blockIdx.x;
+    const int h = a1_head(a.heads);
     const int group = a.heads / a.kv_heads;
     const int g = h / group;
     const int half = a.rope_half;
@@ -548,7 +558,7 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
         hy_sgpr_pin(a.pos_dev), hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.pos0), hy_sgpr_pin(a.ao), hy_sgpr_pin(a.heads),
         hy_sgpr_pin(a.kv_heads), hy_sgpr_pin(a.rope_half), hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.eps);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = blockIdx.x;
+    const int h = a1_head(a.heads);
     const int g = h / (a.heads / a.kv_heads);
     const int half = a.rope_half;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
@@ -878,6 +888,24 @@ __device__ __forceinline__ void so_chain(const float* row, int d, int cnt, float
 
 }  // namespace
 
+// The (query head, dimension part) of this k_attn_out workgroup. Workgroups go to the 8 XCDs
+// round-robin (workgroup b on XCD b % 8), each XCD with its own L2: the ids are dealt so that the
+// workgroups reading the same V lines (a KV head's 64 dimensions of every row, 128 bytes: the
+// group's query heads times the four 16-dimension parts of the line) run on one XCD, which then
+// fetches those lines once (dealt in id order, the eight parts of a head on eight XCDs fetched
+// 4.9x the V and score bytes). Launches whose workgroup count is not a multiple of 8 keep id
+// order.
+template <int HD>
+__device__ __forceinline__ void so_assign(int heads, int group, int& h, int& part) {
+    constexpr int PARTS = HD / kSoDims, LPARTS = 64 / kSoDims, LINES = HD / 64;
+    const int b = blockIdx.x, total = heads * PARTS;
+    const int q = total % 8 ? b : (b % 8) * (total / 8) + b / 8;
+    const int gs = group * LPARTS;  // workgroups of one (KV head, line)
+    const int grp = q / gs, mem = q % gs;
+    h = (grp / LINES) * group + mem / LPARTS;
+    part = (grp % LINES) * LPARTS + mem % LPARTS;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
     constexpr int PARTS = HD / kSoDims;
@@ -886,7 +914,8 @@ __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
         hy_sgpr_pin(a.kv_heads), hy_sgpr_pin(a.ctx), hy_sgpr_pin(a.sc), hy_sgpr_pin(a.segmax),
         hy_sgpr_pin(a.sc_stride), hy_sgpr_pin(a.seg_stride);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = blockIdx.x / PARTS, part = blockIdx.x % PARTS;
+    int h, part;
+    so_assign<HD>(a.heads, a.heads / a.kv_heads, h, part);
     const int g = h / (a.heads / a.kv_heads);
     const uint16_t* V = a.vc + (size_t)g * a.ctx * HD + kSoDims * part;
     const bool prd = wave >= 1 && wave != 4;        // producer wavefronts
