@@ -681,10 +681,12 @@ struct SoSmem {
 template <int HD>
 __global__ __launch_bounds__(kSpThreads) void k_attn_scores(Attn1Args a) {
     constexpr int RPL = HD / 64;
-    constexpr int HW = kSpThreads / 128;  // wavefronts per half of the workgroup (head slots)
-    __shared__ alignas(16) float qn[kSplitMaxGroup][HD];
-    __shared__ alignas(16) float scr[kSpThreads / 64][HD];
-    __shared__ alignas(16) uint16_t kb[HD];
+    constexpr int HW = kSpThreads / 128;               // wavefronts per half of the workgroup (head slots)
+    constexpr int QPW = kSplitMaxGroup / HW;           // query heads per wavefront at most
+    constexpr int NW = kSpThreads / 64;
+    __shared__ alignas(16) float qn[NW][QPW][HD];      // each wavefront's own normalized q rows
+    __shared__ alignas(16) float scr[NW][HD];
+    __shared__ alignas(16) uint16_t kb[NW][HD];        // this token's bf16 k, in each wavefront that scores it
     hy_sgpr_pin(a.q), hy_sgpr_pin(a.k), hy_sgpr_pin(a.v), hy_sgpr_pin(a.kc), hy_sgpr_pin(a.vc),
         hy_sgpr_pin(a.q_norm), hy_sgpr_pin(a.k_norm), hy_sgpr_pin(a.rope_cos), hy_sgpr_pin(a.rope_sin),
         hy_sgpr_pin(a.pos_dev), hy_sgpr_pin(a.rope_cur), hy_sgpr_pin(a.pos0), hy_sgpr_pin(a.heads),
@@ -695,28 +697,34 @@ __global__ __launch_bounds__(kSpThreads) void k_attn_scores(Attn1Args a) {
     const int half = a.rope_half;
     const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
     // wavefront w scores the group's q heads w % HW, w % HW + HW, ... for the half w / HW of the
-    // segment's positions, one key per pair of lanes; the first half's wavefronts RoPE and norm
-    // those heads' q rows, the last wavefront this token's k (in the position's workgroup)
+    // segment's positions, one key per pair of lanes. Nothing is shared between wavefronts:
+    // each RoPEs and norms its own q heads (the two halves' wavefronts of a head both do), and
+    // the wavefronts whose keys include the position RoPE and norm this token's k themselves,
+    // so the workgroup has no barrier (one cost 0.7 us waiting for the slowest row's arrival).
     const int slot = wave % HW, sh = wave / HW;
     const bool hasq = slot < group;
-    const bool qw = hasq && sh == 0;
-    const bool kw = wave == kSpThreads / 64 - 1;
     const int par = lane & 1;
 
-    // 0. q rows and norm weights, this token's k and v rows, then the position (scalar), its RoPE
-    //    row and the first segment's key rows
+    // 0. q row and norm weights, this token's k and v rows, the first segment's key rows (clamped
+    //    inside the cache: which of them lie below the position is known only after its read,
+    //    and the rows arrive about 2.5 us after issue), then the position (scalar) and its RoPE row
     float x[RPL], nw[RPL], kx[RPL], knw[RPL], vx[RPL];
 #pragma unroll
     for (int i = 0; i < RPL; i++) {
         const int d = lane + 64 * i;
-        if (qw) x[i] = a.q[(size_t)(g * group + slot) * HD + d], nw[i] = a.q_norm[d];
-        if (kw) kx[i] = a.k[(size_t)g * HD + d], knw[i] = a.k_norm[d], vx[i] = a.v[(size_t)g * HD + d];
+        if (hasq) x[i] = a.q[(size_t)(g * group + slot) * HD + d], nw[i] = a.q_norm[d];
+        kx[i] = a.k[(size_t)g * HD + d], knw[i] = a.k_norm[d], vx[i] = a.v[(size_t)g * HD + d];
     }
+    const int koff = sh * (kSplitSeg / 2) + (lane >> 1);  // this lane's key within a segment
+    uint4 kr[HD / 8];
+    if (hasq) a1_load_key<HD>(kr, K, min((int)blockIdx.x * kSplitSeg + koff, a.ctx - 1));
     __builtin_amdgcn_sched_barrier(0);
-    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    const int pos = a.pos_dev ? hy_sload_i32(a.pos_dev) : a.pos0;
     const int n = pos + 1, nseg = (n + kSplitSeg - 1) / kSplitSeg;
-    if ((int)blockIdx.x >= nseg) return;  // uniform: no work for this workgroup at this position
-    const bool own = (nseg - 1) % (int)gridDim.x == (int)blockIdx.x;  // it scores the segment holding pos
+    if ((int)blockIdx.x >= nseg || !hasq) return;  // uniform: no work for this workgroup / wavefront
+    // this wavefront scores the position's key: its workgroup has the last segment and its half
+    // of the segment holds the position
+    const bool kw = (nseg - 1) % (int)gridDim.x == (int)blockIdx.x && sh == (pos % kSplitSeg) / (kSplitSeg / 2);
     float rc[RPL], rs[RPL];
     {
         const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
@@ -729,54 +737,50 @@ __global__ __launch_bounds__(kSpThreads) void k_attn_scores(Attn1Args a) {
         }
     }
     a1_fence();
-    const int koff = sh * (kSplitSeg / 2) + (lane >> 1);  // this lane's key within a segment
-    uint4 kr[HD / 8];
-    {
-        const int r = blockIdx.x * kSplitSeg + koff;
-        if (hasq && r < pos) a1_load_key<HD>(kr, K, r);
-    }
-    a1_fence();
 
-    // 1. RoPE + RMSNorm (src/model.c:836-841): this token's k (bf16, stored at the position with
-    //    its v, src/model.c:842-847) and the group's q heads
-    if (own && kw) {
+    // 1. RoPE + RMSNorm (src/model.c:836-841) of the wavefront's q heads and, where it scores the
+    //    position, of this token's k (bf16; stored at the position with its v by the head slot 0
+    //    wavefront, src/model.c:842-847)
+    if (kw) {
         float y[RPL];
         rope_norm_wave<HD>(kx, scr[wave], rc, rs, half, knw, a.eps, lane, y);
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
             const int d = lane + 64 * i;
             const uint16_t kq = hy_to_bf16(y[i]);
-            kb[d] = kq;
-            const size_t off = ((size_t)g * a.ctx + pos) * HD + d;
-            a.kc[off] = kq;
-            a.vc[off] = hy_to_bf16(vx[i]);
-        }
-    }
-    if (qw) {
-        for (int hq = slot; hq < group; hq += HW) {
-            if (hq != slot) {
-#pragma unroll
-                for (int i = 0; i < RPL; i++) x[i] = a.q[(size_t)(g * group + hq) * HD + lane + 64 * i];
+            kb[wave][d] = kq;
+            if (slot == 0) {
+                const size_t off = ((size_t)g * a.ctx + pos) * HD + d;
+                a.kc[off] = kq;
+                a.vc[off] = hy_to_bf16(vx[i]);
             }
-            float y[RPL];
-            rope_norm_wave<HD>(x, scr[wave], rc, rs, half, nw, a.eps, lane, y);
-#pragma unroll
-            for (int i = 0; i < RPL; i++) qn[hq][lane + 64 * i] = y[i];
         }
     }
-    hy_lds_barrier();  // LDS only: the key rows stay in flight
+    for (int hq = slot, k = 0; hq < group; hq += HW, k++) {
+        if (hq != slot) {
+#pragma unroll
+            for (int i = 0; i < RPL; i++) x[i] = a.q[(size_t)(g * group + hq) * HD + lane + 64 * i];
+        }
+        float y[RPL];
+        rope_norm_wave<HD>(x, scr[wave], rc, rs, half, nw, a.eps, lane, y);
+#pragma unroll
+        for (int i = 0; i < RPL; i++) qn[wave][k][lane + 64 * i] = y[i];
+    }
+    // the wavefront reads its own LDS rows from here on
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // 2. scores s_j = dot_bf16(q, K_j) * (1/sqrtf(hd)) (src/model.c:778-782) of this workgroup's
     //    segments, key pos from this token's bf16 k; the maximum of each kSplitMaxSeg positions
     //    (order-free)
-    if (!hasq) return;
     const float scale = 1.0f / sqrtf((float)HD);
     for (int sgm = blockIdx.x; sgm < nseg; sgm += gridDim.x) {
         const int r = sgm * kSplitSeg + koff;
         if (sgm != (int)blockIdx.x && r < pos) a1_load_key<HD>(kr, K, r);
-        if (r == pos) a1_load_key<HD>(kr, kb, 0);
-        for (int hq = slot; hq < group; hq += HW) {
-            const float s = a1_score_pair<HD>(kr, qn[hq], par, scale);
+        if (r == pos) a1_load_key<HD>(kr, kb[wave], 0);
+        for (int hq = slot, k = 0; hq < group; hq += HW, k++) {
+            const float s = a1_score_pair<HD>(kr, qn[wave][k], par, scale);
             const int hh = g * group + hq;
             if (r < n && par == 0) a.sc[(size_t)hh * a.sc_stride + r] = s;
             const float m = hy_wave_max(r < n ? s : -__builtin_inff());
@@ -942,7 +946,7 @@ __global__ __launch_bounds__(kSoThreads) void k_attn_out(Attn1Args a) {
         so_load_v<HD>(vc, V, 2 * kSoTile, pt, cap);
     }
     a1_fence();
-    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    const int pos = a.pos_dev ? hy_sload_i32(a.pos_dev) : a.pos0;  // not waiting for the V loads
     const int n = pos + 1, nseg = (n + kSplitMaxSeg - 1) / kSplitMaxSeg;  // segment maxima in use
 
     // 1. max over the segment maxima (src/model.c:781-782; order-free)

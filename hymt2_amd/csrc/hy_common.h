@@ -69,6 +69,18 @@ __device__ __forceinline__ void hy_sgpr_pin(const T& v) {
     asm volatile("" ::"s"(v));
 }
 
+// A uniform int from device memory by a scalar load, waited for on its own (lgkmcnt). Read as
+// `*p` in a kernel that also stores to global memory, the compiler emits a vector load, whose
+// wait covers every vector load issued before it (the counter runs in order): a kernel that
+// issues its bulk loads first would then wait for all of them to learn, say, the position. The
+// value must not be written by the kernel itself (the scalar cache is not coherent with vector
+// stores; a kernel's start invalidates it).
+__device__ __forceinline__ int hy_sload_i32(const int* p) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+
 // Entry i (i < 32) of hy_expf's table, for a kernel that keeps a copy in LDS (hy_expf_tab): the
 // load is issued at kernel entry and the value stored to LDS before a barrier that precedes the
 // first expf, so no lookup waits on global memory.
