@@ -569,11 +569,7 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
     // 0. loads: this token's q / k / v row for wavefronts 0 / 1 / 2 with the norm weights, the
     //    position (scalar) and its RoPE row (rope_cur when the position lives in device memory),
     //    then the key rows of the first pass (those below the position) and the first V tile
-    // readfirstlane: the position is one value for the workgroup; loaded through a pointer the
-    // compiler could not tell that, and every loop bound and branch derived from it would compile
-    // as divergent (exec-masked exits that merge back into the loops)
-    // The rows and norm weights first, before the position is read: scalar loads are waited
-    // for all together, so a row load issued after the position's load would wait for it.
+    // The rows and norm weights first: loads return in issue order.
     float x[RPL], rc[RPL], rs[RPL], nw[RPL];
     const uint64_t etv = tid < 32 ? hy_exp_tab_entry(tid) : 0;  // expf table entry, into LDS before the max
     {
@@ -586,10 +582,13 @@ __global__ __launch_bounds__(kA1Threads) void k_attn1(Attn1Args a) {
             nw[i] = nsrc[d];
         }
     }
-    // instruction order only (a memory clobber here would turn the position's scalar load into
-    // a vector load whose wait covers the rows)
+    // The position by a scalar load waited for on its own: read as *pos_dev it compiled to a
+    // vector load whose wait covered the row loads just issued (the previous kernel's output,
+    // about 1.8 us), and the key and V loads that need the position went out only after them.
+    // (Issuing the pair form's key rows and the V tiles before the position, clamped, was slower:
+    // their 64 KB delayed the rows the RoPE needs first, 1022 -> 993 tok/s.)
     __builtin_amdgcn_sched_barrier(0);
-    const int pos = __builtin_amdgcn_readfirstlane(a.pos_dev ? *a.pos_dev : a.pos0);
+    const int pos = a.pos_dev ? hy_sload_i32(a.pos_dev) : a.pos0;
     {
         const float* cs = a.rope_cur ? a.rope_cur : a.rope_cos + (size_t)pos * half;
         const float* sn = a.rope_cur ? a.rope_cur + half : a.rope_sin + (size_t)pos * half;
