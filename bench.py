@@ -451,6 +451,22 @@ def summarize_trace(d: str):
         if att:
             print()
             print("Chunk attention per launch step (us): " + " ".join(f"{x:.0f}" for x in att))
+        # the decode that follows the window (config 4: 256 tokens at positions 1024-1279, 255
+        # steps after the prompt's last forward): its split attention, per launch
+        end = int(main[-1]["End_Timestamp"])
+        after = [r for r in rows if int(r["Start_Timestamp"]) > end]
+        dec = {}
+        for name in ("k_attn_scores", "k_attn_out"):
+            v = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0 for r in after
+                 if name in r["Kernel_Name"]][:255 * 32]
+            if v:
+                dec[name] = (len(v), sum(v) / len(v))
+        if dec:
+            print()
+            print("Split attention in the decode after the window: " +
+                  ", ".join(f"{k} {n} launches {a:.2f} us" for k, (n, a) in dec.items()) +
+                  f" ({sum(a for _, a in dec.values()):.2f} us a layer)")
+            summary["decode_after_prefill"] = {k: dict(launches=n, avg_us=round(a, 3)) for k, (n, a) in dec.items()}
     print()
     print(json.dumps(summary))
 
