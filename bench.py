@@ -286,15 +286,25 @@ def config4(b):
     f = np.load(os.path.join(ROOT, "tests", "golden", "baseline_config4.npz"), allow_pickle=False)
     if not (np.array_equal(f["prompt"], prompt) and np.array_equal(ids[:len(f["greedy"])], f["greedy"])):
         raise RuntimeError("config 4: greedy ids differ from the reference's (tests/golden/baseline_config4.npz)")
-    _, st1 = fm.generate_device(prompt, 2, chunk=1)          # the same prompt one position per step
+
+    def after(first2):
+        """Logits of a fused_forward at position n_prompt + 1 after a two-id device run: they
+        read every layer's K/V at all earlier positions, which the prefill wrote."""
+        return fm.forward([int(first2[1])], n_prompt + 1, True).view(np.uint32)
+
+    logits_pipe = after(ids)
+    ids_step, st1 = fm.generate_device(prompt, 2, chunk=1)   # the same prompt one position per step
+    logits_step = after(ids_step)
     depth = b.prefill_pipeline(1)                            # chunks one after another
     try:
         fm.generate_device(prompt[:chunk + 5], 2, chunk=chunk)
         ids_seq, st_seq = fm.generate_device(prompt, 2, chunk=chunk)
     finally:
         b.prefill_pipeline(depth)
-    if ids_seq[0] != ids[0]:
-        raise RuntimeError("config 4: the pipelined and the one-chunk-after-another prefill disagree")
+    logits_seq = after(ids_seq)
+    if not (np.array_equal(ids_seq, ids[:2]) and np.array_equal(ids_step, ids[:2]) and
+            np.array_equal(logits_seq, logits_pipe) and np.array_equal(logits_step, logits_pipe)):
+        raise RuntimeError("config 4: the pipelined, one-chunk-after-another and stepwise prefills disagree")
     weights = sum(L[nm].n * L[nm].k for L in model["layers"] for nm in ("wq", "wk", "wv", "wo", "wg", "wu", "wd"))
     ops = 2.0 * weights * n_prompt
     pre_s = st.prefill_ms / 1e3
@@ -305,7 +315,9 @@ def config4(b):
     fm.close()
     return dict(workload=f"config4: Hy-MT2-1.8B-shaped Q2_0C, {n_prompt}-token random prompt in {chunk}-token "
                          f"chunks, then {n_gen} greedy tokens (device loop)",
-                greedy_parity=f"first {len(f['greedy'])} ids identical to the reference's gen_ids at ISA scalar",
+                greedy_parity=f"first {len(f['greedy'])} ids identical to the reference's gen_ids at ISA scalar; "
+                              f"logits at position {n_prompt + 1} bit-identical after the pipelined, the "
+                              f"one-chunk-after-another and the stepwise prefill",
                 prefill_schedule=f"{chunk}-token chunks pipelined over the layers, up to {depth} in flight "
                                  f"(chunk i's layer l in the launches of chunk i + 1's layer l - 1; the same bits "
                                  f"as one chunk after another)",

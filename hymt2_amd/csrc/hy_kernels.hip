@@ -927,8 +927,7 @@ hipError_t launch_attention(const PipeAttn& J, int rows, hipStream_t s) {
     if (a.hdim == 128 && grp == 4) k_attn_chunk_pipe<128, 4><<<grid, kAcThreads, 0, s>>>(J);
     else if (a.hdim == 128 && grp == 2) k_attn_chunk_pipe<128, 2><<<grid, kAcThreads, 0, s>>>(J);
     else if (a.hdim == 64 && grp == 4) k_attn_chunk_pipe<64, 4><<<grid, kAcThreads, 0, s>>>(J);
-    else if (a.hdim == 64 && grp == 2) k_attn_chunk_pipe<64, 2><<<grid, kAcThreads, 0, s>>>(J);
-    else return hipErrorNotSupported;
+    else return hipErrorNotSupported;  // head dim 64 with 2 query heads per KV head does not quantize in place
     return hipGetLastError();
 }
 

@@ -284,28 +284,36 @@ def test_full_size_model_short_run(backend, mode):
         fm.close()
 
 
-@pytest.mark.parametrize("mode", ["q2", "stq"])
-def test_pipelined_prefill_matches_sequential(backend, mode):
+@pytest.mark.parametrize("mode,heads,kv_heads,hdim", [("q2", 16, 4, 128), ("stq", 16, 4, 128),
+                                                      ("q2", 16, 8, 128), ("stq", 32, 8, 64)])
+def test_pipelined_prefill_matches_sequential(backend, mode, heads, kv_heads, hdim):
     """The device loop's chunked prefill pipelined over the layers (up to 8 chunks in flight,
     chunk i's layer l in the same launches as chunk i + 1's layer l - 1) against one chunk after
     another and the oracle: a 300-token prompt in chunks of 33 (ten chunks, the last of 3
     tokens), so the default depth runs a group of eight and a group of two, and depth 3 four
-    groups; greedy ids equal at every depth and equal the oracle's."""
-    shape = synth.ModelShape(n_layer=3, vocab=1000, ctx=320)
+    groups. At every depth the 10 greedy ids equal the oracle's, and so do the logits of a
+    fused_forward at position 310 after them, bit for bit: that forward reads every layer's K/V
+    of all 310 earlier positions, which the pipelined launches wrote for the prompt. Query
+    heads per KV head and head dims 4 x 128, 2 x 128 and 4 x 64 run the three pipelined
+    attention kernels k_attn_chunk_pipe<128, 4>, <128, 2> and <64, 4>."""
+    shape = synth.ModelShape(n_layer=3, heads=heads, kv_heads=kv_heads, hdim=hdim, vocab=1000, ctx=320)
     model = synth.make_model(shape, mode=mode, seed=59)
     prompt = synth.rand_prompt(synth.rng(60), 300, shape.vocab)
     want = O.OracleModel(model, threads=8).generate(prompt, 10, batch=16)
+    om = O.OracleModel(model, threads=8)
+    for i in range(0, len(prompt), 16):
+        om.forward(prompt[i:i + 16], i, want_logits=False)
+    ref = om.forward(want, len(prompt), want_logits=True)
     fm = lib.FusedModel(backend, model)
     try:
-        got = {}
         for depth in (8, 3, 1):
             prev = backend.prefill_pipeline(depth)
             try:
-                got[depth], _ = fm.generate_device(prompt, 10, chunk=33)
+                ids, _ = fm.generate_device(prompt, 10, chunk=33)
             finally:
                 backend.prefill_pipeline(prev)
-        for depth, ids in got.items():
             assert np.array_equal(ids, want), f"depth={depth}"
+            assert np.array_equal(bits(fm.forward([int(ids[-1])], 309, True)), bits(ref)), f"depth={depth}"
         assert backend.prefill_pipeline(0) == 8
     finally:
         fm.close()
@@ -391,10 +399,10 @@ def test_split_attention_head_dim_256(backend):
 @pytest.mark.parametrize("kv_heads", [1, 2])
 def test_chunk_attention_long_rows(backend, kv_heads):
     """Chunk attention at head dim 128 over rows of up to 1500 positions, 4 or 2 query heads per
-    KV head: the softmax sums of rows up to 256 positions by the lane-serial chain, up to 1024 by
-    the exact segmented workgroup sum with two wavefronts a head, beyond by four wavefronts a head
-    in rounds. The last logits of a 1500-token prompt in 128-token chunks and 16 device greedy
-    ids after it, against the oracle."""
+    KV head: each row's softmax sum by the 16-lane row chain in rounds of 512 positions (one to
+    three rounds here), the running sum carried from one round into the next. The last logits of
+    a 1500-token prompt in 128-token chunks and 16 device greedy ids after it, against the
+    oracle."""
     shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=4, kv_heads=kv_heads, hdim=128, vocab=600, ctx=1536)
     model = synth.make_model(shape, mode="q2", seed=83 + kv_heads)
     prompt = synth.rand_prompt(synth.rng(85 + kv_heads), 1500, shape.vocab)
