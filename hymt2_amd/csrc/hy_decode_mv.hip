@@ -61,8 +61,11 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
     const float* const lx = L.x;
     const float* const lnorm = L.norm_w;
     const HyQ8K* const lact = L.act;
+    const float leps = L.eps;
+    unsigned long long* const lslots = L.slots;
+    const int n_arg = L.n_arg;
     hy_sgpr_pin(pair), hy_sgpr_pin(njobs), hy_sgpr_pin(rows_per_wg), hy_sgpr_pin(lx), hy_sgpr_pin(lnorm),
-        hy_sgpr_pin(lact);
+        hy_sgpr_pin(lact), hy_sgpr_pin(leps), hy_sgpr_pin(lslots), hy_sgpr_pin(n_arg);
     mv1_pin_job<KIND>(j0), mv1_pin_job<KIND>(j1), mv1_pin_job<KIND>(j2);
     int jsel = 0;
     if (!pair) {
@@ -133,7 +136,7 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
             // RMSNorm, src/model.c:719-739: sequential sum of squares, then x * scale * w
             static_assert(R == 1, "RMSNorm prologue over 2048 values");
             const float sum = hy_block_exact_sq_sum8<kMv1Waves>(e[0], ex_lds, wave, lane);
-            const float scale = 1.0f / sqrtf(sum / (float)K + L.eps);
+            const float scale = 1.0f / sqrtf(sum / (float)K + leps);
 #pragma unroll
             for (int i = 0; i < 8; i++) e[0][i] = e[0][i] * scale * nw[0][i];
         }
@@ -174,10 +177,10 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
 #pragma unroll
                 for (int b = 0; b < NB; b++) acc += terms[wave][lane][b];
                 J.out[r] = J.epi == EPI_ADD ? resid + acc : acc;  // residual: h += tmp
-                if (r < L.n_arg) key = argmax_key(acc, r);
+                if (r < n_arg) key = argmax_key(acc, r);
             }
         }
-        if (L.slots) hy_wg_slot_max(key, L.slots + wg);
+        if (lslots) hy_wg_slot_max(key, lslots + wg);
     } else if (lane < ITERS) {
         const int p = row0 + wave * ITERS + lane;
         if (p < n) {

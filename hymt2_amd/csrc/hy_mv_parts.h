@@ -30,11 +30,20 @@ __device__ __forceinline__ uint32_t row_max_u(uint32_t v) {
     x = (int)max((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
     return (uint32_t)x;
 }
+__device__ __forceinline__ uint32_t row_min_u(uint32_t v) {
+    int x = (int)v;
+    x = (int)min((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP1>(x));
+    x = (int)min((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_QSWAP2>(x));
+    x = (int)min((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_HMIRROR>(x));
+    x = (int)min((uint32_t)x, (uint32_t)hy_dpp<HY_DPP_MIRROR>(x));
+    return (uint32_t)x;
+}
 // Q8_K of two 256-element blocks (quantize_q8k, src/kernels.c:128-165) held 8 consecutive
 // elements per lane: lanes 0..31 hold dst[0]'s elements 8l..8l+7, lanes 32..63 dst[1]'s.
 // The block's maximum magnitude (|x| bits, as the unsigned integers order them) by a row
-// reduction and a row-pair swap; its first element by a ballot of the lanes holding one (the
-// lowest such lane, then its lowest element).
+// reduction and a row-pair swap; the sign of its first element (in element order) by the same
+// reduction over keys 2 * index + sign of the lanes holding it, so the block's signed maximum
+// stays in vector registers (a ballot and readlanes would round-trip through scalar ones).
 __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int lane) {
     const int hl = lane >> 5, jl = lane & 31;
     uint32_t ab[8];
@@ -47,16 +56,17 @@ __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int 
     int li = 8;  // this lane's first element of magnitude am
 #pragma unroll
     for (int i = 7; i >= 0; i--) li = ab[i] == am ? i : li;
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(li < 8);  // each half has one: am is one of its values
-    const int l0 = __builtin_ctz((uint32_t)hit), l1 = 32 + __builtin_ctz((uint32_t)(hit >> 32));
-    float cand = e[0];
+    uint32_t sg = hy_fbits(e[0]) >> 31;
 #pragma unroll
-    for (int i = 1; i < 8; i++) cand = li == i ? e[i] : cand;
-    const float vm0 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), l0));
-    const float vm1 = hy_bitsf((uint32_t)__builtin_amdgcn_readlane((int)hy_fbits(cand), l1));
-    const float vmax = hl ? vm1 : vm0;
+    for (int i = 1; i < 8; i++) sg = li == i ? hy_fbits(e[i]) >> 31 : sg;
+    // each half holds am at least once: the smallest key is its first occurrence
+    const uint32_t key = li < 8 ? ((uint32_t)(8 * jl + li) << 1 | sg) : 0xffffffffu;
+    uint32_t ke, ko;
+    hy_row_pair(row_min_u(key), ke, ko);
+    const float vmax = hy_bitsf(am | (min(ke, ko) & 1u) << 31);
     const bool zero = am == 0;
     const float iscale = zero ? 0.f : -127.f / vmax;
+    const float dq = zero ? 0.f : 1.f / iscale;  // the block's d, off the path of the stores below
     int q[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -86,7 +96,7 @@ __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int 
     if ((jl & 1) == 0) y->bsums[jl >> 1] = (int16_t)s16;
     if (jl < 6) dw[296 / 4 + jl] = 0;
     if (jl == 0) {
-        y->d = zero ? 0.f : 1.f / iscale;
+        y->d = dq;
         y->sum = total;
     }
 }
