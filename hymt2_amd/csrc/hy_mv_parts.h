@@ -184,18 +184,22 @@ __device__ __forceinline__ WSeg load_wseg(int kind, const uint8_t* w, const uint
 // The panel segment's exact int32 block dot enc (reduced over the block's four lanes), and the
 // fp32 term made from it (src/kernels.c:576): mv1_term for KIND_PANEL in two steps, so that the
 // dot can run before the activation's d and sum are final.
+// Field l of a panel byte is taken in place (w & 3 << 2l: the code times 4^l, at most 48 for
+// l <= 2, a non-negative int8) or, for l = 3, shifted down to the l = 2 position; the dots of
+// each scale run as their own chain and the exact multiples are shifted back at the end.
 __device__ __forceinline__ int mv1_panel_enc(const WSeg& S, const ActSeg& A) {
     const uint32_t w4[4] = {S.a.x, S.a.y, S.a.z, S.a.w};
-    const int4 qa[4] = {A.q0, A.q1, A.q2, A.q3};
-    int p = 0;
+    const int qa[4][4] = {{A.q0.x, A.q0.y, A.q0.z, A.q0.w}, {A.q1.x, A.q1.y, A.q1.z, A.q1.w},
+                          {A.q2.x, A.q2.y, A.q2.z, A.q2.w}, {A.q3.x, A.q3.y, A.q3.z, A.q3.w}};
+    int p0 = 0, p1 = 0, p2 = 0, p3 = 0;
 #pragma unroll
-    for (int l = 0; l < 4; l++) {
-        p = hy_dot4(hy_field(w4[0], l), qa[l].x, p);
-        p = hy_dot4(hy_field(w4[1], l), qa[l].y, p);
-        p = hy_dot4(hy_field(w4[2], l), qa[l].z, p);
-        p = hy_dot4(hy_field(w4[3], l), qa[l].w, p);
+    for (int k = 0; k < 4; k++) {
+        p0 = hy_dot4((int)(w4[k] & 0x03030303u), qa[0][k], p0);
+        p1 = hy_dot4((int)(w4[k] & 0x0C0C0C0Cu), qa[1][k], p1);
+        p2 = hy_dot4((int)(w4[k] & 0x30303030u), qa[2][k], p2);
+        p3 = hy_dot4((int)((w4[k] >> 2) & 0x30303030u), qa[3][k], p3);
     }
-    return hy_quad_sum(p);
+    return hy_quad_sum(p0 + (p1 >> 2) + ((p2 + p3) >> 4));
 }
 __device__ __forceinline__ float mv1_panel_term(const WSeg& S, int enc, float d, int sum, int pshift, int poff) {
     return hy_bitsf(S.sd) * d * (float)((enc << pshift) - poff * sum);
