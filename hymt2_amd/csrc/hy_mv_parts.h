@@ -40,30 +40,46 @@ __device__ __forceinline__ uint32_t row_min_u(uint32_t v) {
 }
 // Q8_K of two 256-element blocks (quantize_q8k, src/kernels.c:128-165) held 8 consecutive
 // elements per lane: lanes 0..31 hold dst[0]'s elements 8l..8l+7, lanes 32..63 dst[1]'s.
-// The block's maximum magnitude (|x| bits, as the unsigned integers order them) by a row
-// reduction and a row-pair swap; the sign of its first element (in element order) by the same
-// reduction over keys 2 * index + sign of the lanes holding it, so the block's signed maximum
-// stays in vector registers (a ballot and readlanes would round-trip through scalar ones).
+// The block's signed maximum stays in vector registers (a ballot and readlanes would round-trip
+// through scalar ones): two row reductions and row-pair swaps, run together, of the keys
+// |x| bits << 1 | sign and |x| bits << 1 | !sign give the maximum magnitude (as the unsigned
+// integers order |x| bits) and tell whether it occurs with one sign only, which then is the
+// first occurrence's. Only a block holding both +max and -max looks for its first occurrence
+// (a third reduction, over keys 2 * index + sign of the lanes holding the magnitude).
 __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int lane) {
     const int hl = lane >> 5, jl = lane & 31;
-    uint32_t ab[8];
+    uint32_t kn[8], kp[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) ab[i] = hy_fbits(e[i]) & 0x7fffffffu;
-    uint32_t m = max(max(max(ab[0], ab[1]), max(ab[2], ab[3])), max(max(ab[4], ab[5]), max(ab[6], ab[7])));
-    uint32_t me, mo;
-    hy_row_pair(row_max_u(m), me, mo);
-    const uint32_t am = max(me, mo);
-    int li = 8;  // this lane's first element of magnitude am
+    for (int i = 0; i < 8; i++) {
+        const uint32_t u = hy_fbits(e[i]);
+        kn[i] = u << 1 | u >> 31;        // ties of magnitude: the negative one is larger
+        kp[i] = u << 1 | (~u >> 31);     // ties of magnitude: the positive one is larger
+    }
+    uint32_t mn = max(max(max(kn[0], kn[1]), max(kn[2], kn[3])), max(max(kn[4], kn[5]), max(kn[6], kn[7])));
+    uint32_t mp = max(max(max(kp[0], kp[1]), max(kp[2], kp[3])), max(max(kp[4], kp[5]), max(kp[6], kp[7])));
+    uint32_t ne, no, pe, po;
+    mn = row_max_u(mn);
+    mp = row_max_u(mp);
+    hy_row_pair(mn, ne, no);
+    hy_row_pair(mp, pe, po);
+    mn = max(ne, no);
+    mp = max(pe, po);
+    const uint32_t am = mn >> 1;  // the maximum |x| bits
+    uint32_t sgn = mn & 1u;       // 1 if -max occurs; then, unless +max occurs too, the sign
+    if (mn & mp & 1u & (am != 0)) {  // both signs (uniform per half, so whole 16-lane rows)
+        int li = 8;  // this lane's first element of magnitude am
 #pragma unroll
-    for (int i = 7; i >= 0; i--) li = ab[i] == am ? i : li;
-    uint32_t sg = hy_fbits(e[0]) >> 31;
+        for (int i = 7; i >= 0; i--) li = kn[i] >> 1 == am ? i : li;
+        uint32_t sg = kn[0] & 1u;
 #pragma unroll
-    for (int i = 1; i < 8; i++) sg = li == i ? hy_fbits(e[i]) >> 31 : sg;
-    // each half holds am at least once: the smallest key is its first occurrence
-    const uint32_t key = li < 8 ? ((uint32_t)(8 * jl + li) << 1 | sg) : 0xffffffffu;
-    uint32_t ke, ko;
-    hy_row_pair(row_min_u(key), ke, ko);
-    const float vmax = hy_bitsf(am | (min(ke, ko) & 1u) << 31);
+        for (int i = 1; i < 8; i++) sg = li == i ? kn[i] & 1u : sg;
+        // each half holds am at least once: the smallest key is its first occurrence
+        const uint32_t key = li < 8 ? ((uint32_t)(8 * jl + li) << 1 | sg) : 0xffffffffu;
+        uint32_t ke, ko;
+        hy_row_pair(row_min_u(key), ke, ko);
+        sgn = min(ke, ko) & 1u;
+    }
+    const float vmax = hy_bitsf(am | sgn << 31);
     const bool zero = am == 0;
     const float iscale = zero ? 0.f : -127.f / vmax;
     const float dq = zero ? 0.f : 1.f / iscale;  // the block's d, off the path of the stores below
@@ -93,12 +109,12 @@ __device__ inline void q8k_quantize_halves(const float (&e)[8], HyQ8K* dst, int 
     const int seg = (c == 1) ? 2 : (c == 2 ? 1 : c);
     dw[(l * 64 + seg * 16 + i0) / 4] = p[0];
     dw[(l * 64 + seg * 16 + i0) / 4 + 1] = p[1];
-    if ((jl & 1) == 0) y->bsums[jl >> 1] = (int16_t)s16;
-    if (jl < 6) dw[296 / 4 + jl] = 0;
-    if (jl == 0) {
-        y->d = dq;
-        y->sum = total;
-    }
+    // unconditional stores, several lanes writing the same value to one address: lanes 2k and
+    // 2k + 1 hold the same 16-element sum, every lane of a half the same d and sum
+    y->bsums[jl >> 1] = (int16_t)s16;
+    dw[296 / 4 + min(jl, 5)] = 0;
+    y->d = dq;
+    y->sum = total;
 }
 
 // 6-bit scale / min j of a Q4_K header (src/kernels.c:839-842) from its words y, z, w.

@@ -187,7 +187,11 @@ def test_q8k_vs_oracle(backend, k, nt):
     g = synth.rng(k + nt)
     x = synth.activations(g, nt, k)
     x[0, :256] = 0.0
-    x[-1, 11], x[-1, 40] = -4.0, 4.0
+    x[-1, 11], x[-1, 40] = -4.0, 4.0        # the block's maximum magnitude with both signs: -max first
+    if k >= 1024:
+        x[-1, 261], x[-1, 456] = 5.0, -5.0  # +max first, in another lane
+        x[-1, 520], x[-1, 523] = -6.0, 6.0  # both in one lane's eight elements
+        x[-1, 770], x[-1, 771] = 7.0, -7.0
     x[nt // 2, 300 % k] = 1e25
     _, got = q8k_dev(backend, x)
     assert got.tobytes() == O.quantize_q8k(x).tobytes()
