@@ -161,7 +161,9 @@ __global__ __launch_bounds__(kMv1Threads) void k_mv1(Mv1Launch L) {
             } else {
                 t = mv1_term<KIND>(ws[i][s], A[s], sub, pshift, poff);
             }
-            if (sub == 0) terms[wave][rw][b] = t;
+            // every lane of the block holds the same term (its dot is reduced over the block's
+            // lanes, its scales are the block's): an unconditional store, no exec-mask round trip
+            terms[wave][rw][b] = t;
         }
     }
     __syncthreads();

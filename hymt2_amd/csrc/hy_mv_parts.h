@@ -221,8 +221,9 @@ __device__ __forceinline__ float mv1_panel_term(const WSeg& S, int enc, float d,
     return hy_bitsf(S.sd) * d * (float)((enc << pshift) - poff * sum);
 }
 
-// fp32 block term of one segment, valid in the lane with sub == 0 of each block. Every lane of
-// the block must call it (DPP group reductions).
+// fp32 block term of one segment, the same value in every lane of the block (the dot reduced
+// over the block's lanes, the block's scales). Every lane of the block must call it (DPP group
+// reductions).
 template <int KIND>
 __device__ __forceinline__ float mv1_term(const WSeg& S, const ActSeg& A, int sub, int pshift, int poff) {
     if (KIND == KIND_PANEL) {
