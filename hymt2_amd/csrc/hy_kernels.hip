@@ -3,6 +3,8 @@
 // are exact in any order, and every fp32 reduction runs sequentially in the reference's order
 // in one lane, while the parallel work (loads, int8 dot products, exponentials, elementwise
 // ops) is spread over the wavefronts.
+#include <cstdlib>
+
 #include "hy_kernels.h"
 #include "hy_mv_parts.h"
 
@@ -907,6 +909,248 @@ __global__ __launch_bounds__(kAcThreads, 3) void k_attn_chunk_pipe(PipeAttn J) {
     attn_chunk_row<HD, GRP, kAcTilePipe>(J.a[j], blockIdx.x, row - J.row0[j]);
 }
 
+// Four-token chunk attention (pipelined prefill, head dim 128, four query heads a KV head): one
+// 512-thread workgroup per (KV head, four consecutive tokens) computes the 16 (token, head) rows
+// with the arithmetic of attn_chunk_row (src/model.c:767-795), the products on the matrix cores.
+// v_mfma_f32_16x16x1f32 with a zero accumulator returns, in lane l, register r, the product
+// A[16 (r / 4) + 4 (l / 16) + r % 4] * B[16 (r / 4) + l % 16] of the lanes' operands, rounded
+// once, as the separately rounded product a * b (measured bit for bit over normal, denormal and
+// overflowing operands; a -0 product comes back as +0, which no sum here can tell apart: each
+// starts at +0, and a round-to-nearest sum that starts at +0 is never -0). Its 16 rows are the
+// (token, head) rows, 4 t + h; its four blocks are
+//   scores: dot_bf16's four partial sums (src/kernels.c:1111-1121): block c takes dimension
+//     4 i + c, so lane l's register 4 c + h is the chain-c product of head h of token l / 16
+//     with key l % 16, and the lane keeps the 16 chains of its four scores;
+//   output: four consecutive positions 4 i + b, so register 4 b + h is position 4 i + b's
+//     product p_j * V_j[d] of head h of token l / 16 at dimension d = 16 w + l % 16 (wavefront w),
+//     added to the head's chain in position order (axpy_bf16, :1122-1124).
+// A key and a V row are read once for four tokens, each MFMA leaves the VALU 16 adds (one per
+// product), and all eight wavefronts carry output chains. Rows past a token's position have
+// p_j = 0, whose products add nothing. The sums of e_j in position order: wavefront t < 4 takes
+// token t's four rows (hy_row_seq_sums). Scores live in LDS, 16 rows of P.sstride floats.
+constexpr int kA4Threads = 512;
+constexpr int kA4Tok = 4;
+constexpr int kA4Tile = 32;  // V positions per bf16 LDS tile (one 16-byte piece a thread)
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f a4_products(float row_operand, float col_operand) {
+    const v16f z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(row_operand, col_operand, z, 0, 0, 0);
+}
+
+struct PipeAttn4 {
+    PipeAttn J;
+    int grp0[kPipeMax];  // first grid row (four-token group) of each job
+    int sstride;         // score row stride in LDS, floats (4 mod 32, past the longest row)
+};
+
+size_t attn4_lds_bytes(int sstride) { return (size_t)16 * sstride * sizeof(float) + (size_t)kA4Tile * 128 * sizeof(uint16_t); }
+constexpr size_t kA4MaxDynLds = 156 * 1024;  // of the CU's 160 KB, beside the kernel's static LDS
+
+static bool attn4_enabled() {
+    static const bool on = [] { const char* e = getenv("HYMT2_ATTN4"); return !(e && e[0] == '0'); }();
+    return on;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kA4Threads) void k_attn_chunk4_pipe(PipeAttn4 P) {
+    static_assert(HD == 128, "16 output dimensions a wavefront, 8 wavefronts");
+    constexpr int NW = kA4Threads / 64;
+    constexpr int GRP = 4;
+    static_assert(kA4Tile * HD * 2 == 16 * kA4Threads && 16 * HD * 4 == kA4Tile * HD * 2,
+                  "one V piece a thread; the q rows and the outputs stage in the V tile's bytes");
+    extern __shared__ __align__(16) float a4_lds[];
+    __shared__ float red[NW][16];
+    __shared__ float rmax[16];
+    __shared__ float inv_s[16];
+    __shared__ uint64_t etab[32];
+    const int S = P.sstride;
+    float* sc = a4_lds;                                               // [16][S]: s, then e, then p
+    uint16_t* vt = reinterpret_cast<uint16_t*>(a4_lds + 16 * S);      // [kA4Tile][HD] bf16
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grow = (int)(gridDim.y - 1 - blockIdx.y);  // the jobs' last (longest) groups first
+    const int jb = pipe_job(P.grp0, P.J.njobs, grow);
+    const AttnArgs& a = P.J.a[jb];
+    const int g = blockIdx.x;
+    const int t0 = (grow - P.grp0[jb]) * kA4Tok;
+    const int ntv = min(kA4Tok, a.nt - t0);  // tokens of the group
+    const int pos0 = a.pos0 + t0;            // position of its first token
+    const int nmax = pos0 + ntv;             // keys 0 .. nmax - 1 (the last token's row)
+    const int nmax4 = (nmax + 3) & ~3;
+    const int qdim = a.heads * HD;
+    const uint16_t* K = a.kc + (size_t)g * a.ctx * HD;
+    const uint16_t* V = a.vc + (size_t)g * a.ctx * HD;
+
+    // first V tile's piece of this thread (position tid / 16, dimensions 8 (tid % 16) ..)
+    constexpr int PPR = HD / 8;  // 16-byte pieces a position
+    uint4 vr = *reinterpret_cast<const uint4*>(V + (size_t)min(tid / PPR, nmax - 1) * HD + 8 * (tid % PPR));
+
+    // q rows chain-major in the V tile's bytes: qs[row][32 c + i] = q[token row / 4][head row % 4][4 i + c]
+    if (tid < 32) etab[tid] = hy_exp_tab_entry(tid);
+    {
+        float* qs = reinterpret_cast<float*>(vt);
+        for (int e = tid; e < 16 * HD; e += kA4Threads) {
+            const int row = e / HD, d = e % HD;
+            const int tt = min(row / GRP, ntv - 1), h = row % GRP;
+            qs[row * HD + (d & 3) * 32 + (d >> 2)] = a.q[(size_t)(t0 + tt) * qdim + (size_t)(g * GRP + h) * HD + d];
+        }
+    }
+    __syncthreads();
+    // this lane's row operands: row l % 16, chain l / 16, i = 0 .. 31
+    float qa[32];
+    {
+        const float* qs = reinterpret_cast<const float*>(vt) + (lane & 15) * HD + (lane >> 4) * 32;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(qs + i);
+            qa[i] = x.x, qa[i + 1] = x.y, qa[i + 2] = x.z, qa[i + 3] = x.w;
+        }
+    }
+
+    // scores: wavefront w takes the 16-key batches w, w + 8, ... (uniform loop bound); lane l
+    // supplies key l % 16's dimension 4 i + l / 16, picked out of the key's 16-byte piece m = i / 2
+    // into the high half of a dword (the bf16 -> fp32 conversion) by a byte permute
+    const float scale = 1.0f / sqrtf((float)HD);
+    const uint32_t kc2 = 2u * (uint32_t)(lane >> 4);
+    const uint32_t ksel = (kc2 + 1) << 24 | kc2 << 16 | 0x0c0cu;
+    const int tl = lane >> 4;                     // the token of this lane's scores
+    const int nl = tl < ntv ? pos0 + tl + 1 : 0;  // its row length
+    float lmax[GRP];
+#pragma unroll
+    for (int h = 0; h < GRP; h++) lmax[h] = -__builtin_inff();
+    constexpr int KPF = 3;  // 16-byte pieces of the key row loaded ahead of their use
+    uint4 kv[HD / 8];
+    {
+        const uint4* kr0 = reinterpret_cast<const uint4*>(K + (size_t)min(wave * 16 + (lane & 15), nmax - 1) * HD);
+#pragma unroll
+        for (int m = 0; m < KPF; m++) kv[m] = kr0[m];
+    }
+    for (int kb = wave * 16; kb < nmax; kb += NW * 16) {
+        const int key = kb + (lane & 15);
+        const uint4* kr = reinterpret_cast<const uint4*>(K + (size_t)min(key, nmax - 1) * HD);
+        const uint4* krn = reinterpret_cast<const uint4*>(K + (size_t)min(key + NW * 16, nmax - 1) * HD);
+        float acc[4][GRP];  // [chain][head]
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int h = 0; h < GRP; h++) acc[c][h] = 0.f;
+        v16f prev;
+#pragma unroll
+        for (int i = 0; i <= HD / 4; i++) {
+            v16f cur;
+            if (i < HD / 4) {
+                const int m = i >> 1;
+                if ((i & 1) == 0) {
+                    if (m + KPF < HD / 8) kv[m + KPF] = kr[m + KPF];
+                    else kv[m + KPF - HD / 8] = krn[m + KPF - HD / 8];
+                }
+                const uint4 x = kv[m];
+                const uint32_t kb32 = (i & 1) ? __builtin_amdgcn_perm(x.w, x.z, ksel) : __builtin_amdgcn_perm(x.y, x.x, ksel);
+                cur = a4_products(qa[i], hy_bitsf(kb32));
+            }
+            if (i > 0) {
+                // the previous dimension's products (its MFMA ran beside this one)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int h = 0; h < GRP; h++) acc[c][h] += prev[4 * c + h];
+#pragma unroll
+                for (int c = 0; c < 4; c++) asm volatile("" : "+v"(acc[c][0]), "+v"(acc[c][1]), "+v"(acc[c][2]), "+v"(acc[c][3]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            prev = cur;
+        }
+        if (key < nl)
+#pragma unroll
+            for (int h = 0; h < GRP; h++) {
+                const float s = ((acc[0][h] + acc[1][h]) + (acc[2][h] + acc[3][h])) * scale;
+                sc[(GRP * tl + h) * S + key] = s;
+                lmax[h] = fmaxf(lmax[h], s);
+            }
+    }
+    // row maxima: over the 16 lanes of a token, then over the wavefronts
+#pragma unroll
+    for (int h = 0; h < GRP; h++) {
+        float m = lmax[h];
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+        lmax[h] = m;
+    }
+    if ((lane & 15) == 0)
+#pragma unroll
+        for (int h = 0; h < GRP; h++) red[wave][GRP * tl + h] = lmax[h];
+    __syncthreads();
+    if (tid < 16) {
+        float m = red[0][tid];
+#pragma unroll
+        for (int w = 1; w < NW; w++) m = fmaxf(m, red[w][tid]);
+        rmax[tid] = m;
+    }
+    __syncthreads();
+    // e_j = expf(s_j - max) within a row, 0 from its length to nmax4
+    for (int row = 0; row < 16; row++) {
+        const int tt = row / GRP, n = tt < ntv ? pos0 + tt + 1 : 0;
+        const float mx = rmax[row];
+        for (int j = tid; j < nmax4; j += kA4Threads) sc[row * S + j] = j < n ? hy_expf_tab(sc[row * S + j] - mx, etab) : 0.f;
+    }
+    __syncthreads();
+    // the sums in position order: wavefront t < ntv takes token t's rows
+    if (wave < ntv) {
+        float sum[4];
+        hy_row_seq_sums<GRP>(sc + (size_t)GRP * wave * S, S, pos0 + wave + 1, lane, sum);
+        if (lane == 0)
+#pragma unroll
+            for (int h = 0; h < GRP; h++) inv_s[GRP * wave + h] = 1.0f / sum[h];
+    }
+    __syncthreads();
+    // p_j = e_j * inv, once per position
+    for (int row = 0; row < 16; row++) {
+        const int tt = row / GRP, n = tt < ntv ? pos0 + tt + 1 : 0;
+        const float inv = tt < ntv ? inv_s[row] : 0.f;
+        for (int j = tid; j < n; j += kA4Threads) sc[row * S + j] = sc[row * S + j] * inv;
+    }
+
+    // output: wavefront w holds dimensions 16 w .. 16 w + 15; lane l supplies p of row l % 16 at
+    // position 4 i + l / 16 and V at that position and dimension 16 w + l % 16
+    const int dcol = wave * 16 + (lane & 15), prow = lane & 15, pc = lane >> 4;
+    const float* pr = sc + prow * S + pc;
+    float o[GRP];
+#pragma unroll
+    for (int h = 0; h < GRP; h++) o[h] = 0.f;
+    for (int tb = 0; tb < nmax4; tb += kA4Tile) {
+        __syncthreads();  // the previous tile read (the first time: p written, q rows read)
+        *reinterpret_cast<uint4*>(vt + (tid / PPR) * HD + 8 * (tid % PPR)) = vr;
+        if (tb + kA4Tile < nmax4)
+            vr = *reinterpret_cast<const uint4*>(V + (size_t)min(tb + kA4Tile + tid / PPR, nmax - 1) * HD + 8 * (tid % PPR));
+        __syncthreads();
+        const int cnt = min(kA4Tile, nmax4 - tb);
+        const uint16_t* vc = vt + pc * HD + dcol;
+        for (int i = 0; i < cnt; i += 4) {
+            const v16f p = a4_products(pr[tb + i], hy_bitsf((uint32_t)vc[i * HD] << 16));
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int h = 0; h < GRP; h++) o[h] += p[4 * b + h];
+        }
+    }
+    if (tl < ntv)
+#pragma unroll
+        for (int h = 0; h < GRP; h++) a.ao[(size_t)(t0 + tl) * qdim + (size_t)(g * GRP + h) * HD + dcol] = o[h];
+    // each token's GRP * HD = 512 outputs are two Q8_K blocks of its row: quantize them here
+    // (quantize_q8k, src/kernels.c:128-165), staged in the V tile's bytes
+    if (a.act_out) {
+        __syncthreads();  // every chain has read its last V tile
+        float* ob = reinterpret_cast<float*>(vt);
+#pragma unroll
+        for (int h = 0; h < GRP; h++) ob[tl * GRP * HD + h * HD + dcol] = o[h];
+        __syncthreads();
+        const int tq = wave >> 1, bq = wave & 1;
+        if (tq < ntv) q8k_quantize_wave(ob + tq * GRP * HD + bq * HY_QK, a.act_out + (size_t)(t0 + tq) * (qdim / HY_QK) + g * 2 + bq, lane);
+    }
+}
+
 bool attention_quantizes(const AttnArgs& a) {
     if (a.ctx > kAcMaxCtx || a.heads % a.kv_heads) return false;
     const int grp = a.heads / a.kv_heads;
@@ -923,6 +1167,28 @@ hipError_t launch_attention(const PipeAttn& J, int rows, hipStream_t s) {
             return hipErrorNotSupported;
     }
     const int grp = a.heads / a.kv_heads;
+    if (a.hdim == 128 && grp == 4 && attn4_enabled()) {
+        // four tokens a workgroup where the positions are the host's and the rows fit in LDS
+        PipeAttn4 P;
+        P.J = J;
+        int groups = 0, nmax = 0;
+        bool host_pos = true;
+        for (int j = 0; j < J.njobs; j++) {
+            host_pos = host_pos && !J.a[j].pos_dev;
+            P.grp0[j] = groups;
+            groups += (J.a[j].nt + kA4Tok - 1) / kA4Tok;
+            nmax = std::max(nmax, J.a[j].pos0 + J.a[j].nt);
+        }
+        P.sstride = ((nmax + 31) & ~31) + 4;
+        const size_t lds = attn4_lds_bytes(P.sstride);
+        if (host_pos && lds <= kA4MaxDynLds) {
+            static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_chunk4_pipe<128>),
+                                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kA4MaxDynLds);
+            if (attr != hipSuccess) return attr;
+            k_attn_chunk4_pipe<128><<<dim3(a.kv_heads, groups), kA4Threads, lds, s>>>(P);
+            return hipGetLastError();
+        }
+    }
     const dim3 grid(a.kv_heads, rows);
     if (a.hdim == 128 && grp == 4) k_attn_chunk_pipe<128, 4><<<grid, kAcThreads, 0, s>>>(J);
     else if (a.hdim == 128 && grp == 2) k_attn_chunk_pipe<128, 2><<<grid, kAcThreads, 0, s>>>(J);
