@@ -1127,12 +1127,37 @@ __global__ __launch_bounds__(kA4Threads) void k_attn_chunk4_pipe(PipeAttn4 P) {
         __syncthreads();
         const int cnt = min(kA4Tile, nmax4 - tb);
         const uint16_t* vc = vt + pc * HD + dcol;
-        for (int i = 0; i < cnt; i += 4) {
-            const v16f p = a4_products(pr[tb + i], hy_bitsf((uint32_t)vc[i * HD] << 16));
+        if (cnt == kA4Tile) {
+            // a whole tile: every operand read at once, each MFMA issued two steps ahead of its
+            // adds (a step's region may place its MFMA last: the next step does not wait on it)
+            constexpr int NQ = kA4Tile / 4;
+            float pa[NQ], va[NQ];
 #pragma unroll
-            for (int b = 0; b < 4; b++)
+            for (int q = 0; q < NQ; q++) {
+                pa[q] = pr[tb + 4 * q];
+                va[q] = hy_bitsf((uint32_t)vc[4 * q * HD] << 16);
+            }
+            v16f pp[NQ];
 #pragma unroll
-                for (int h = 0; h < GRP; h++) o[h] += p[4 * b + h];
+            for (int q = 0; q < NQ + 2; q++) {
+                if (q < NQ) pp[q] = a4_products(pa[q], va[q]);
+                if (q >= 2) {
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+#pragma unroll
+                        for (int h = 0; h < GRP; h++) o[h] += pp[q - 2][4 * b + h];
+                    asm volatile("" : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else {
+            for (int i = 0; i < cnt; i += 4) {
+                const v16f p = a4_products(pr[tb + i], hy_bitsf((uint32_t)vc[i * HD] << 16));
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+#pragma unroll
+                    for (int h = 0; h < GRP; h++) o[h] += p[4 * b + h];
+            }
         }
     }
     if (tl < ntv)
