@@ -281,8 +281,13 @@ def config4(b):
     log(f"config 4 model built in {time.time() - t:.1f} s")
     fm = lib.FusedModel(b, model)
     prompt, _ = synth.baseline_prompt(cfg)
-    fm.generate_device(prompt[:chunk + 5], 4, chunk=chunk)  # warm: kernels loaded, graphs captured
-    ids, st = fm.generate_device(prompt, n_gen, chunk=chunk)
+    # warm: kernels loaded, graphs captured, every KV-cache and activation page touched by a whole
+    # run; then three timed runs, the median run (by prefill time) reported
+    fm.generate_device(prompt, n_gen, chunk=chunk)
+    runs = [fm.generate_device(prompt, n_gen, chunk=chunk) for _ in range(3)]
+    if any(not np.array_equal(r[0], runs[0][0]) for r in runs):
+        raise RuntimeError("config 4: the timed runs' greedy ids differ")
+    ids, st = sorted(runs, key=lambda r: r[1].prefill_ms)[1]
     f = np.load(os.path.join(ROOT, "tests", "golden", "baseline_config4.npz"), allow_pickle=False)
     if not (np.array_equal(f["prompt"], prompt) and np.array_equal(ids[:len(f["greedy"])], f["greedy"])):
         raise RuntimeError("config 4: greedy ids differ from the reference's (tests/golden/baseline_config4.npz)")
@@ -321,6 +326,8 @@ def config4(b):
                 prefill_schedule=f"{chunk}-token chunks pipelined over the layers, up to {depth} in flight "
                                  f"(chunk i's layer l in the launches of chunk i + 1's layer l - 1; the same bits "
                                  f"as one chunk after another)",
+                timing="one whole warm-up run, then the median of three timed runs (by prefill time); HIP events "
+                       "on the backend stream",
                 prefill_tok_s=round(n_prompt / pre_s, 1), prefill_ms=round(st.prefill_ms, 3),
                 prefill_sequential_tok_s=round(n_prompt / (st_seq.prefill_ms / 1e3), 1),
                 prefill_int8_ops=int(ops), prefill_mfma_util=round(ops / pre_s / 1e12 / INT8_PEAK_TOPS, 4),

@@ -3,8 +3,6 @@
 // are exact in any order, and every fp32 reduction runs sequentially in the reference's order
 // in one lane, while the parallel work (loads, int8 dot products, exponentials, elementwise
 // ops) is spread over the wavefronts.
-#include <cstdlib>
-
 #include "hy_kernels.h"
 #include "hy_mv_parts.h"
 
@@ -948,10 +946,7 @@ struct PipeAttn4 {
 size_t attn4_lds_bytes(int sstride) { return (size_t)16 * sstride * sizeof(float) + (size_t)kA4Tile * 128 * sizeof(uint16_t); }
 constexpr size_t kA4MaxDynLds = 156 * 1024;  // of the CU's 160 KB, beside the kernel's static LDS
 
-static bool attn4_enabled() {
-    static const bool on = [] { const char* e = getenv("HYMT2_ATTN4"); return !(e && e[0] == '0'); }();
-    return on;
-}
+constexpr int kA4MinWorkgroups = 256;
 
 template <int HD>
 __global__ __launch_bounds__(kA4Threads) void k_attn_chunk4_pipe(PipeAttn4 P) {
@@ -1176,6 +1171,36 @@ __global__ __launch_bounds__(kA4Threads) void k_attn_chunk4_pipe(PipeAttn4 P) {
     }
 }
 
+// The four-token kernel for head dim 128 with four query heads a KV head, where every job's
+// positions are the host's and the rows fit in LDS; false where it does not apply.
+static bool launch_attn4(const PipeAttn& J, hipStream_t s, hipError_t& err) {
+    PipeAttn4 P;
+    P.J = J;
+    int groups = 0, nmax = 0;
+    for (int j = 0; j < J.njobs; j++) {
+        if (J.a[j].pos_dev) return false;
+        P.grp0[j] = groups;
+        groups += (J.a[j].nt + kA4Tok - 1) / kA4Tok;
+        nmax = std::max(nmax, J.a[j].pos0 + J.a[j].nt);
+    }
+    // at least a workgroup a CU: below that (one 128-token chunk at four KV heads: 128 groups) the
+    // per-token kernel's four times as many workgroups finish first (config-4 prefill one chunk
+    // after another: 46.2k against 39.7k tok/s; pipelined, with 256 and more: 99k against 90k)
+    if (groups * J.a[0].kv_heads < kA4MinWorkgroups) return false;
+    P.sstride = ((nmax + 31) & ~31) + 4;
+    const size_t lds = attn4_lds_bytes(P.sstride);
+    if (lds > kA4MaxDynLds) return false;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_chunk4_pipe<128>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kA4MaxDynLds);
+    if (attr != hipSuccess) {
+        err = attr;
+        return true;
+    }
+    k_attn_chunk4_pipe<128><<<dim3(J.a[0].kv_heads, groups), kA4Threads, lds, s>>>(P);
+    err = hipGetLastError();
+    return true;
+}
+
 bool attention_quantizes(const AttnArgs& a) {
     if (a.ctx > kAcMaxCtx || a.heads % a.kv_heads) return false;
     const int grp = a.heads / a.kv_heads;
@@ -1192,27 +1217,9 @@ hipError_t launch_attention(const PipeAttn& J, int rows, hipStream_t s) {
             return hipErrorNotSupported;
     }
     const int grp = a.heads / a.kv_heads;
-    if (a.hdim == 128 && grp == 4 && attn4_enabled()) {
-        // four tokens a workgroup where the positions are the host's and the rows fit in LDS
-        PipeAttn4 P;
-        P.J = J;
-        int groups = 0, nmax = 0;
-        bool host_pos = true;
-        for (int j = 0; j < J.njobs; j++) {
-            host_pos = host_pos && !J.a[j].pos_dev;
-            P.grp0[j] = groups;
-            groups += (J.a[j].nt + kA4Tok - 1) / kA4Tok;
-            nmax = std::max(nmax, J.a[j].pos0 + J.a[j].nt);
-        }
-        P.sstride = ((nmax + 31) & ~31) + 4;
-        const size_t lds = attn4_lds_bytes(P.sstride);
-        if (host_pos && lds <= kA4MaxDynLds) {
-            static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_chunk4_pipe<128>),
-                                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kA4MaxDynLds);
-            if (attr != hipSuccess) return attr;
-            k_attn_chunk4_pipe<128><<<dim3(a.kv_heads, groups), kA4Threads, lds, s>>>(P);
-            return hipGetLastError();
-        }
+    if (a.hdim == 128 && grp == 4) {
+        hipError_t e;
+        if (launch_attn4(J, s, e)) return e;
     }
     const dim3 grid(a.kv_heads, rows);
     if (a.hdim == 128 && grp == 4) k_attn_chunk_pipe<128, 4><<<grid, kAcThreads, 0, s>>>(J);
@@ -1225,6 +1232,13 @@ hipError_t launch_attention(const PipeAttn& J, int rows, hipStream_t s) {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     // causal chunk attention per (KV head, token) where it applies
     int grp = a.heads % a.kv_heads == 0 ? a.heads / a.kv_heads : 0;
+    if (a.ctx <= kAcMaxCtx && a.hdim == 128 && grp == 4) {
+        PipeAttn J{};
+        J.a[0] = a;
+        J.njobs = 1;
+        hipError_t e;
+        if (launch_attn4(J, s, e)) return e;
+    }
     if (a.ctx <= kAcMaxCtx) {
         const dim3 grid(a.kv_heads, a.nt);
         if (a.hdim == 128 && grp == 4) k_attn_chunk<128, 4><<<grid, kAcThreads, 0, s>>>(a);
