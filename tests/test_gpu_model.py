@@ -418,6 +418,29 @@ def test_chunk_attention_long_rows(backend, kv_heads):
         fm.close()
 
 
+def test_four_token_attention_one_chunk(backend):
+    """The four-token chunk attention (k_attn_chunk4_pipe) through the one-chunk launch: 8 KV
+    heads of 4 query heads at head dim 128, so a 128-token chunk is 32 groups x 8 KV heads = 256
+    workgroups, the least that takes that kernel (the 44-token last chunk, 88, takes the
+    per-token one). A 300-token prompt through fused_forward in chunks of 128, 128 and 44: the
+    last logits against the oracle's bit for bit; then the device loop's chunked prefill (its
+    pipelined launches, every step on the four-token kernel) and 8 greedy ids against the
+    oracle's."""
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=32, kv_heads=8, hdim=128, vocab=600, ctx=320)
+    model = synth.make_model(shape, mode="q2", seed=91)
+    prompt = synth.rand_prompt(synth.rng(92), 300, shape.vocab)
+    om = O.OracleModel(model, threads=8)
+    ref = _stepwise_logits(om, prompt)
+    want = O.OracleModel(model, threads=8).generate(prompt, 8, batch=16)
+    fm = lib.FusedModel(backend, model)
+    try:
+        assert np.array_equal(bits(fm.prefill(list(prompt), batch=128)), bits(ref))
+        ids, _ = fm.generate_device(prompt, 8, chunk=128)
+        assert np.array_equal(ids, want)
+    finally:
+        fm.close()
+
+
 def test_long_context_beyond_4096(backend):
     """Context 4400 (past the one-kernel form's 4096 and the chunk kernel's 2048): two layers, a
     4150-token prompt in 128-token chunks (the general chunk attention, rows up to 4150), the last
