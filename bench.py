@@ -466,7 +466,7 @@ def summarize_trace(d: str):
         for k, (c, s) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
             print(f"| `{k[:96]}` | {c} | {s:.1f} | {s / c:.2f} | {100 * s / ksum:.1f} |")
         att = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0 for r in main
-               if "k_attn_chunk_pipe" in r["Kernel_Name"]]
+               if "k_attn_chunk_pipe" in r["Kernel_Name"] or "k_attn_chunk4_pipe" in r["Kernel_Name"]]
         if att:
             print()
             print("Chunk attention per launch step (us): " + " ".join(f"{x:.0f}" for x in att))

@@ -1123,6 +1123,12 @@ int hymt2_hip_selftest_sqsum(void* impl, const float* x, int n, int m, float* ou
     return launch_selftest_sqsum(x, n, m, out, method, c->s) == hipSuccess ? 0 : -2;
 }
 
+int hymt2_hip_selftest_mfma(void* impl, const float* a, const float* b, float* out, int nw) {
+    Ctx* c = static_cast<Ctx*>(impl);
+    if (!c || !a || !b || !out || nw < 1) return -1;
+    return launch_selftest_mfma(a, b, out, nw, c->s) == hipSuccess ? 0 : -2;
+}
+
 int hymt2_hip_selftest_expf(void* impl, const float* src, float* dst, int n) {
     Ctx* c = static_cast<Ctx*>(impl);
     if (!c || n < 0) return -1;

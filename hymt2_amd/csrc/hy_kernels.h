@@ -290,5 +290,6 @@ hipError_t launch_argmax(const float* v, int n, unsigned long long* slots, hipSt
 hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_selftest(const void* src, float* dst, int n, int what, hipStream_t s);
 hipError_t launch_selftest_sqsum(const float* x, int n, int m, float* out, int method, hipStream_t s);
+hipError_t launch_selftest_mfma(const float* a, const float* b, float* out, int nw, hipStream_t s);
 
 }  // namespace hy

@@ -943,6 +943,22 @@ struct PipeAttn4 {
     int sstride;         // score row stride in LDS, floats (4 mod 32, past the longest row)
 };
 
+// One wavefront per 64 operand pairs: the 16 products a4_products returns in each lane, stored
+// out[w][r][lane] (the self-check of the zero-accumulator products and their layout)
+__global__ __launch_bounds__(64) void k_selftest_mfma(const float* a, const float* b, float* out, int nw) {
+    const int w = blockIdx.x, l = threadIdx.x;
+    if (w >= nw) return;  // uniform
+    const v16f p = a4_products(a[(size_t)w * 64 + l], b[(size_t)w * 64 + l]);
+#pragma unroll
+    for (int r = 0; r < 16; r++) out[((size_t)w * 16 + r) * 64 + l] = p[r];
+}
+
+hipError_t launch_selftest_mfma(const float* a, const float* b, float* out, int nw, hipStream_t s) {
+    if (nw < 1) return hipErrorInvalidValue;
+    k_selftest_mfma<<<nw, 64, 0, s>>>(a, b, out, nw);
+    return hipGetLastError();
+}
+
 size_t attn4_lds_bytes(int sstride) { return (size_t)16 * sstride * sizeof(float) + (size_t)kA4Tile * 128 * sizeof(uint16_t); }
 constexpr size_t kA4MaxDynLds = 156 * 1024;  // of the CU's 160 KB, beside the kernel's static LDS
 

@@ -62,6 +62,7 @@ def load():
         "hymt2_hip_selftest_f16": (i, [vp, vp, vp, i]),
         "hymt2_hip_selftest_expf": (i, [vp, vp, vp, i]),
         "hymt2_hip_selftest_sqsum": (i, [vp, vp, i, i, vp, i]),
+        "hymt2_hip_selftest_mfma": (i, [vp, vp, vp, vp, i]),
         "hymt2_hip_generate": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i, vp, C.POINTER(GenStats)]),
         "hymt2_hip_gen_begin": (i, [vp, C.POINTER(abi.FusedArgs), vp, i, vp, i, i]),
         "hymt2_hip_gen_steps": (i, [vp, i]),
@@ -86,7 +87,7 @@ def load():
 
 EXPORTS = ["hy_cuda_create", "hy_cuda_probe", "hymt2_hip_open", "hymt2_hip_ops", "hymt2_hip_last_error",
            "hymt2_hip_abi_layout", "hymt2_hip_stream", "hymt2_hip_quantize_q8k", "hymt2_hip_matvec",
-           "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_selftest_sqsum", "hymt2_hip_generate", "hymt2_hip_gen_begin",
+           "hymt2_hip_selftest_f16", "hymt2_hip_selftest_expf", "hymt2_hip_selftest_sqsum", "hymt2_hip_selftest_mfma", "hymt2_hip_generate", "hymt2_hip_gen_begin",
            "hymt2_hip_gen_steps", "hymt2_hip_gen_read", "hymt2_hip_head", "hymt2_hip_ffn_in",
            "hymt2_hip_gen_prefill", "hymt2_hip_generate_chunked", "hymt2_hip_matmul_static",
            "hymt2_hip_attn_split_from", "hymt2_hip_prefill_pipeline", "hymt2_hip_generate_ids"]

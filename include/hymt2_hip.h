@@ -153,6 +153,12 @@ HYMT2_HIP_API int hymt2_hip_selftest_expf(void *impl, const float *src_dev, floa
  * x0 + x1 + ... of n <= 4096 non-negative values by the 8-wavefront exact form of the decode
  * attention's softmax denominator (src/model.c:781-789). */
 HYMT2_HIP_API int hymt2_hip_selftest_sqsum(void *impl, const float *x_dev, int n, int m, float *out_dev, int method);
+/* The fp32 products of the four-token chunk attention's matrix-core form (no counterpart in the
+ * reference: it checks an instruction property the attention's bit-exactness rests on):
+ * v_mfma_f32_16x16x1f32 with a zero accumulator over nw wavefronts of 64 operand pairs
+ * a[w][lane], b[w][lane]; out[w][r][lane] = a[w][16 (r/4) + 4 (lane/16) + r%4] *
+ * b[w][16 (r/4) + lane%16], each the separately rounded fp32 product (a -0 product as +0). */
+HYMT2_HIP_API int hymt2_hip_selftest_mfma(void *impl, const float *a_dev, const float *b_dev, float *out_dev, int nw);
 
 /* Device-resident greedy generation (no host round trip per token). Each step runs one
  * position through the fused forward and the LM head; the argmax (first index on ties over

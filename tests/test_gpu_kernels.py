@@ -81,6 +81,67 @@ def test_expf_matches_libm(backend):
     assert np.array_equal(bits(out.cpu().numpy()), bits(O.expf(x)))
 
 
+def _mfma_operands(nw, g):
+    """nw wavefronts of 64 (a, b) fp32 pairs, six kinds by wavefront: attention scores (q x bf16
+    key), attention outputs (p in (0, 1] x bf16 value), random bit patterns over +-40 binades,
+    products in and near the denormal range, denormal inputs and signed zeros, products that
+    overflow."""
+    def bf16(x):
+        u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+    def pattern(shape, lo, hi):
+        s = g.integers(0, 2, shape, dtype=np.uint32) << 31
+        e = g.integers(lo, hi, shape, dtype=np.uint32) << 23
+        m = g.integers(0, 1 << 23, shape, dtype=np.uint32)
+        return (s | e | m).view(np.float32)
+
+    a = np.empty((nw, 64), np.float32)
+    b = np.empty((nw, 64), np.float32)
+    for k in range(6):
+        w = slice(k, nw, 6)
+        shape = a[w].shape
+        if k == 0:
+            a[w], b[w] = g.standard_normal(shape) * 3, bf16(g.standard_normal(shape))
+        elif k == 1:
+            a[w], b[w] = g.random(shape) ** 4, bf16(g.standard_normal(shape) * 0.1)
+        elif k == 2:
+            a[w], b[w] = pattern(shape, 127 - 40, 127 + 41), pattern(shape, 127 - 40, 127 + 41)
+        elif k == 3:
+            a[w], b[w] = pattern(shape, 1, 31), pattern(shape, 40, 110)
+        elif k == 4:
+            a[w] = np.where(g.random(shape) < 0.5, pattern(shape, 0, 1), np.where(g.random(shape) < 0.5, -0.0, 0.0))
+            b[w] = pattern(shape, 100, 160)
+        else:
+            a[w], b[w] = pattern(shape, 200, 220), pattern(shape, 170, 190)
+    return a, b
+
+
+def test_mfma_zero_accumulator_products(backend):
+    """The four-token chunk attention's products (a4_products: v_mfma_f32_16x16x1f32 with a zero
+    accumulator) against numpy's IEEE single products, bit for bit, placed by the layout the
+    kernel assumes: out[w][r][l] = a[w][16 (r / 4) + 4 (l / 16) + r % 4] * b[w][16 (r / 4) + l % 16].
+    A -0 product may come back as +0 (no sum that starts at +0 can tell them apart); no other
+    output may differ."""
+    import torch
+    nw = 3072
+    a, b = _mfma_operands(nw, np.random.default_rng(23))
+    out = torch.zeros(nw * 16 * 64, dtype=torch.float32, device="cuda:0")
+    sync()
+    ad, bd = dev(a), dev(b)
+    assert backend.L.hymt2_hip_selftest_mfma(backend.impl, ad.data_ptr(), bd.data_ptr(), out.data_ptr(), nw) == 0
+    sync()
+    got = bits(out.cpu().numpy().reshape(nw, 16, 64))
+    r, lane = np.arange(16)[:, None], np.arange(64)[None, :]
+    with np.errstate(over="ignore", under="ignore"):
+        want = bits(a[:, 16 * (r // 4) + 4 * (lane // 16) + r % 4] * b[:, 16 * (r // 4) + lane % 16])
+    diff = got != want
+    zero_sign = diff & (want == 0x80000000) & (got == 0)
+    assert not (diff & ~zero_sign).any(), f"{int((diff & ~zero_sign).sum())} products differ"
+    # the cases the operands were built for occur
+    assert (want & 0x7F800000 == 0).sum() > 10000 and (want & 0x7FFFFFFF == 0x7F800000).sum() > 1000
+
+
 def _sq_inputs(mode, m, n, g):
     x = g.standard_normal((m, n)).astype(np.float32)
     if mode == "small":
