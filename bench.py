@@ -588,6 +588,25 @@ def attn_traffic():
     b.close()
 
 
+def prefill_pass():
+    """The config-4 prompt's pipelined chunked prefill alone, twice (hymt2_hip_gen_prefill, no
+    decode step and so no graph replay): the launches the chunk kernels' counter passes read."""
+    from hymt2_amd import lib, synth
+    b = lib.Backend()
+    cfg = synth.CONFIG4
+    prompt, _ = synth.baseline_prompt(cfg)
+    model = synth.baseline_model(cfg, len(prompt) + 64)
+    fm = lib.FusedModel(b, model)
+    log(f"{len(prompt)}-token prompt: model uploaded")
+    for _ in range(2):
+        fm.gen_begin(prompt, len(prompt) + 8)
+        fm.gen_prefill(cfg["chunk"])
+        fm.gen_read(0, 1)
+        log("prefill done")
+    fm.close()
+    b.close()
+
+
 def summarize_pmc(fetch_dir: str, write_dir: str):
     """HBM bytes per dispatch of every kernel in two rocprofv3 --pmc runs (FETCH_SIZE, then
     WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for the calibration copy
@@ -790,6 +809,8 @@ def main():
     ap.add_argument("--attn-traffic", action="store_true",
                     help="only decode steps of the config-3 and config-4 models and the calibration copy (counter runs)")
     ap.add_argument("--layer-sets-only", action="store_true", help="only the configs 0-2 matvec legs (kernel trace)")
+    ap.add_argument("--prefill-pass", action="store_true",
+                    help="only the config-4 prompt's pipelined prefill, twice, no decode (counter runs)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print HBM bytes per dispatch from two rocprofv3 --pmc output directories and exit")
     ap.add_argument("--summarize-trace", metavar="DIR",
@@ -817,6 +838,9 @@ def main():
         return
     if args.attn_traffic:
         attn_traffic()
+        return
+    if args.prefill_pass:
+        prefill_pass()
         return
     if args.layer_sets_only:
         layer_sets_only()
