@@ -352,6 +352,7 @@ GEMM_SHAPES = [
     (abi.GT_Q2_0C, 1, 512),       # one row, one Q2_0C block (two panel pieces)
     (abi.GT_STQ1_0, 100, 1536),
     (abi.GT_Q2_0C, 8200, 2048),   # the large-contraction tiles at 128 tokens, ragged rows
+    (abi.GT_Q2_0C, 16390, 2048),  # 256 row tiles of 64 and 6 rows (64 x 32 tiles), ragged tokens
 ]
 
 
