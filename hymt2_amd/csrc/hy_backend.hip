@@ -462,11 +462,16 @@ static bool run_mv1(Ctx* c, const JobSpec* js, int njobs, bool pair, const MvOpt
     return true;
 }
 
-// Several tokens: panel weights go to the int8-MFMA GEMM once a chunk is larger than the
-// reference's batch; otherwise (and for Q4_K / Q6_K) the general matvec kernel runs over groups of
-// at most HY_MAX_BATCH tokens. Both give every token the single-token result.
+// Several tokens: panel weights go to the int8-MFMA GEMM from kGemmMinTokens + 1 tokens (the
+// reference host's 16-token batches among them); otherwise (and for Q4_K / Q6_K) the general
+// matvec kernel runs over groups of at most HY_MAX_BATCH tokens. Both give every token the
+// single-token result. The threshold as measured (a fused_forward of the config-3 model, matvec
+// against GEMM: 16 tokens 3.27 -> 1.95-2.01 ms, 8 tokens 2.34 -> 1.91-1.97, 4 tokens equal,
+// 2 tokens 1.71-1.78 against 1.87-1.92 ms)
+constexpr int kGemmMinTokens = 4;
+
 static bool run_multi(Ctx* c, const JobSpec* js, int njobs, bool pair, int nt, const MvOpts& o) {
-    if (nt > HY_MAX_BATCH && o.pro == PRO_NONE) {
+    if (nt > kGemmMinTokens && o.pro == PRO_NONE) {
         GemmLaunch G;
         memset(&G, 0, sizeof G);
         G.njobs = njobs;
