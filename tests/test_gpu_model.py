@@ -441,6 +441,31 @@ def test_four_token_attention_one_chunk(backend):
         fm.close()
 
 
+def test_four_token_attention_unaligned_long_rows(backend):
+    """The four-token chunk attention over long rows at unaligned positions: a 1000-token prompt
+    in chunks of 99 (ten full chunks and one of 10; every chunk after the first starts at a
+    position that is not a multiple of 4 and ends in a 3-token group), pipelined, rows up to 1000
+    positions. The 8 greedy ids, and the logits of a fused_forward of those ids at positions
+    1000-1007 (reading every layer's K/V of the prompt, which layer 0's attention output shapes
+    from layer 1 on), against the oracle's."""
+    shape = synth.ModelShape(n_layer=2, hidden=512, ffn=1024, heads=16, kv_heads=4, hdim=128, vocab=600, ctx=1040)
+    model = synth.make_model(shape, mode="stq", seed=95)
+    prompt = synth.rand_prompt(synth.rng(96), 1000, shape.vocab)
+    want = O.OracleModel(model, threads=16).generate(prompt, 8, batch=16)
+    om = O.OracleModel(model, threads=16)
+    for i in range(0, len(prompt), 16):
+        om.forward(prompt[i:i + 16], i, want_logits=False)
+    ref = om.forward(want, len(prompt), want_logits=True)
+    fm = lib.FusedModel(backend, model)
+    try:
+        ids, _ = fm.generate_device(prompt, 8, chunk=99)
+        assert np.array_equal(ids, want)
+        got = fm.forward(list(ids), len(prompt), True)
+        assert np.array_equal(bits(got), bits(ref))
+    finally:
+        fm.close()
+
+
 def test_long_context_beyond_4096(backend):
     """Context 4400 (past the one-kernel form's 4096 and the chunk kernel's 2048): two layers, a
     4150-token prompt in 128-token chunks (the general chunk attention, rows up to 4150), the last
