@@ -1206,11 +1206,15 @@ static bool launch_attn4(const PipeAttn& J, hipStream_t s, hipError_t& err) {
     P.sstride = ((nmax + 31) & ~31) + 4;
     const size_t lds = attn4_lds_bytes(P.sstride);
     if (lds > kA4MaxDynLds) return false;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_chunk4_pipe<128>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kA4MaxDynLds);
-    if (attr != hipSuccess) {
-        err = attr;
-        return true;
+    // the dynamic-LDS allowance, once per device (a repeat from another host thread is harmless)
+    static bool attr_set[64] = {};
+    int dev = 0;
+    if ((err = hipGetDevice(&dev)) != hipSuccess) return true;
+    if (dev < 0 || dev >= 64 || !attr_set[dev]) {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_chunk4_pipe<128>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kA4MaxDynLds);
+        if (err != hipSuccess) return true;
+        if (dev >= 0 && dev < 64) attr_set[dev] = true;
     }
     k_attn_chunk4_pipe<128><<<dim3(J.a[0].kv_heads, groups), kA4Threads, lds, s>>>(P);
     err = hipGetLastError();
