@@ -358,13 +358,14 @@ GEMM_SHAPES = [
 
 @pytest.mark.parametrize("gt,n,k", GEMM_SHAPES)
 def test_gemm_vs_oracle(backend, gt, n, k):
-    """Chunks above 16 tokens run panel weights on the int8-MFMA GEMM (k_gemm_panel): every
+    """Chunks of more than 4 tokens run panel weights on the int8-MFMA GEMM (k_gemm_panel): every
     token's row equals panel_rows_scalar (src/kernels.c:565-581) bit for bit, for token counts
-    that fill, straddle and undershoot the 64-token tiles. Each call runs three times: a result
-    that depends on wave timing shows up as a repeat that differs."""
+    that fill, straddle and undershoot the 16-, 32- and 64-token tiles (5 and 13: the reference
+    host's batches of up to 16). Each call runs three times: a result that depends on wave
+    timing shows up as a repeat that differs."""
     g = synth.rng(gt * 11 + n + k)
     w = synth.make_weight(g, gt, n, k)
-    for nt in (17, 64, 77, 128):
+    for nt in (5, 13, 17, 64, 77, 128):
         x = synth.activations(g, nt, k)
         out, xq = run_matvec(backend, w, x)
         assert np.array_equal(bits(out), bits(O.matvec(w, x, xq, nt))), f"nt={nt}"
